@@ -1,0 +1,117 @@
+/*
+ * spbitnet_amd.h -- C ABI of the MI355X (gfx950) sparse-ternary hot path.
+ *
+ * Plain pointers and sizes; no HIP or torch types.  Every pointer except the
+ * scalar arguments is caller-owned DEVICE memory; no entry point allocates
+ * or frees.  `stream` is a hipStream_t passed as void* (NULL = the null
+ * stream); launches are asynchronous on it, like the reference's wrappers.
+ *
+ * Return value: 0 on success, otherwise a hipError_t code (1 =
+ * hipErrorInvalidValue for rejected arguments); spb_last_error_string()
+ * then describes the failure.  Entry points never exit the process (the
+ * reference's CUDA_CHECK does, include/spbitnet/cuda_utils.h:13-21; the C++
+ * mirror in include/spbitnet/ restores that behaviour for drop-in callers).
+ * rows == 0 or cols == 0 (size == 0) is a successful no-op, as in the
+ * reference (src/kernels/sparse_ternary.cu:244, 261, 280).
+ *
+ * Weight layout (reference include/spbitnet/sparse_ternary_tensor.h:12-39):
+ *   meta   uint32 [rows][meta_row_stride],   meta_row_stride  >= ceil(cols/32)
+ *   values uint32 [rows][values_row_stride], values_row_stride >= ceil(cols/64)
+ * cols must be a multiple of 4.  Every 4-bit bitmap must have exactly two
+ * bits set (the format's invariant); results for malformed bitmaps are
+ * unspecified.
+ *
+ * 16-bit activations are passed as uint16_t bit patterns (IEEE fp16 for the
+ * _f16 entry points, bfloat16 for _bf16).
+ */
+#ifndef SPBITNET_AMD_H
+#define SPBITNET_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* spb_stream_t;
+
+/* Version of this ABI (major*100 + minor). */
+int spb_abi_version(void);
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* spb_last_error_string(void);
+
+/* Replaces spbitnet::sparse_ternary_unpack_gpu
+ * (reference include/spbitnet/sparse_ternary_kernels.h:16-19,
+ *  src/kernels/sparse_ternary.cu:240-254).
+ * out: int8 [rows][cols] row-major dense {-1,0,+1}. */
+int spb_sparse_ternary_unpack(const uint32_t* meta, const uint32_t* values, int8_t* out,
+                              int rows, int cols, int meta_row_stride,
+                              int values_row_stride, spb_stream_t stream);
+
+/* Replaces spbitnet::sparse_ternary_gemv_gpu
+ * (reference include/spbitnet/sparse_ternary_kernels.h:29-33,
+ *  src/kernels/sparse_ternary.cu:256-272).
+ * y[r] = sum_c W[r][c] * x[c] as exact int32; x int8 [cols], y int32 [rows]. */
+int spb_sparse_ternary_gemv(const uint32_t* meta, const uint32_t* values, const int8_t* x,
+                            int32_t* y, int rows, int cols, int meta_row_stride,
+                            int values_row_stride, spb_stream_t stream);
+
+/* Replaces spbitnet::fused_sparse_bitlinear_gpu
+ * (reference include/spbitnet/sparse_ternary_kernels.h:43-48,
+ *  src/kernels/sparse_ternary.cu:181-234, 274-291), fp16 in / fp16 out.
+ * q = clamp(rint(x * (absmax>0 ? 127/absmax : 0)), -128, 127) per element,
+ * acc = W q (int32), output[r] = fp16(float(acc) * ((gamma*absmax)/127)).
+ * d_absmax: device float written by spb_absmax_reduce_* on the same stream. */
+int spb_fused_sparse_bitlinear_f16(const uint32_t* meta, const uint32_t* values,
+                                   const uint16_t* x, uint16_t* output,
+                                   const float* d_absmax, float gamma, int rows, int cols,
+                                   int meta_row_stride, int values_row_stride,
+                                   spb_stream_t stream);
+
+/* Same as spb_fused_sparse_bitlinear_f16 with bfloat16 input and output
+ * (BitNet-2B-4T-shape decode stores activations in bf16). */
+int spb_fused_sparse_bitlinear_bf16(const uint32_t* meta, const uint32_t* values,
+                                    const uint16_t* x, uint16_t* output,
+                                    const float* d_absmax, float gamma, int rows, int cols,
+                                    int meta_row_stride, int values_row_stride,
+                                    spb_stream_t stream);
+
+/* Replaces spbitnet::absmax_reduce_gpu
+ * (reference include/spbitnet/inference_kernels.h:24-25,
+ *  src/kernels/inference_kernels.cu:120-148, 549-553): *d_absmax = max|x|. */
+int spb_absmax_reduce_f16(const uint16_t* input, float* d_absmax, int size,
+                          spb_stream_t stream);
+int spb_absmax_reduce_bf16(const uint16_t* input, float* d_absmax, int size,
+                           spb_stream_t stream);
+
+/* Replaces spbitnet::absmax_quantize_gpu
+ * (reference include/spbitnet/inference_kernels.h:19-20,
+ *  src/kernels/inference_kernels.cu:69-114, 543-547). */
+int spb_absmax_quantize_f16(const uint16_t* input, int8_t* output, float* d_absmax,
+                            int size, spb_stream_t stream);
+int spb_absmax_quantize_bf16(const uint16_t* input, int8_t* output, float* d_absmax,
+                             int size, spb_stream_t stream);
+
+/* Replaces spbitnet::dequantize_gpu
+ * (reference include/spbitnet/inference_kernels.h:29-30,
+ *  src/kernels/inference_kernels.cu:162-171, 555-561):
+ * output[i] = 16-bit(float(input[i]) * ((gamma * *d_absmax) / 127)). */
+int spb_dequantize_f16(const int32_t* input, uint16_t* output, const float* d_absmax,
+                       float gamma, int size, spb_stream_t stream);
+int spb_dequantize_bf16(const int32_t* input, uint16_t* output, const float* d_absmax,
+                        float gamma, int size, spb_stream_t stream);
+
+/* Which GEMV kernel a call with these arguments runs: 1 = the bit-plane
+ * kernel (cols % 128 == 0, cols <= 32768, 16-byte aligned meta rows, 8-byte
+ * aligned values rows), 0 = the general kernel.  Host-only query, no launch;
+ * no reference counterpart (the reference has a single kernel). */
+int spb_sparse_ternary_gemv_kernel_id(const uint32_t* meta, const uint32_t* values,
+                                      int rows, int cols, int meta_row_stride,
+                                      int values_row_stride);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPBITNET_AMD_H */

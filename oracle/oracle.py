@@ -1,0 +1,266 @@
+"""numpy-level access to the CPU checker (oracle/spb_oracle.c) and, when built,
+to the reference's own format code (oracle/_ref/libspb_ref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the spbitnet_amd package.  Each wrapper
+names the reference file:line its C function restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "_build", "libspb_oracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libspb_ref.so")
+
+_lib = None
+_ref = None
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+
+def build() -> None:
+    """Compile the checker (and the reference-header bridge where the
+    reference tree is present)."""
+    subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_SO):
+            build()
+        L = ctypes.CDLL(ORACLE_SO)
+        L.spbo_meta_stride.argtypes = [_I]
+        L.spbo_values_stride.argtypes = [_I]
+        L.spbo_mask_top2.argtypes = [_P, _I, _I, _P]
+        L.spbo_kept_sign.argtypes = [_P, _P, _I, _P]
+        L.spbo_absmean.argtypes = [_P, ctypes.c_size_t]
+        L.spbo_absmean.restype = ctypes.c_double
+        L.spbo_pack.argtypes = [_P, _P, _I, _I, _P, _P]
+        L.spbo_unpack.argtypes = [_P, _P, _I, _I, _I, _I, _P]
+        L.spbo_gemv.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I]
+        L.spbo_gemm.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I]
+        L.spbo_absmax.argtypes = [_P, _I]
+        L.spbo_absmax.restype = _F
+        L.spbo_quant_scale.argtypes = [_F]
+        L.spbo_quant_scale.restype = _F
+        L.spbo_round_clamp.argtypes = [_F]
+        L.spbo_quantize.argtypes = [_P, _I, _P]
+        L.spbo_quantize.restype = _F
+        L.spbo_dequant_scale.argtypes = [_F, _F]
+        L.spbo_dequant_scale.restype = _F
+        L.spbo_dequant.argtypes = [_P, _I, _F, _F, _P]
+        L.spbo_fused_bitlinear.argtypes = [_P, _P, _P, _F, _F, _I, _I, _I, _I, _P, _P]
+        L.spbo_bf16_round_array.argtypes = [_P, _I, _P]
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_SO)
+
+
+def ref():
+    """The reference's own SparseTernaryTensor code, via oracle/ref_bridge.cpp."""
+    global _ref
+    if _ref is None:
+        R = ctypes.CDLL(REF_SO)
+        R.ref_meta_stride.argtypes = [_I]
+        R.ref_values_stride.argtypes = [_I]
+        R.ref_pack_from_dense.argtypes = [_P, _P, _I, _I, _P, _P]
+        R.ref_pack_with_pruning.argtypes = [_P, _I, _I, _P, _P]
+        R.ref_unpack.argtypes = [_P, _P, _I, _I, _P]
+        R.ref_make_test_case.argtypes = [ctypes.c_uint, _I, _I, _I, _P, _P, _P]
+        R.ref_cpu_sparse_gemv.argtypes = [_P, _P, _P, _P, _I, _I]
+        _ref = R
+    return _ref
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def meta_stride(cols: int) -> int:
+    """sparse_ternary_tensor.h:254-257"""
+    return lib().spbo_meta_stride(cols)
+
+
+def values_stride(cols: int) -> int:
+    """sparse_ternary_tensor.h:261-264"""
+    return lib().spbo_values_stride(cols)
+
+
+def mask_top2(w: np.ndarray) -> np.ndarray:
+    """python/convert_model.py:88-119 (stable argsort: higher index wins ties)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    m = np.zeros((rows, cols), np.uint8)
+    lib().spbo_mask_top2(_p(w), rows, cols, _p(m))
+    return m
+
+
+def kept_sign(w: np.ndarray, mask: np.ndarray) -> np.ndarray:
+    """python/convert_model.py:270-283 (kept value = sign(w), w >= 0 -> +1)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    mask = np.ascontiguousarray(mask, dtype=np.uint8)
+    out = np.zeros(w.shape, np.int8)
+    lib().spbo_kept_sign(_p(w), _p(mask), w.size, _p(out))
+    return out
+
+
+def absmean(w: np.ndarray) -> float:
+    """python/convert_model.py:132 (in double; see spb_oracle.c)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    return lib().spbo_absmean(_p(w), w.size)
+
+
+def pack(w: np.ndarray, mask: np.ndarray):
+    """SparseTernaryTensor::pack_from_dense (sparse_ternary_tensor.h:58-108)."""
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    mask = np.ascontiguousarray(mask, dtype=np.uint8)
+    rows, cols = w.shape
+    meta = np.zeros((rows, meta_stride(cols)), np.uint32)
+    values = np.zeros((rows, values_stride(cols)), np.uint32)
+    rc = lib().spbo_pack(_p(w), _p(mask), rows, cols, _p(meta), _p(values))
+    if rc != 0:
+        raise ValueError(f"spbo_pack failed ({rc}): cols%4 or a group without exactly 2 kept")
+    return meta, values
+
+
+def unpack(meta: np.ndarray, values: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """SparseTernaryTensor::unpack_to_int8 (sparse_ternary_tensor.h:197-232)."""
+    meta = np.ascontiguousarray(meta, dtype=np.uint32)
+    values = np.ascontiguousarray(values, dtype=np.uint32)
+    out = np.zeros((rows, cols), np.int8)
+    lib().spbo_unpack(_p(meta), _p(values), rows, cols, meta.shape[-1], values.shape[-1], _p(out))
+    return out
+
+
+def gemv(meta, values, x, rows, cols) -> np.ndarray:
+    """cpu_sparse_gemv (tests/test_sparse_ternary.cu:17-33)."""
+    meta = np.ascontiguousarray(meta, dtype=np.uint32)
+    values = np.ascontiguousarray(values, dtype=np.uint32)
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    y = np.zeros(rows, np.int32)
+    lib().spbo_gemv(_p(meta), _p(values), _p(x), _p(y), rows, cols, meta.shape[-1], values.shape[-1])
+    return y
+
+
+def gemm(meta, values, X, rows, cols) -> np.ndarray:
+    """cpu_int8_gemm (tests/test_cusparselt.cu:16-28), token-major X[n][cols] -> Y[n][rows]."""
+    meta = np.ascontiguousarray(meta, dtype=np.uint32)
+    values = np.ascontiguousarray(values, dtype=np.uint32)
+    X = np.ascontiguousarray(X, dtype=np.int8)
+    n = X.shape[0]
+    Y = np.zeros((n, rows), np.int32)
+    lib().spbo_gemm(_p(meta), _p(values), _p(X), _p(Y), rows, cols, n, meta.shape[-1], values.shape[-1])
+    return Y
+
+
+def absmax(x: np.ndarray) -> float:
+    """absmax_reduce_kernel (src/kernels/inference_kernels.cu:120-148)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return float(np.float32(lib().spbo_absmax(_p(x), x.size)))
+
+
+def quantize(x: np.ndarray):
+    """absmax_quantize_kernel (src/kernels/inference_kernels.cu:69-114) -> (q, absmax)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.zeros(x.size, np.int8)
+    a = lib().spbo_quantize(_p(x), x.size, _p(q))
+    return q, float(np.float32(a))
+
+
+def dequant(acc: np.ndarray, gamma: float, absmax_: float) -> np.ndarray:
+    """dequantize_kernel (src/kernels/inference_kernels.cu:162-171), float32 before the final cast."""
+    acc = np.ascontiguousarray(acc, dtype=np.int32)
+    out = np.zeros(acc.size, np.float32)
+    lib().spbo_dequant(_p(acc), acc.size, float(gamma), float(absmax_), _p(out))
+    return out
+
+
+def fused_bitlinear(meta, values, x_f32, absmax_, gamma, rows, cols):
+    """fused_sparse_bitlinear_kernel (src/kernels/sparse_ternary.cu:181-234).
+    Returns (float32 output before the 16-bit cast, int32 accumulators)."""
+    meta = np.ascontiguousarray(meta, dtype=np.uint32)
+    values = np.ascontiguousarray(values, dtype=np.uint32)
+    x = np.ascontiguousarray(x_f32, dtype=np.float32)
+    out = np.zeros(rows, np.float32)
+    acc = np.zeros(rows, np.int32)
+    lib().spbo_fused_bitlinear(_p(meta), _p(values), _p(x), float(absmax_), float(gamma), rows, cols,
+                               meta.shape[-1], values.shape[-1], _p(out), _p(acc))
+    return out, acc
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns, round to nearest even."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size, np.uint16)
+    lib().spbo_bf16_round_array(_p(x), x.size, _p(out))
+    return out.reshape(x.shape)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, np.uint32) << 16).view(np.float32)
+
+
+def to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> fp16 bit patterns, round to nearest even (IEEE, as __float2half)."""
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+# ---- reference's own code (oracle/_ref), where built ------------------------
+
+def ref_pack_from_dense(w, mask):
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    mask = np.ascontiguousarray(mask, dtype=np.uint8)
+    rows, cols = w.shape
+    R = ref()
+    meta = np.zeros((rows, R.ref_meta_stride(cols)), np.uint32)
+    values = np.zeros((rows, R.ref_values_stride(cols)), np.uint32)
+    R.ref_pack_from_dense(_p(w), _p(mask), rows, cols, _p(meta), _p(values))
+    return meta, values
+
+
+def ref_pack_with_pruning(latent):
+    latent = np.ascontiguousarray(latent, dtype=np.float32)
+    rows, cols = latent.shape
+    R = ref()
+    meta = np.zeros((rows, R.ref_meta_stride(cols)), np.uint32)
+    values = np.zeros((rows, R.ref_values_stride(cols)), np.uint32)
+    R.ref_pack_with_pruning(_p(latent), rows, cols, _p(meta), _p(values))
+    return meta, values
+
+
+def ref_unpack(meta, values, rows, cols):
+    meta = np.ascontiguousarray(meta, dtype=np.uint32)
+    values = np.ascontiguousarray(values, dtype=np.uint32)
+    out = np.zeros((rows, cols), np.int8)
+    ref().ref_unpack(_p(meta), _p(values), rows, cols, _p(out))
+    return out
+
+
+def ref_cpu_sparse_gemv(meta, values, x, rows, cols):
+    """The reference's CPU GEMV: its own unpack_to_int8 + dense int32 MAC."""
+    meta = np.ascontiguousarray(meta, dtype=np.uint32)
+    values = np.ascontiguousarray(values, dtype=np.uint32)
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    y = np.zeros(rows, np.int32)
+    ref().ref_cpu_sparse_gemv(_p(meta), _p(values), _p(x), _p(y), rows, cols)
+    return y
+
+
+def ref_make_test_case(seed: int, rows: int, cols: int, want_x: bool):
+    w = np.zeros((rows, cols), np.int8)
+    mask = np.zeros((rows, cols), np.uint8)
+    x = np.zeros(cols, np.int8)
+    ref().ref_make_test_case(seed, rows, cols, int(want_x), _p(w), _p(mask), _p(x))
+    return w, mask, (x if want_x else None)

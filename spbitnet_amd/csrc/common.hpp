@@ -1,0 +1,95 @@
+// common.hpp -- shared device helpers and C-ABI error plumbing for the
+// gfx950 sparse-ternary library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+namespace spb {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// ---- error reporting (per host thread) -------------------------------------
+
+void set_error(const char* fmt, ...);
+void clear_error();
+const char* last_error();
+
+// Returns hipErrorInvalidValue after recording a message.
+int invalid(const char* fmt, ...);
+
+// Checks the launch status and records it.
+int launch_status(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+// ---- 16-bit float conversions (bit patterns in uint16_t) --------------------
+
+struct F16 {
+    static __device__ __forceinline__ float to_float(uint16_t b) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, b));
+    }
+    // IEEE round-to-nearest-even, as __float2half.
+    static __device__ __forceinline__ uint16_t from_float(float f) {
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+    }
+};
+
+struct BF16 {
+    static __device__ __forceinline__ float to_float(uint16_t b) {
+        return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
+    }
+    // Round to nearest even; NaN stays a quiet NaN.
+    static __device__ __forceinline__ uint16_t from_float(float f) {
+        uint32_t u = __builtin_bit_cast(uint32_t, f);
+        if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))
+            return static_cast<uint16_t>((u >> 16) | 0x40u);
+        u += 0x7FFFu + ((u >> 16) & 1u);
+        return static_cast<uint16_t>(u >> 16);
+    }
+};
+
+// ---- activation quantisation, shared by every kernel that quantises --------
+// scale = absmax > 0 ? 127/absmax : 0 (correctly rounded float32 divide), and
+// q = clamp(rint_ne(x * scale), -128, 127); NaN products give -128, which is
+// what clamping the INT_MIN that __float2int_rn returns for NaN produces
+// (reference src/kernels/sparse_ternary.cu:199, 214-217).
+__device__ __forceinline__ float quant_scale(float absmax) {
+    return absmax > 0.0f ? 127.0f / absmax : 0.0f;
+}
+
+__device__ __forceinline__ int quant_round_clamp(float v) {
+    float r = __builtin_rintf(v);
+    r = __builtin_fmaxf(r, -128.0f);  // maxnum: NaN -> -128
+    r = __builtin_fminf(r, 127.0f);
+    return static_cast<int>(r);
+}
+
+// (gamma * absmax) / 127, each step rounded to float32
+// (reference src/kernels/sparse_ternary.cu:231, inference_kernels.cu:169).
+__device__ __forceinline__ float dequant_scale(float gamma, float absmax) {
+    const float ga = gamma * absmax;
+    return ga / 127.0f;
+}
+
+// ---- wave64 reductions -------------------------------------------------------
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+}  // namespace spb

@@ -1,0 +1,130 @@
+"""Python mirror of the reference's kernel host API for the sparse-ternary
+path (include/spbitnet/sparse_ternary_kernels.h:16-48 and
+include/spbitnet/inference_kernels.h:19-30 of the reference): same names,
+same argument order and meaning, device tensors in place of raw pointers.
+
+Each call checks on the host that every tensor is on the GPU, has the dtype
+the kernel expects, is contiguous and is at least as large as the shape
+arguments require, then launches through the C ABI on the given stream
+(default: torch's current stream).  Failures raise SpbError; rows == 0 or
+cols == 0 is a no-op, as in the reference.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_HALF_KIND = {torch.float16: "f16", torch.bfloat16: "bf16"}
+
+
+def _stream_ptr(stream) -> Optional[int]:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    if isinstance(stream, int):
+        return stream or None
+    return stream.cuda_stream or None
+
+
+def _dev(t: torch.Tensor, name: str, dtype, min_numel: int) -> int:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if t.dtype not in (dtype if isinstance(dtype, tuple) else (dtype,)):
+        raise TypeError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() < min_numel:
+        raise ValueError(f"{name} holds {t.numel()} elements, needs at least {min_numel}")
+    return t.data_ptr()
+
+
+def _weights(meta, values, rows, cols, meta_row_stride, values_row_stride):
+    if rows < 0 or cols < 0:
+        raise ValueError(f"negative shape ({rows}, {cols})")
+    if cols % 4:
+        raise ValueError(f"cols={cols} is not a multiple of 4")
+    if meta_row_stride < (cols // 4 + 7) // 8 or values_row_stride < (cols // 4 + 15) // 16:
+        raise ValueError("row strides are smaller than the format requires")
+    need_m = rows * meta_row_stride if rows and cols else 0
+    need_v = rows * values_row_stride if rows and cols else 0
+    pm = _dev(meta, "meta", (torch.int32, torch.uint32), need_m)
+    pv = _dev(values, "values", (torch.int32, torch.uint32), need_v)
+    return pm, pv
+
+
+def sparse_ternary_unpack_gpu(meta, values, out, rows, cols, meta_row_stride,
+                              values_row_stride, stream=None):
+    """reference src/kernels/sparse_ternary.cu:240-254"""
+    pm, pv = _weights(meta, values, rows, cols, meta_row_stride, values_row_stride)
+    po = _dev(out, "out", torch.int8, rows * cols)
+    _lib.check(_lib.load().spb_sparse_ternary_unpack(pm, pv, po, rows, cols, meta_row_stride,
+                                                     values_row_stride, _stream_ptr(stream)),
+               "sparse_ternary_unpack_gpu")
+
+
+def sparse_ternary_gemv_gpu(meta, values, x, y, rows, cols, meta_row_stride,
+                            values_row_stride, stream=None):
+    """reference src/kernels/sparse_ternary.cu:256-272 (int8 x -> int32 y)"""
+    pm, pv = _weights(meta, values, rows, cols, meta_row_stride, values_row_stride)
+    px = _dev(x, "x", torch.int8, cols)
+    py = _dev(y, "y", torch.int32, rows)
+    _lib.check(_lib.load().spb_sparse_ternary_gemv(pm, pv, px, py, rows, cols, meta_row_stride,
+                                                   values_row_stride, _stream_ptr(stream)),
+               "sparse_ternary_gemv_gpu")
+
+
+def fused_sparse_bitlinear_gpu(meta, values, x, output, d_absmax, gamma, rows, cols,
+                               meta_row_stride, values_row_stride, stream=None):
+    """reference src/kernels/sparse_ternary.cu:274-291; x/output fp16 or bf16."""
+    pm, pv = _weights(meta, values, rows, cols, meta_row_stride, values_row_stride)
+    if x.dtype not in _HALF_KIND:
+        raise TypeError("x must be float16 or bfloat16")
+    kind = _HALF_KIND[x.dtype]
+    px = _dev(x, "x", x.dtype, cols)
+    po = _dev(output, "output", x.dtype, rows)
+    pa = _dev(d_absmax, "d_absmax", torch.float32, 1)
+    fn = getattr(_lib.load(), f"spb_fused_sparse_bitlinear_{kind}")
+    _lib.check(fn(pm, pv, px, po, pa, float(gamma), rows, cols, meta_row_stride,
+                  values_row_stride, _stream_ptr(stream)), "fused_sparse_bitlinear_gpu")
+
+
+def absmax_reduce_gpu(input, d_absmax, size, stream=None):
+    """reference src/kernels/inference_kernels.cu:549-553"""
+    if input.dtype not in _HALF_KIND:
+        raise TypeError("input must be float16 or bfloat16")
+    pi = _dev(input, "input", input.dtype, size)
+    pa = _dev(d_absmax, "d_absmax", torch.float32, 1)
+    fn = getattr(_lib.load(), f"spb_absmax_reduce_{_HALF_KIND[input.dtype]}")
+    _lib.check(fn(pi, pa, size, _stream_ptr(stream)), "absmax_reduce_gpu")
+
+
+def absmax_quantize_gpu(input, output, d_absmax, size, stream=None):
+    """reference src/kernels/inference_kernels.cu:543-547"""
+    if input.dtype not in _HALF_KIND:
+        raise TypeError("input must be float16 or bfloat16")
+    pi = _dev(input, "input", input.dtype, size)
+    po = _dev(output, "output", torch.int8, size)
+    pa = _dev(d_absmax, "d_absmax", torch.float32, 1)
+    fn = getattr(_lib.load(), f"spb_absmax_quantize_{_HALF_KIND[input.dtype]}")
+    _lib.check(fn(pi, po, pa, size, _stream_ptr(stream)), "absmax_quantize_gpu")
+
+
+def dequantize_gpu(input, output, d_absmax, gamma, size, stream=None):
+    """reference src/kernels/inference_kernels.cu:555-561; output fp16 or bf16."""
+    if output.dtype not in _HALF_KIND:
+        raise TypeError("output must be float16 or bfloat16")
+    pi = _dev(input, "input", torch.int32, size)
+    po = _dev(output, "output", output.dtype, size)
+    pa = _dev(d_absmax, "d_absmax", torch.float32, 1)
+    fn = getattr(_lib.load(), f"spb_dequantize_{_HALF_KIND[output.dtype]}")
+    _lib.check(fn(pi, po, pa, float(gamma), size, _stream_ptr(stream)), "dequantize_gpu")
+
+
+def gemv_kernel_id(meta, values, rows, cols, meta_row_stride, values_row_stride) -> int:
+    """1 if the bit-plane GEMV kernel would run for these arguments, else 0."""
+    return _lib.load().spb_sparse_ternary_gemv_kernel_id(
+        meta.data_ptr(), values.data_ptr(), rows, cols, meta_row_stride, values_row_stride)
