@@ -102,9 +102,52 @@ int spb_dequantize_f16(const int32_t* input, uint16_t* output, const float* d_ab
 int spb_dequantize_bf16(const int32_t* input, uint16_t* output, const float* d_absmax,
                         float gamma, int size, spb_stream_t stream);
 
+/* ---- Bit-plane activation layout -------------------------------------------
+ * No reference counterpart: an activation layout of this build.  An int8
+ * vector of `cols` columns is stored as 8 * ceil(cols/32) uint32 words;
+ * word [w*8 + b] holds bit b (two's complement) of columns 32w .. 32w+31,
+ * column 32w+j at bit j; columns beyond `cols` are 0.  Same size as the
+ * int8 vector.  The GEMV kernel consumes activations in this form; producing
+ * it once per activation vector, instead of in every GEMV workgroup, is what
+ * these entry points are for.  Buffers must be 16-byte aligned. */
+
+/* int8 x [cols] -> planes.  cols % 8 == 0; x 8-byte aligned. */
+int spb_activation_planes(const int8_t* x, uint32_t* planes, int cols, spb_stream_t stream);
+
+/* absmax_quantize (as spb_absmax_quantize_*) writing the plane layout, the
+ * absmax, and, when `output` is non-NULL, the int8 vector as well.
+ * size % 8 == 0; input 16-byte aligned. */
+int spb_absmax_quantize_planes_f16(const uint16_t* input, uint32_t* planes, int8_t* output,
+                                   float* d_absmax, int size, spb_stream_t stream);
+int spb_absmax_quantize_planes_bf16(const uint16_t* input, uint32_t* planes, int8_t* output,
+                                    float* d_absmax, int size, spb_stream_t stream);
+
+/* spb_sparse_ternary_gemv with the activations given as planes; results are
+ * identical to the int8 entry point on the same activations. */
+int spb_sparse_ternary_gemv_planes(const uint32_t* meta, const uint32_t* values,
+                                   const uint32_t* planes, int32_t* y, int rows, int cols,
+                                   int meta_row_stride, int values_row_stride,
+                                   spb_stream_t stream);
+
+/* BitLinear on already-quantised plane activations: the GEMV followed by the
+ * reference's dequant epilogue, output[r] = 16-bit(float(acc) * ((gamma *
+ * *d_absmax) / 127)); identical to spb_fused_sparse_bitlinear_* when the
+ * planes come from spb_absmax_quantize_planes_* of the same input. */
+int spb_fused_sparse_bitlinear_planes_f16(const uint32_t* meta, const uint32_t* values,
+                                          const uint32_t* planes, uint16_t* output,
+                                          const float* d_absmax, float gamma, int rows,
+                                          int cols, int meta_row_stride, int values_row_stride,
+                                          spb_stream_t stream);
+int spb_fused_sparse_bitlinear_planes_bf16(const uint32_t* meta, const uint32_t* values,
+                                           const uint32_t* planes, uint16_t* output,
+                                           const float* d_absmax, float gamma, int rows,
+                                           int cols, int meta_row_stride, int values_row_stride,
+                                           spb_stream_t stream);
+
 /* Which GEMV kernel a call with these arguments runs: 1 = the bit-plane
  * kernel (cols % 128 == 0, cols <= 32768, 16-byte aligned meta rows, 8-byte
- * aligned values rows), 0 = the general kernel.  Host-only query, no launch;
+ * aligned values rows; the int8 / fp16 / bf16 activation pointer must also be
+ * 16-byte aligned), 0 = the general kernel.  Host-only query, no launch;
  * no reference counterpart (the reference has a single kernel). */
 int spb_sparse_ternary_gemv_kernel_id(const uint32_t* meta, const uint32_t* values,
                                       int rows, int cols, int meta_row_stride,

@@ -59,6 +59,7 @@ def lib():
         L.spbo_dequant.argtypes = [_P, _I, _F, _F, _P]
         L.spbo_fused_bitlinear.argtypes = [_P, _P, _P, _F, _F, _I, _I, _I, _I, _P, _P]
         L.spbo_bf16_round_array.argtypes = [_P, _I, _P]
+        L.spbo_planes.argtypes = [_P, _I, _P]
         _lib = L
     return _lib
 
@@ -198,6 +199,14 @@ def fused_bitlinear(meta, values, x_f32, absmax_, gamma, rows, cols):
     lib().spbo_fused_bitlinear(_p(meta), _p(values), _p(x), float(absmax_), float(gamma), rows, cols,
                                meta.shape[-1], values.shape[-1], _p(out), _p(acc))
     return out, acc
+
+
+def planes(x: np.ndarray) -> np.ndarray:
+    """Bit-plane activation layout: word [w*8+b] bit j = bit b of x[32w+j]."""
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    out = np.zeros(8 * ((x.size + 31) // 32), np.uint32)
+    lib().spbo_planes(_p(x), x.size, _p(out))
+    return out
 
 
 def to_bf16_bits(x: np.ndarray) -> np.ndarray:

@@ -264,3 +264,19 @@ uint16_t spbo_bf16_round(float f) {
 void spbo_bf16_round_array(const float* in, int n, uint16_t* out) {
     for (int i = 0; i < n; ++i) out[i] = spbo_bf16_round(in[i]);
 }
+
+/*
+ * Bit-plane activation layout of this build (no reference counterpart):
+ * word [w*8 + b] bit j = bit b of the two's-complement byte x[32w + j];
+ * columns beyond cols are 0.  Pinned by a round trip (planes -> bytes) and
+ * by the GEMV identity sum_j w_j x_j = sum_b c_b sum_j w_j bit_b(x_j).
+ */
+void spbo_planes(const int8_t* x, int cols, uint32_t* planes) {
+    int nw = (cols + 31) / 32;
+    memset(planes, 0, (size_t)nw * 8 * 4);
+    for (int c = 0; c < cols; ++c) {
+        uint32_t byte = (uint8_t)x[c];
+        for (int b = 0; b < 8; ++b)
+            planes[(c / 32) * 8 + b] |= ((byte >> b) & 1u) << (c % 32);
+    }
+}

@@ -33,6 +33,12 @@ SIGNATURES = {
     "spb_dequantize_f16": [_P, _P, _P, _F, _I, _P],
     "spb_dequantize_bf16": [_P, _P, _P, _F, _I, _P],
     "spb_sparse_ternary_gemv_kernel_id": [_P, _P, _I, _I, _I, _I],
+    "spb_activation_planes": [_P, _P, _I, _P],
+    "spb_absmax_quantize_planes_f16": [_P, _P, _P, _P, _I, _P],
+    "spb_absmax_quantize_planes_bf16": [_P, _P, _P, _P, _I, _P],
+    "spb_sparse_ternary_gemv_planes": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "spb_fused_sparse_bitlinear_planes_f16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
+    "spb_fused_sparse_bitlinear_planes_bf16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
 }
 _RESTYPES = {"spb_last_error_string": ctypes.c_char_p}
 

@@ -21,6 +21,9 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
+    # Every float32 step rounds on its own, as in the reference: no mul+add
+    # contraction and no fused multiply-and-narrow (v_fma_mix*) conversions.
+    "-ffp-contract=off",
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

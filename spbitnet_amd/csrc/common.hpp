@@ -35,8 +35,12 @@ struct F16 {
     static __device__ __forceinline__ float to_float(uint16_t b) {
         return static_cast<float>(__builtin_bit_cast(_Float16, b));
     }
-    // IEEE round-to-nearest-even, as __float2half.
+    // IEEE round-to-nearest-even of a float32 value, as __float2half.  The
+    // empty asm keeps f an already-rounded float32: without it the backend
+    // folds a preceding float multiply into v_fma_mixlo_f16, which rounds the
+    // exact product once to fp16 instead of rounding to fp32 and then fp16.
     static __device__ __forceinline__ uint16_t from_float(float f) {
+        asm("" : "+v"(f));
         return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
     }
 };
@@ -90,6 +94,24 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, kWave));
     return v;
+}
+
+// max |x| over x[0..n) for a block of kRedBlock threads; every thread gets
+// the result.  Exact and order-independent (a max of absolute values).
+constexpr int kRedBlock = 1024;
+
+template <class T>
+__device__ __forceinline__ float block_absmax(const uint16_t* __restrict__ x, int n) {
+    __shared__ float part[kRedBlock / kWave];
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kRedBlock) m = __builtin_fmaxf(m, __builtin_fabsf(T::to_float(x[i])));
+    m = wave_max(m);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (lane == 0) part[wave] = m;
+    __syncthreads();
+    float r = lane < kRedBlock / kWave ? part[lane] : 0.0f;
+    r = wave_max(r);
+    return r;  // every thread holds the block result
 }
 
 }  // namespace spb

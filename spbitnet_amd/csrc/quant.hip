@@ -11,22 +11,6 @@
 namespace spb {
 namespace {
 
-constexpr int kRedBlock = 1024;
-
-template <class T>
-__device__ float block_absmax(const uint16_t* __restrict__ x, int n) {
-    __shared__ float part[kRedBlock / kWave];
-    float m = 0.0f;
-    for (int i = threadIdx.x; i < n; i += kRedBlock) m = __builtin_fmaxf(m, __builtin_fabsf(T::to_float(x[i])));
-    m = wave_max(m);
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    if (lane == 0) part[wave] = m;
-    __syncthreads();
-    float r = lane < kRedBlock / kWave ? part[lane] : 0.0f;
-    r = wave_max(r);
-    return r;  // every thread holds the block result
-}
-
 template <class T>
 __global__ __launch_bounds__(kRedBlock) void absmax_reduce_kernel(const uint16_t* __restrict__ x,
                                                                   float* __restrict__ d_absmax,

@@ -70,8 +70,9 @@ def sparse_ternary_gemv_gpu(meta, values, x, y, rows, cols, meta_row_stride,
                             values_row_stride, stream=None):
     """reference src/kernels/sparse_ternary.cu:256-272 (int8 x -> int32 y)"""
     pm, pv = _weights(meta, values, rows, cols, meta_row_stride, values_row_stride)
-    px = _dev(x, "x", torch.int8, cols)
-    py = _dev(y, "y", torch.int32, rows)
+    empty = rows == 0 or cols == 0
+    px = _dev(x, "x", torch.int8, 0 if empty else cols)
+    py = _dev(y, "y", torch.int32, 0 if empty else rows)
     _lib.check(_lib.load().spb_sparse_ternary_gemv(pm, pv, px, py, rows, cols, meta_row_stride,
                                                    values_row_stride, _stream_ptr(stream)),
                "sparse_ternary_gemv_gpu")
@@ -84,8 +85,9 @@ def fused_sparse_bitlinear_gpu(meta, values, x, output, d_absmax, gamma, rows, c
     if x.dtype not in _HALF_KIND:
         raise TypeError("x must be float16 or bfloat16")
     kind = _HALF_KIND[x.dtype]
-    px = _dev(x, "x", x.dtype, cols)
-    po = _dev(output, "output", x.dtype, rows)
+    empty = rows == 0 or cols == 0
+    px = _dev(x, "x", x.dtype, 0 if empty else cols)
+    po = _dev(output, "output", x.dtype, 0 if empty else rows)
     pa = _dev(d_absmax, "d_absmax", torch.float32, 1)
     fn = getattr(_lib.load(), f"spb_fused_sparse_bitlinear_{kind}")
     _lib.check(fn(pm, pv, px, po, pa, float(gamma), rows, cols, meta_row_stride,
@@ -122,6 +124,61 @@ def dequantize_gpu(input, output, d_absmax, gamma, size, stream=None):
     pa = _dev(d_absmax, "d_absmax", torch.float32, 1)
     fn = getattr(_lib.load(), f"spb_dequantize_{_HALF_KIND[output.dtype]}")
     _lib.check(fn(pi, po, pa, float(gamma), size, _stream_ptr(stream)), "dequantize_gpu")
+
+
+# ---- bit-plane activation layout (no reference counterpart) -----------------
+
+def planes_words(cols: int) -> int:
+    """uint32 words of the plane layout of a `cols`-column activation."""
+    return 8 * ((cols + 31) // 32)
+
+
+def activation_planes_gpu(x, planes, cols, stream=None):
+    """int8 x[cols] -> bit-plane layout (word [w*8+b] = plane b of columns 32w..32w+31)."""
+    px = _dev(x, "x", torch.int8, cols)
+    pp = _dev(planes, "planes", (torch.int32, torch.uint32), planes_words(cols))
+    _lib.check(_lib.load().spb_activation_planes(px, pp, cols, _stream_ptr(stream)),
+               "activation_planes_gpu")
+
+
+def absmax_quantize_planes_gpu(input, planes, d_absmax, size, output=None, stream=None):
+    """absmax + int8 quantisation emitting the plane layout (and the int8 vector if given)."""
+    if input.dtype not in _HALF_KIND:
+        raise TypeError("input must be float16 or bfloat16")
+    pi = _dev(input, "input", input.dtype, size)
+    pp = _dev(planes, "planes", (torch.int32, torch.uint32), planes_words(size))
+    pa = _dev(d_absmax, "d_absmax", torch.float32, 1)
+    po = _dev(output, "output", torch.int8, size) if output is not None else None
+    fn = getattr(_lib.load(), f"spb_absmax_quantize_planes_{_HALF_KIND[input.dtype]}")
+    _lib.check(fn(pi, pp, po, pa, size, _stream_ptr(stream)), "absmax_quantize_planes_gpu")
+
+
+def sparse_ternary_gemv_planes_gpu(meta, values, planes, y, rows, cols, meta_row_stride,
+                                   values_row_stride, stream=None):
+    """sparse_ternary_gemv_gpu with plane-layout activations."""
+    pm, pv = _weights(meta, values, rows, cols, meta_row_stride, values_row_stride)
+    empty = rows == 0 or cols == 0
+    pp = _dev(planes, "planes", (torch.int32, torch.uint32), 0 if empty else planes_words(cols))
+    py = _dev(y, "y", torch.int32, 0 if empty else rows)
+    _lib.check(_lib.load().spb_sparse_ternary_gemv_planes(pm, pv, pp, py, rows, cols,
+                                                          meta_row_stride, values_row_stride,
+                                                          _stream_ptr(stream)),
+               "sparse_ternary_gemv_planes_gpu")
+
+
+def fused_sparse_bitlinear_planes_gpu(meta, values, planes, output, d_absmax, gamma, rows, cols,
+                                      meta_row_stride, values_row_stride, stream=None):
+    """GEMV on plane activations + the reference's dequant epilogue; output fp16 or bf16."""
+    pm, pv = _weights(meta, values, rows, cols, meta_row_stride, values_row_stride)
+    if output.dtype not in _HALF_KIND:
+        raise TypeError("output must be float16 or bfloat16")
+    empty = rows == 0 or cols == 0
+    pp = _dev(planes, "planes", (torch.int32, torch.uint32), 0 if empty else planes_words(cols))
+    po = _dev(output, "output", output.dtype, 0 if empty else rows)
+    pa = _dev(d_absmax, "d_absmax", torch.float32, 1)
+    fn = getattr(_lib.load(), f"spb_fused_sparse_bitlinear_planes_{_HALF_KIND[output.dtype]}")
+    _lib.check(fn(pm, pv, pp, po, pa, float(gamma), rows, cols, meta_row_stride,
+                  values_row_stride, _stream_ptr(stream)), "fused_sparse_bitlinear_planes_gpu")
 
 
 def gemv_kernel_id(meta, values, rows, cols, meta_row_stride, values_row_stride) -> int:

@@ -232,16 +232,38 @@ def test_quantize_all_zero(gpu, kind):
     assert d_a.item() == 0.0 and (q.cpu().numpy() == 0).all()
 
 
+def double_rounding_cases(gamma, absmax, kind):
+    """Accumulators whose dequantised value rounds differently when the
+    float32 product is narrowed (the reference's order) than when the exact
+    product is rounded once: an implementation that fuses the multiply into
+    the narrowing conversion fails on exactly these."""
+    acc = np.arange(-442368, 442369, dtype=np.int64)
+    s = np.float32(np.float32(gamma) * np.float32(absmax)) / np.float32(127.0)
+    exact = acc.astype(np.float64) * np.float64(s)
+    via32 = exact.astype(np.float32)
+    if kind == "f16":
+        diff = via32.astype(np.float16) != exact.astype(np.float16)
+    else:
+        import torch as T
+        diff = (T.from_numpy(via32).to(T.bfloat16).float().numpy()
+                != T.from_numpy(exact).to(T.bfloat16).float().numpy())
+    return acc[diff].astype(np.int32)
+
+
 @pytest.mark.parametrize("kind", ["f16", "bf16"])
 def test_dequantize(gpu, kind):
-    n = 6912
-    acc = np.random.default_rng(3).integers(-442368, 442369, n).astype(np.int32)
-    acc[:4] = [0, 1, -1, 442368]
-    d_a = torch.tensor([5.25], dtype=torch.float32, device=gpu)
+    gamma, absmax = 0.8123, 3.37
+    tricky = double_rounding_cases(gamma, absmax, kind)
+    if kind == "f16":
+        assert tricky.size > 10  # the check below has teeth
+    rnd = np.random.default_rng(3).integers(-442368, 442369, 6912).astype(np.int32)
+    acc = np.concatenate([np.array([0, 1, -1, 442368, -442368], np.int32), tricky, rnd])
+    n = acc.size
+    d_a = torch.tensor([absmax], dtype=torch.float32, device=gpu)
     out = torch.zeros(n, dtype=HALF[kind], device=gpu)
-    K.dequantize_gpu(dev(acc, gpu), out, d_a, 0.0123, n)
+    K.dequantize_gpu(dev(acc, gpu), out, d_a, gamma, n)
     torch.cuda.synchronize()
-    assert (half_bits(out) == oracle_half_bits(O.dequant(acc, 0.0123, 5.25), kind)).all()
+    assert (half_bits(out) == oracle_half_bits(O.dequant(acc, gamma, absmax), kind)).all()
 
 
 @pytest.mark.parametrize("kind", ["f16", "bf16"])

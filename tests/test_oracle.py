@@ -264,3 +264,25 @@ def test_bf16_rounding_matches_torch():
     assert (ours == ref).all()
     nan = O.to_bf16_bits(np.array([np.nan], np.float32))[0]
     assert (nan & 0x7F80) == 0x7F80 and (nan & 0x7F) != 0
+
+
+# ---- bit-plane activation layout (this build's own format) -------------------
+
+def test_planes_round_trip_and_identity():
+    rng = np.random.default_rng(15)
+    for cols in [8, 40, 64, 2560, 6912]:
+        x = rng.integers(-128, 128, cols).astype(np.int8)
+        p = O.planes(x)
+        assert p.size == 8 * ((cols + 31) // 32)
+        words = p.reshape(-1, 8)
+        back = np.zeros(cols, np.int64)
+        for c in range(cols):
+            v = sum(((int(words[c // 32, b]) >> (c % 32)) & 1) << b for b in range(8))
+            back[c] = v - 256 if v >= 128 else v
+        assert (back == x).all()
+    # sum_j w_j x_j = sum_b c_b sum_j w_j bit_b(x_j), c_7 = -128
+    dense, meta, values = _random_packed(8, 64, 16)
+    x = rng.integers(-128, 128, 64).astype(np.int8)
+    bits = ((x.astype(np.int64)[None, :] & 0xFF) >> np.arange(8)[:, None]) & 1
+    c = np.array([1, 2, 4, 8, 16, 32, 64, -128])
+    assert (dense.astype(np.int64) @ (c @ bits) == O.gemv(meta, values, x, 8, 64)).all()
