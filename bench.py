@@ -44,6 +44,20 @@ def gemv_bytes(rows: int, cols: int) -> int:
     return rows * cols // 8 + rows * cols // 16 + cols + 4 * rows
 
 
+def read_traffic():
+    """HBM bytes per launch of the streamed GEMV, from the committed rocprofv3
+    PMC summary (FETCH_SIZE and WRITE_SIZE runs, scaled by a copy of known
+    size); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_bitplane_streamed_config1.pmc.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return {"bytes_per_launch": int(d["traffic_bytes_per_launch_avg"]),
+                "source": os.path.relpath(path, ROOT)}
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -54,7 +68,20 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 256 MiB once (known bytes, for scaling rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
+
+    if args.copy_calibration:
+        import torch
+        a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        print("copied 268435456 bytes", flush=True)
+        return 0
 
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the reference is "
@@ -308,6 +335,10 @@ def main() -> int:
         "cpu_baseline": cpu,
         "detail": detail,
     }
+    traffic = read_traffic()
+    if traffic is not None:
+        out["roofline"]["traffic"] = traffic["bytes_per_launch"]
+        out["roofline"]["traffic_source"] = traffic["source"]
     print(json.dumps(out), flush=True)
     return 0
 

@@ -330,14 +330,14 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(Weights wt, Act a
     const int ro = tid / C;
     const bool active = ro < RS;
 
-    const long my_tiles = (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x;
-    const long nitems = my_tiles * tile_steps;
-    auto row_of = [&](long i) -> long {
-        const long tile = blockIdx.x + (i / tile_steps) * static_cast<long>(gridDim.x);
-        return tile * tile_rows + static_cast<long>(i % tile_steps) * RS + ro;
-    };
+    // (tile, step) advance uniformly across the block (scalar registers); each
+    // thread's row follows from them without divisions.
+    long tile = blockIdx.x;
+    int step = 0;
+    long row = tile * tile_rows + ro;
+    int parity = 0;
 
-    ChunkLoad cur = load_chunk(wt, row_of(0), c, active);
+    ChunkLoad cur = load_chunk(wt, row, c, active);
     act.prepare();
     sink.prepare();
     uint32_t X[4][8];
@@ -346,22 +346,33 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(Weights wt, Act a
     __syncthreads();
     if (active) load_x(planes + c * 32, X);
 
-    for (long i = 0; i < nitems; ++i) {
-        const ChunkLoad nxt =
-            (i + 1 < nitems) ? load_chunk(wt, row_of(i + 1), c, active) : ChunkLoad{};
-        const int s = static_cast<int>(i % tile_steps);
-        const long t = i / tile_steps;
-        int* acc = (t & 1) ? acc1 : acc0;
-        if (cur.ok) atomicAdd(&acc[s * RS + ro], chunk_dot(cur.k, cur.v, X));
-        if (s == tile_steps - 1) {
-            __syncthreads();  // uniform: every thread has the same item count
-            const long row0 = (blockIdx.x + t * static_cast<long>(gridDim.x)) * tile_rows;
+    for (;;) {
+        int step_n = step + 1;
+        long tile_n = tile;
+        long row_n = row + RS;
+        if (step_n == tile_steps) {
+            step_n = 0;
+            tile_n = tile + gridDim.x;
+            row_n = tile_n * tile_rows + ro;
+        }
+        const bool more = tile_n < ntiles;
+        const ChunkLoad nxt = more ? load_chunk(wt, row_n, c, active) : ChunkLoad{};
+        int* acc = parity ? acc1 : acc0;
+        if (cur.ok) atomicAdd(&acc[step * RS + ro], chunk_dot(cur.k, cur.v, X));
+        if (step == tile_steps - 1) {
+            __syncthreads();  // uniform: (tile, step) are the same in every thread
+            const long row0 = tile * tile_rows;
             for (int j = tid; j < tile_rows; j += kBlock) {
                 if (row0 + j < wt.rows) sink.store(row0 + j, acc[j]);
                 acc[j] = 0;
             }
+            parity ^= 1;
         }
+        if (!more) break;
         cur = nxt;
+        step = step_n;
+        tile = tile_n;
+        row = row_n;
     }
 }
 

@@ -88,3 +88,20 @@ def test_gemv_kernel_selection(lib):
     assert kid(a16, a16, 64, 256, 8, 5) == 0        # values rows not 8-byte aligned
     assert kid(ctypes.c_void_p(0x10004), a16, 64, 256, 8, 4) == 0
     assert kid(a16, a16, 4, 65536, 2048, 1024) == 0  # beyond the bit-plane column limit
+
+
+def test_cpp_mirror_header_compiles_links_and_runs_noops(tmp_path):
+    """include/spbitnet/sparse_ternary_kernels.h (the reference's C++ names
+    over the C ABI) builds into a host program (ROCm clang, as hipcc uses for host code) and
+    links the library."""
+    from spbitnet_amd import _lib
+    exe = tmp_path / "mirror_api"
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    cmd = ["/opt/rocm/llvm/bin/clang++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+           "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "cpp", "mirror_api.cpp"),
+           "-L", libdir, "-lspbitnet_amd", f"-Wl,-rpath,{libdir}", "-o", str(exe)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "mirror api ok (abi 100)" in r.stdout
