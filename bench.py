@@ -271,6 +271,49 @@ def main() -> int:
                 "ms": round(t, 4), "GBs": round(dec_bytes / (t * 1e-3) / 1e9, 1), "exact": ok}
             del gph
 
+    if not args.no_detail:
+        # ---- config 2: batched GEMM, matrix-core (SMFMAC) vs add/sub kernel
+        L = base["gate"]
+        m, v = dev_base["gate"]
+        g2 = {}
+        for n in (16, 64, 256):
+            X = torch.from_numpy(np.stack([W.quantize_absmax_host(
+                W.normal_f32(W.seed_for("bench-gemm", t), H))[0] for t in range(n)])).to(dev)
+            Y = torch.empty((n, L.rows), dtype=torch.int32, device=dev)
+            row = {}
+            for kern in ("auto", "addsub"):
+                K.sparse_ternary_gemm_gpu(m, v, X, Y, L.rows, L.cols, n, L.meta_stride,
+                                          L.values_stride, kernel=kern)
+                torch.cuda.synchronize()
+                if kern == "auto":
+                    dense = W.unpack(L.meta, L.values, L.rows, L.cols).astype(np.float64)
+                    want2 = (X.cpu().numpy().astype(np.float64) @ dense.T).astype(np.int32)
+                    row["exact"] = bool((Y.cpu().numpy() == want2).all())
+                # 20 back-to-back launches captured in a graph, so the host's
+                # launch cost stays out of the kernel time
+                gph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gph):
+                    for _ in range(20):
+                        K.sparse_ternary_gemm_gpu(m, v, X, Y, L.rows, L.cols, n, L.meta_stride,
+                                                  L.values_stride, kernel=kern)
+                gph.replay()
+                torch.cuda.synchronize()
+                a, b = ev(), ev()
+                a.record(stream)
+                for _ in range(5):
+                    gph.replay()
+                b.record(stream)
+                torch.cuda.synchronize()
+                us = a.elapsed_time(b) * 1e3 / 100
+                del gph
+                name = "smfmac" if kern == "auto" else "addsub"
+                nb = L.rows * L.cols * 3 // 16 + n * L.cols + 4 * n * L.rows
+                row[f"{name}_us"] = round(us, 2)
+                row[f"{name}_GBs"] = round(nb / (us * 1e-6) / 1e9, 1)
+                row[f"{name}_dense_equiv_TOPS"] = round(2.0 * L.rows * L.cols * n / (us * 1e-6) / 1e12, 2)
+            g2[f"n{n}"] = row
+        detail["gemm_config2_6912x2560_warm_b2b"] = g2
+
     # ---- CPU baseline: the reference's CPU GEMV on this host, single thread
     cpu = None
     if not args.no_cpu_baseline:

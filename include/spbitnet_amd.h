@@ -102,6 +102,34 @@ int spb_dequantize_f16(const int32_t* input, uint16_t* output, const float* d_ab
 int spb_dequantize_bf16(const int32_t* input, uint16_t* output, const float* d_absmax,
                         float gamma, int size, spb_stream_t stream);
 
+/* ---- Batched GEMM ---------------------------------------------------------------
+ * Replaces the cuSPARSELt path CuSparseLtGemm(m,k,n) + execute
+ * (reference include/spbitnet/cusparselt_backend.h:28-77,
+ *  src/cusparselt_backend.cu:38-207): Y[t][r] = sum_c W[r][c] * X[t][c] as
+ * exact int32 on the packed 2:4 ternary weights (no library pruning or
+ * compression step).  X int8 [n][cols] and Y int32 [n][rows] are token-major,
+ * which is the column-major B [K x N] / D [M x N] memory of the reference.
+ * Any n >= 1 (the reference requires n >= 16, src/cusparselt_backend.cu:41-45).
+ * Runs on the int8 structured-sparse matrix cores (v_smfmac_i32_16x16x128_i8)
+ * when cols % 128 == 0 and X is 16-byte aligned, else a general kernel. */
+int spb_sparse_ternary_gemm(const uint32_t* meta, const uint32_t* values, const int8_t* X,
+                            int32_t* Y, int rows, int cols, int n, int meta_row_stride,
+                            int values_row_stride, spb_stream_t stream);
+
+/* The same product on the add/sub bit-plane GEMV kernel (tokens on grid.y),
+ * kept as the comparator for the matrix-core kernel.  Needs the bit-plane
+ * kernel's shape conditions and cols % 16 == 0. */
+int spb_sparse_ternary_gemm_addsub(const uint32_t* meta, const uint32_t* values,
+                                   const int8_t* X, int32_t* Y, int rows, int cols, int n,
+                                   int meta_row_stride, int values_row_stride,
+                                   spb_stream_t stream);
+
+/* 1 if spb_sparse_ternary_gemm would use the matrix-core kernel, else 0.
+ * Host-only query; no reference counterpart. */
+int spb_sparse_ternary_gemm_kernel_id(const uint32_t* meta, const uint32_t* values,
+                                      const int8_t* X, int rows, int cols, int n,
+                                      int meta_row_stride, int values_row_stride);
+
 /* ---- Bit-plane activation layout -------------------------------------------
  * No reference counterpart: an activation layout of this build.  An int8
  * vector of `cols` columns is stored as 8 * ceil(cols/32) uint32 words;

@@ -34,6 +34,9 @@ SIGNATURES = {
     "spb_dequantize_bf16": [_P, _P, _P, _F, _I, _P],
     "spb_sparse_ternary_gemv_kernel_id": [_P, _P, _I, _I, _I, _I],
     "spb_activation_planes": [_P, _P, _I, _P],
+    "spb_sparse_ternary_gemm": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "spb_sparse_ternary_gemm_addsub": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "spb_sparse_ternary_gemm_kernel_id": [_P, _P, _P, _I, _I, _I, _I, _I],
     "spb_absmax_quantize_planes_f16": [_P, _P, _P, _P, _I, _P],
     "spb_absmax_quantize_planes_bf16": [_P, _P, _P, _P, _I, _P],
     "spb_sparse_ternary_gemv_planes": [_P, _P, _P, _P, _I, _I, _I, _I, _P],

@@ -1,0 +1,250 @@
+// gemm.hip -- batched 2:4 sparse-ternary GEMM on the int8 structured-sparse
+// matrix cores of gfx950 (v_smfmac_i32_16x16x128_i8).
+//
+// What it computes: Y[t][r] = sum_c W[r][c] * X[t][c] (exact int32), X
+// token-major int8 [n][cols], Y token-major int32 [n][rows]; this is the
+// reference's cuSPARSELt product D = A * B with B [K x N] and D [M x N]
+// column-major (src/cusparselt_backend.cu:53-62, 83-89, 186-207), computed
+// directly on spbitnet's packed format instead of a library-pruned copy.
+//
+// Why the format maps onto SMFMAC with no repacking:
+//   * The sparse A operand of v_smfmac_i32_16x16x128_i8 is 16 rows x 128 K in
+//     compressed form: lane l holds row l%16, logical K [32*(l/16), +32) as 8
+//     groups of 4, two int8 values per group (16 bytes), plus a 32-bit index
+//     word with the 2-bit position of compressed byte j at bits [2j, 2j+1].
+//     One spbitnet meta word is exactly one lane's 32 columns.
+//   * The compressed values are the kept weights in column order, lower first;
+//     spbitnet's sign bits are in the same order (bit 2g = lower, 2g+1 =
+//     higher), so byte j = (sign bit j ? -1 : +1).
+//   * The index nibble of group g is p0 | p1 << 2 (p0 < p1 the set bits of
+//     bitmap b), computed for 8 groups at once:
+//       p0 bit0 = ~b0 & b1,  p0 bit1 = ~(b0 | b1),
+//       p1 bit0 =  b3 | ~b2, p1 bit1 =  b3 | b2
+//     (four v_bitop3_b32 on the meta word and its 1-bit shifts).
+//   * B (activations, 128 K x 16 tokens): lane l holds token l%16; bytes
+//     0..15 are K 16*(l/16) + i and bytes 16..31 are K 64 + 16*(l/16) + i.
+//     C (16 rows x 16 tokens, int32): lane l holds token l%16, rows
+//     4*(l/16) + v in VGPR v.
+// These operand layouts were established on the hardware with register-only
+// probes and are pinned by the GPU parity tests against the CPU oracle.
+//
+// Work mapping: a block of 8 waves owns kStrips 16-row strips and one pass
+// of kTiles*16 tokens (grid.y); the waves split K in 128-column steps.  Per
+// step a wave decodes each strip's A operand once (one meta word and 16 sign
+// bits per lane: ~24 VALU ops) and reuses each B tile for kStrips SMFMACs.
+// Partial sums are reduced across the waves in LDS.
+#include "common.hpp"
+#include "spbitnet_amd.h"
+
+namespace spb {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kGemmBlock = 512;  // 8 waves splitting K
+
+template <uint32_t kTable>
+__device__ __forceinline__ uint32_t bitop3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, kTable);
+}
+
+// Index word of one meta word (8 groups): nibble g = p0 | p1 << 2.
+__device__ __forceinline__ int smfmac_index(uint32_t k) {
+    const uint32_t a = k >> 1, c = k << 1;
+    const uint32_t t0 = bitop3<0x20>(a, k, 0x11111111u);  // (a & ~b) & m : ~b0 & b1
+    const uint32_t t1 = bitop3<0x02>(c, k, 0x22222222u);  // ~(a | b) & m : ~(b0 | b1)
+    const uint32_t t2 = bitop3<0xA2>(a, k, 0x44444444u);  // (a | ~b) & m : b3 | ~b2
+    const uint32_t t3 = bitop3<0xA8>(c, k, 0x88888888u);  // (a | b) & m  : b3 | b2
+    return static_cast<int>(bitop3<0xFE>(t0, t1, t2) | t3);
+}
+
+// Four compressed-value dwords (16 int8 +-1) from 16 sign bits: bit j -> byte j.
+__device__ __forceinline__ v4i smfmac_values(uint32_t s16) {
+    v4i a;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t nib = (s16 >> (4 * d)) & 0xFu;
+        const uint32_t nb = (nib * 0x00204081u) & 0x01010101u;  // bit i -> byte i (0/1)
+        // per 16-bit half: 0/1 bytes * 0xFE + 0x0101 -> 0x01 / 0xFF bytes, no carries
+        u16x2 h = __builtin_bit_cast(u16x2, nb);
+        h = h * (u16x2){0xFE, 0xFE} + (u16x2){0x0101, 0x0101};
+        a[d] = __builtin_bit_cast(int, h);
+    }
+    return a;
+}
+
+// Block: kWaves waves on the same kStrips*16 rows and the same pass of
+// kTiles*16 tokens (pass = blockIdx.y), splitting K: wave w takes the
+// 128-column steps s = w, w + kWaves, ...  Each wave decodes its A operands
+// once per step and reuses every B tile for kStrips SMFMACs.  The waves'
+// int32 partial sums meet in LDS (integer atomics, exact in any order).
+template <int kStrips, int kTiles>
+__global__ __launch_bounds__(kGemmBlock) void gemm_smfmac_kernel(
+    const uint32_t* __restrict__ meta, const uint32_t* __restrict__ values,
+    const int8_t* __restrict__ X, int32_t* __restrict__ Y, int rows, int cols, int n, int ms,
+    int vs) {
+    constexpr int kWaves = kGemmBlock / kWave;
+    constexpr int kAcc = kStrips * kTiles * 4;  // int32 accumulators per lane
+    __shared__ int red[kAcc * kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const long r0 = static_cast<long>(blockIdx.x) * (kStrips * 16);
+    const int tok0 = blockIdx.y * (kTiles * 16);
+    const int q = lane >> 4;   // lane group
+    const int li = lane & 15;  // A row / B,C token within a tile
+
+    for (int i = threadIdx.x; i < kAcc * kWave; i += kGemmBlock) red[i] = 0;
+
+    v4i acc[kStrips][kTiles];
+#pragma unroll
+    for (int st = 0; st < kStrips; ++st)
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[st][t] = (v4i){0, 0, 0, 0};
+
+    const int nsteps = cols >> 7;
+    for (int s = wave; s < nsteps; s += kWaves) {
+        const int w = 4 * s + q;  // this lane's meta word
+        v4i a[kStrips];
+        int idx[kStrips];
+#pragma unroll
+        for (int st = 0; st < kStrips; ++st) {
+            const long ra = r0 + st * 16 + li;
+            a[st] = (v4i){0, 0, 0, 0};
+            idx[st] = 0;
+            if (ra < rows) {
+                const uint32_t k = meta[ra * ms + w];
+                const uint32_t vw = values[ra * vs + (w >> 1)];
+                idx[st] = smfmac_index(k);
+                a[st] = smfmac_values((w & 1) ? (vw >> 16) : (vw & 0xFFFFu));
+            }
+        }
+        const int kb = s * 128 + 16 * q;  // B bytes 0..15 -> K kb.., 16..31 -> K kb+64..
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            const int tok = tok0 + t * 16 + li;
+            v8i b = (v8i){0, 0, 0, 0, 0, 0, 0, 0};
+            if (tok < n) {
+                const int8_t* xr = X + static_cast<long>(tok) * cols + kb;
+                const uint4 lo = *reinterpret_cast<const uint4*>(xr);
+                const uint4 hi = *reinterpret_cast<const uint4*>(xr + 64);
+                b = (v8i){static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
+                          static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
+                          static_cast<int>(hi.z), static_cast<int>(hi.w)};
+            }
+#pragma unroll
+            for (int st = 0; st < kStrips; ++st)
+                acc[st][t] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a[st], b, acc[st][t],
+                                                                       idx[st], 0, 0);
+        }
+    }
+    __syncthreads();  // red[] zeroed
+#pragma unroll
+    for (int st = 0; st < kStrips; ++st)
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                atomicAdd(&red[((st * kTiles + t) * 4 + v) * kWave + lane], acc[st][t][v]);
+    __syncthreads();
+    // Write-out: entry (st, t, v) of lane l is token tok0 + 16t + l%16, row
+    // r0 + 16st + 4(l/16) + v.  Waves share the entries.
+    for (int e = threadIdx.x; e < kAcc * kWave; e += kGemmBlock) {
+        const int l = e % kWave;
+        const int sv = e / kWave;  // (st * kTiles + t) * 4 + v
+        const int v = sv & 3;
+        const int t = (sv >> 2) % kTiles;
+        const int st = (sv >> 2) / kTiles;
+        const int tok = tok0 + 16 * t + (l & 15);
+        const long row = r0 + 16 * st + 4 * (l >> 4) + v;
+        if (tok < n && row < rows) Y[static_cast<long>(tok) * rows + row] = red[e];
+    }
+}
+
+// General batched kernel: one wave per row, tokens looped inside; any shape.
+__global__ __launch_bounds__(256) void gemm_general_kernel(const uint32_t* __restrict__ meta,
+                                                           const uint32_t* __restrict__ values,
+                                                           const int8_t* __restrict__ X,
+                                                           int32_t* __restrict__ Y, int rows,
+                                                           int cols, int n, int ms, int vs) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const long row = static_cast<long>(blockIdx.x) * 4 + threadIdx.x / kWave;
+    const int tok = blockIdx.y;
+    if (row >= rows) return;
+    const uint32_t* mr = meta + row * ms;
+    const uint32_t* vr = values + row * vs;
+    const int8_t* x = X + static_cast<long>(tok) * cols;
+    int acc = 0;
+    for (int g = lane; g < (cols >> 2); g += kWave) {
+        const uint32_t bm = (mr[g >> 3] >> ((g & 7) * 4)) & 0xFu;
+        const uint32_t sg = (vr[g >> 4] >> ((g & 15) * 2)) & 0x3u;
+        const bool ok = __builtin_popcount(bm) == 2;
+        const int p0 = ok ? __builtin_ctz(bm) : 0;
+        const int p1 = ok ? __builtin_ctz(bm & (bm - 1)) : 0;
+        const int x0 = x[4 * g + p0], x1 = x[4 * g + p1];
+        acc += (sg & 1u) ? -x0 : x0;
+        acc += (sg & 2u) ? -x1 : x1;
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) Y[static_cast<long>(tok) * rows + row] = acc;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+}  // namespace
+}  // namespace spb
+
+using namespace spb;
+
+extern "C" int spb_sparse_ternary_gemm_kernel_id(const uint32_t* meta, const uint32_t* values,
+                                                 const int8_t* X, int rows, int cols, int n,
+                                                 int ms, int vs) {
+    (void)meta;
+    (void)values;
+    (void)rows;
+    (void)n;
+    (void)ms;
+    (void)vs;
+    return (cols > 0 && cols % 128 == 0 && aligned(X, 16)) ? 1 : 0;
+}
+
+extern "C" int spb_sparse_ternary_gemm(const uint32_t* meta, const uint32_t* values,
+                                       const int8_t* X, int32_t* Y, int rows, int cols, int n,
+                                       int ms, int vs, spb_stream_t stream) {
+    clear_error();
+    const char* fn = "spb_sparse_ternary_gemm";
+    if (rows < 0 || cols < 0 || n < 0) return invalid("%s: negative shape", fn);
+    if (cols % 4) return invalid("%s: cols=%d is not a multiple of 4", fn, cols);
+    if (ms < (cols / 4 + 7) / 8 || vs < (cols / 4 + 15) / 16)
+        return invalid("%s: row strides are smaller than the format requires", fn);
+    if (rows == 0 || cols == 0 || n == 0) return 0;
+    if (!meta || !values || !X || !Y) return invalid("%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    if (spb_sparse_ternary_gemm_kernel_id(meta, values, X, rows, cols, n, ms, vs)) {
+        // Rows per block (16 * strips) and tokens per pass (16 * tiles): more
+        // rows per block when there are many tokens, so each activation tile
+        // read from L2 feeds more matrix-core operations.
+        if (n <= 16) {
+            const int bx = (rows + 15) / 16;
+            hipLaunchKernelGGL((gemm_smfmac_kernel<1, 1>), dim3(bx, 1), dim3(kGemmBlock), 0, st,
+                               meta, values, X, Y, rows, cols, n, ms, vs);
+        } else if (n <= 64) {
+            const int bx = (rows + 31) / 32;
+            const int by = (n + 63) / 64;
+            hipLaunchKernelGGL((gemm_smfmac_kernel<2, 4>), dim3(bx, by), dim3(kGemmBlock), 0, st,
+                               meta, values, X, Y, rows, cols, n, ms, vs);
+        } else {
+            const int bx = (rows + 63) / 64;
+            const int by = (n + 63) / 64;
+            if (by > 65535) return invalid("%s: batch %d too large", fn, n);
+            hipLaunchKernelGGL((gemm_smfmac_kernel<4, 4>), dim3(bx, by), dim3(kGemmBlock), 0, st,
+                               meta, values, X, Y, rows, cols, n, ms, vs);
+        }
+    } else {
+        if (n > 65535) return invalid("%s: batch %d exceeds 65535", fn, n);
+        hipLaunchKernelGGL(gemm_general_kernel, dim3((rows + 3) / 4, n), dim3(256), 0, st, meta,
+                           values, X, Y, rows, cols, n, ms, vs);
+    }
+    return launch_status(fn);
+}

@@ -109,6 +109,8 @@ __device__ __forceinline__ void transpose8x8(uint32_t& lo, uint32_t& hi) {
 // int8 activations.
 struct Int8Src {
     const int8_t* x;
+    long token_stride = 0;  // batched use: token t reads x + t * token_stride
+    __device__ void offset(long t) { x += t * token_stride; }
     __device__ void prepare() {}
     __device__ int load(int c) const { return x[c]; }
     // Columns c0..c7 as two little-endian dwords (c0 % 8 == 0, x 8-byte aligned).
@@ -125,6 +127,7 @@ struct QuantSrc {
     const uint16_t* x;
     const float* d_absmax;
     float scale;
+    __device__ void offset(long) {}
     __device__ void prepare() { scale = quant_scale(*d_absmax); }
     __device__ int load(int c) const { return quant_round_clamp(T::to_float(x[c]) * scale); }
     __device__ uint32_t q8(uint32_t h) const {
@@ -162,6 +165,7 @@ struct PlaneSrc {
 template <class Src>
 struct BuildPlanes {
     Src src;
+    __device__ void offset(long t) { src.offset(t); }
     __device__ void prepare() { src.prepare(); }
     // Transposes the activations, 8 columns per thread, into LDS planes
     // (bytes of word [w*8+b]).  The loads of up to two units are issued
@@ -201,6 +205,7 @@ struct BuildPlanes {
 // from L2 for cols bytes of data).
 struct GlobalPlanes {
     const uint32_t* p;
+    __device__ void offset(long) {}
     __device__ void prepare() {}
     __device__ void build(uint32_t* planes, int cols, int tid) const {
         const uint4* src = reinterpret_cast<const uint4*>(p);
@@ -213,6 +218,8 @@ struct GlobalPlanes {
 
 struct Int32Sink {
     int32_t* y;
+    long token_stride = 0;  // batched use: token t writes y + t * token_stride
+    __device__ void offset(long t) { y += t * token_stride; }
     __device__ void prepare() {}
     __device__ void store(long r, int acc) const { y[r] = acc; }
 };
@@ -223,6 +230,7 @@ struct DequantSink {
     const float* d_absmax;
     float gamma;
     float dq;
+    __device__ void offset(long) {}
     __device__ void prepare() { dq = dequant_scale(gamma, *d_absmax); }
     __device__ void store(long r, int acc) const {
         out[r] = T::from_float(static_cast<float>(acc) * dq);
@@ -337,6 +345,8 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(Weights wt, Act a
     long row = tile * tile_rows + ro;
     int parity = 0;
 
+    act.offset(blockIdx.y);
+    sink.offset(blockIdx.y);
     ChunkLoad cur = load_chunk(wt, row, c, active);
     act.prepare();
     sink.prepare();
@@ -533,14 +543,15 @@ int bitplane_blocks_per_cu(size_t lds) {
 }
 
 template <class Act, class Sink>
-void launch_bitplane(const Weights& wt, Act act, Sink sink, hipStream_t stream) {
+void launch_bitplane(const Weights& wt, Act act, Sink sink, hipStream_t stream, int tokens = 1) {
     const int C = wt.cols / kChunk;
     const long RS = kBlock / C;
     const long steps_max = 8;
     const size_t plane_lds = static_cast<size_t>(wt.cols);
     const size_t lds_max = plane_lds + 2 * RS * steps_max * 4;
-    const long resident =
+    long resident =
         static_cast<long>(bitplane_blocks_per_cu<Act, Sink>(lds_max)) * device_cu_count();
+    resident = (resident + tokens - 1) / tokens;  // tokens share the resident capacity
     // Enough tiles for every resident block; longer tiles once the matrix
     // is several times the resident capacity.
     long steps = (static_cast<long>(wt.rows) + RS * resident - 1) / (RS * resident);
@@ -549,8 +560,8 @@ void launch_bitplane(const Weights& wt, Act act, Sink sink, hipStream_t stream) 
     const long tiles = (wt.rows + tile_rows - 1) / tile_rows;
     const int grid = static_cast<int>(tiles < resident ? tiles : resident);
     const size_t lds = plane_lds + 2 * static_cast<size_t>(tile_rows) * 4;
-    hipLaunchKernelGGL((gemv_bitplane_kernel<Act, Sink>), dim3(grid), dim3(kBlock), lds, stream,
-                       wt, act, sink, static_cast<int>(steps), tiles);
+    hipLaunchKernelGGL((gemv_bitplane_kernel<Act, Sink>), dim3(grid, tokens), dim3(kBlock), lds,
+                       stream, wt, act, sink, static_cast<int>(steps), tiles);
 }
 
 template <class Src, class Sink>
@@ -737,4 +748,28 @@ extern "C" int spb_absmax_quantize_planes_bf16(const uint16_t* input, uint32_t* 
                                                spb_stream_t stream) {
     return absmax_quantize_planes<BF16>("spb_absmax_quantize_planes_bf16", input, planes,
                                         output, d_absmax, size, stream);
+}
+
+// Batched add/sub GEMM: the bit-plane GEMV kernel with tokens on grid.y (each
+// token's activations decoded into planes by its own blocks; weights re-read
+// per token from L2).  X token-major [n][cols] int8, Y token-major [n][rows].
+extern "C" int spb_sparse_ternary_gemm_addsub(const uint32_t* meta, const uint32_t* values,
+                                              const int8_t* X, int32_t* Y, int rows, int cols,
+                                              int n, int ms, int vs, spb_stream_t stream) {
+    clear_error();
+    const char* fn = "spb_sparse_ternary_gemm_addsub";
+    if (int e = check_weights(fn, meta, values, rows, cols, ms, vs)) return e;
+    if (n < 0) return invalid("%s: negative batch", fn);
+    if (rows == 0 || cols == 0 || n == 0) return 0;
+    if (!X || !Y) return invalid("%s: null activation or output pointer", fn);
+    if (n > 65535) return invalid("%s: batch %d exceeds 65535", fn, n);
+    if (!bitplane_ok(meta, values, cols, ms, vs) || !aligned(X, 16) || (cols % 16))
+        return invalid("%s: needs cols %% 128 == 0, aligned rows and 16-byte aligned X", fn);
+    Int8Src src{X};
+    src.token_stride = cols;
+    Int32Sink sink{Y};
+    sink.token_stride = rows;
+    launch_bitplane(Weights{meta, values, rows, cols, ms, vs}, BuildPlanes<Int8Src>{src}, sink,
+                    as_stream(stream), n);
+    return launch_status(fn);
 }

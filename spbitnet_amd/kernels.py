@@ -126,6 +126,34 @@ def dequantize_gpu(input, output, d_absmax, gamma, size, stream=None):
     _lib.check(fn(pi, po, pa, float(gamma), size, _stream_ptr(stream)), "dequantize_gpu")
 
 
+# ---- batched GEMM (replaces the reference's cuSPARSELt path) ------------------
+
+def sparse_ternary_gemm_gpu(meta, values, X, Y, rows, cols, n, meta_row_stride,
+                            values_row_stride, stream=None, kernel="auto"):
+    """Y[t][r] = sum_c W[r][c] X[t][c] (int32), X int8 [n][cols], Y int32 [n][rows].
+
+    Replaces CuSparseLtGemm::execute (reference src/cusparselt_backend.cu:186-207);
+    kernel="auto" uses the matrix-core kernel where the shape allows,
+    kernel="addsub" the bit-plane GEMV kernel over tokens (the comparator)."""
+    pm, pv = _weights(meta, values, rows, cols, meta_row_stride, values_row_stride)
+    if n < 0:
+        raise ValueError("negative batch")
+    empty = rows == 0 or cols == 0 or n == 0
+    px = _dev(X, "X", torch.int8, 0 if empty else n * cols)
+    py = _dev(Y, "Y", torch.int32, 0 if empty else n * rows)
+    L = _lib.load()
+    fn = L.spb_sparse_ternary_gemm if kernel == "auto" else L.spb_sparse_ternary_gemm_addsub
+    _lib.check(fn(pm, pv, px, py, rows, cols, n, meta_row_stride, values_row_stride,
+                  _stream_ptr(stream)), "sparse_ternary_gemm_gpu")
+
+
+def gemm_kernel_id(meta, values, X, rows, cols, n, meta_row_stride, values_row_stride) -> int:
+    """1 if the matrix-core GEMM kernel would run for these arguments, else 0."""
+    return _lib.load().spb_sparse_ternary_gemm_kernel_id(
+        meta.data_ptr(), values.data_ptr(), X.data_ptr(), rows, cols, n, meta_row_stride,
+        values_row_stride)
+
+
 # ---- bit-plane activation layout (no reference counterpart) -----------------
 
 def planes_words(cols: int) -> int:

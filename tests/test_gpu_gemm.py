@@ -1,0 +1,81 @@
+"""GPU parity of the batched GEMM (replacing the reference's cuSPARSELt path,
+whose own test checks D = A_pruned * B exactly against cpu_int8_gemm,
+tests/test_cusparselt.cu:16-28, 127-274) against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from spbitnet_amd import kernels as K
+from spbitnet_amd import weights as W
+from tests.test_gpu_sparse_ternary import dev, dev_u32
+
+pytestmark = pytest.mark.gpu
+
+
+def expected(L, X):
+    """Exact int32 product via the oracle's unpacked matrix (float64 BLAS is
+    exact here: |products| <= 128 and |sums| < 2^53)."""
+    dense = O.unpack(L.meta, L.values, L.rows, L.cols).astype(np.float64)
+    return (X.astype(np.float64) @ dense.T).astype(np.int64).astype(np.int32)
+
+
+def run(L, X, gpu, kernel="auto"):
+    n = X.shape[0]
+    Y = torch.full((n, L.rows), -7, dtype=torch.int32, device=gpu)
+    K.sparse_ternary_gemm_gpu(dev_u32(L.meta, gpu), dev_u32(L.values, gpu), dev(X, gpu), Y,
+                              L.rows, L.cols, n, L.meta_stride, L.values_stride, kernel=kernel)
+    torch.cuda.synchronize()
+    return Y.cpu().numpy()
+
+
+def activations(n, cols, seed):
+    q = np.zeros((n, cols), np.int8)
+    for t in range(n):
+        q[t], _ = W.quantize_absmax_host(W.normal_f32(seed + t, cols))
+    return q
+
+
+def test_gemm_n16_matches_oracle_gemm(gpu):
+    """cpu_int8_gemm (the oracle) at the reference test's shape family."""
+    rows, cols, n = 64, 256, 16
+    L = W.random_layer(rows, cols, 5)
+    X = np.random.default_rng(6).integers(-5, 6, (n, cols)).astype(np.int8)
+    assert (run(L, X, gpu) == O.gemm(L.meta, L.values, X, rows, cols)).all()
+
+
+@pytest.mark.parametrize("n", [16, 64, 256])
+def test_gemm_config2(gpu, n):
+    rows, cols = 6912, 2560
+    L = W.random_layer(rows, cols, W.seed_for("gemm", n))
+    X = activations(n, cols, 1000 + n)
+    X_dev = dev(X, gpu)
+    assert K.gemm_kernel_id(dev_u32(L.meta, gpu), dev_u32(L.values, gpu), X_dev, rows, cols, n,
+                            L.meta_stride, L.values_stride) == 1
+    assert (run(L, X, gpu) == expected(L, X)).all()
+
+
+@pytest.mark.parametrize("rows,cols,n", [(2560, 6912, 16), (7, 128, 1), (333, 384, 5),
+                                         (100, 256, 17), (16, 512, 100), (45, 100, 3),
+                                         (9, 36, 20)])
+def test_gemm_odd_shapes(gpu, rows, cols, n):
+    L = W.random_layer(rows, cols, W.seed_for("gemm-odd", rows, cols, n))
+    X = np.random.default_rng(rows + cols + n).integers(-128, 128, (n, cols)).astype(np.int8)
+    assert (run(L, X, gpu) == expected(L, X)).all()
+
+
+def test_gemm_extremes(gpu):
+    rows, cols, n = 32, 6912, 16
+    L = W.random_layer(rows, cols, 8)
+    dense = O.unpack(L.meta, L.values, rows, cols)
+    X = np.stack([np.full(cols, -128), np.full(cols, 127)] +
+                 [np.where(dense[i] < 0, -128, 127) for i in range(14)]).astype(np.int8)
+    assert (run(L, X, gpu) == expected(L, X)).all()
+
+
+@pytest.mark.parametrize("n", [1, 16, 37])
+def test_gemm_addsub_comparator(gpu, n):
+    rows, cols = 2560, 2560
+    L = W.random_layer(rows, cols, W.seed_for("addsub", n))
+    X = activations(n, cols, 77)
+    assert (run(L, X, gpu, kernel="addsub") == expected(L, X)).all()
