@@ -181,6 +181,92 @@ int spb_sparse_ternary_gemv_kernel_id(const uint32_t* meta, const uint32_t* valu
                                       int rows, int cols, int meta_row_stride,
                                       int values_row_stride);
 
+
+/* ---- decode engine --------------------------------------------------------
+ * bs=1 greedy decode of a BitNet b1.58 transformer whose linear layers are
+ * 2:4 sparse-ternary, with bf16 activations, bf16 KV cache and a bf16 tied or
+ * separate LM head.  One token step is a HIP graph of 5 kernels per layer
+ * plus the LM head; greedy generation runs entirely on the device.
+ * Replaces the reference's InferenceEngine (include/spbitnet/inference.h:23-70,
+ * src/inference.cu:16-283) and its generate loop (src/main.cpp:119-200).
+ * Constraints: every projection takes the bit-plane kernel (cols % 128 == 0,
+ * meta_stride % 4 == 0, values_stride % 2 == 0, 16/8-byte aligned rows),
+ * head_dim even and <= 128, at most 8 query heads per kv head,
+ * hidden_size <= 8192. */
+
+/* SparseLinear (reference include/spbitnet/model.h:46-60). */
+typedef struct spb_sparse_linear {
+    const uint32_t* meta;
+    const uint32_t* values;
+    float gamma;
+    int rows, cols, meta_stride, values_stride;
+} spb_sparse_linear;
+
+/* TransformerLayer (reference include/spbitnet/model.h:63-82); norm weights
+ * are device float32; attn_sub_norm / ffn_sub_norm may be NULL (skipped, as
+ * in src/inference.cu:205-210, 239-245). */
+typedef struct spb_transformer_layer {
+    spb_sparse_linear q_proj, k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj;
+    const float* input_layernorm;
+    const float* post_attention_layernorm;
+    const float* attn_sub_norm;
+    const float* ffn_sub_norm;
+} spb_transformer_layer;
+
+/* ModelConfig (reference include/spbitnet/model.h:23-40), numeric fields. */
+typedef struct spb_model_config {
+    int hidden_size, num_hidden_layers, num_attention_heads, num_key_value_heads;
+    int intermediate_size, vocab_size, max_position_embeddings, head_dim;
+    float rms_norm_eps, rope_theta;
+    int bos_token_id, eos_token_id;
+} spb_model_config;
+
+typedef struct spb_engine spb_engine;
+
+/* InferenceEngine(const Model&) (inference.h:27): borrows the weights (they
+ * must outlive the engine), allocates the KV cache for max_seq positions and
+ * scratch, and captures the token-step graph.  embed_tokens / lm_head: bf16
+ * [vocab][hidden]; lm_head NULL = tied to the embedding. */
+int spb_engine_create(const spb_model_config* config, const spb_transformer_layer* layers,
+                      const uint16_t* embed_tokens, const uint16_t* lm_head,
+                      const float* final_norm, int max_seq, spb_engine** engine);
+int spb_engine_destroy(spb_engine* engine);
+/* Stream the engine's graphs run on (default: the null stream). */
+int spb_engine_set_stream(spb_engine* engine, spb_stream_t stream);
+/* InferenceEngine::reset (inference.h:36; inference.cu:92-101). */
+int spb_engine_reset(spb_engine* engine);
+/* InferenceEngine::forward (inference.h:33; inference.cu:126-283): one token
+ * at the next position; *d_logits = device float32 [vocab] (valid until the
+ * next call; ordered on the engine stream). */
+int spb_engine_forward(spb_engine* engine, int token_id, const float** d_logits);
+/* InferenceEngine::seq_len (inference.h:38). */
+int spb_engine_seq_len(const spb_engine* engine);
+/* Greedy generation (src/main.cpp:133-155): reset, prefill prompt[0..n-1)
+ * one token at a time, then n_new greedy steps starting from the last prompt
+ * token (argmax = lowest index among maxima); stops after EOS when
+ * stop_at_eos.  All steps are graph launches; the host waits once. */
+int spb_engine_generate(spb_engine* engine, const int* prompt, int n_prompt, int n_new,
+                        int stop_at_eos, int* out_tokens, int* n_generated);
+/* Launches `steps` more token steps continuing the current state (timing
+ * loops); no host synchronisation. */
+int spb_engine_decode_steps(spb_engine* engine, int steps);
+/* Device buffers: logits float32 [vocab], tokens int32 [max_seq + 1]. */
+int spb_engine_buffers(const spb_engine* engine, const float** logits, const int** tokens);
+
+/* ---- random-init weights on the device ------------------------------------
+ * Latent W ~ N(0,1) from a counter-based generator (seed, element index),
+ * 2:4 top-2 |W| mask (higher index wins ties), kept value sign(W) (W >= 0 ->
+ * +1), packed; *d_gamma = mean|W|; latent (nullable) receives W.  The
+ * recipe of python/convert_model.py:88-207, 257-316 on a synthetic W.
+ * cols % 64 == 0.  Calls on one device must not overlap (they share a
+ * 1024-entry partial-sum array). */
+int spb_generate_sparse_ternary(uint64_t seed, int rows, int cols, uint32_t* meta,
+                                uint32_t* values, int meta_stride, int values_stride,
+                                float* d_gamma, float* latent, spb_stream_t stream);
+/* out[i] = bf16(std * N(0,1)) from the same generator (embedding init). */
+int spb_generate_normal_bf16(uint64_t seed, long n, float std_dev, uint16_t* out,
+                             spb_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -273,3 +273,110 @@ def ref_make_test_case(seed: int, rows: int, cols: int, want_x: bool):
     x = np.zeros(cols, np.int8)
     ref().ref_make_test_case(seed, rows, cols, int(want_x), _p(w), _p(mask), _p(x))
     return w, mask, (x if want_x else None)
+
+
+# ---- decode-step restatement (spb_engine_oracle.c) ---------------------------------
+
+_engine_lib = None
+
+
+def _elib():
+    global _engine_lib
+    if _engine_lib is None:
+        L = lib()
+        L.spbo_engine_new.argtypes = [_P] * 11
+        L.spbo_engine_new.restype = _P
+        L.spbo_engine_free.argtypes = [_P]
+        L.spbo_engine_reset.argtypes = [_P]
+        L.spbo_engine_step.argtypes = [_P, _I, _P]
+        L.spbo_engine_step.restype = _I
+        L.spbo_engine_hidden.argtypes = [_P, _P]
+        L.spbo_exp_neg.argtypes = [_F]
+        L.spbo_exp_neg.restype = _F
+        _engine_lib = L
+    return _engine_lib
+
+
+def exp_neg(x: float) -> float:
+    return float(np.float32(_elib().spbo_exp_neg(float(x))))
+
+
+class EngineOracle:
+    """CPU decode step of the reference engine (src/inference.cu:126-283) on
+    host copies of a model (spbitnet_amd.model.Model.to_host())."""
+
+    PROJ = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+    def __init__(self, host: dict, max_seq: int):
+        c = host["config"]
+        self._keep = []
+        nl = len(host["layers"])
+
+        def arr(a, dt):
+            a = np.ascontiguousarray(a, dtype=dt)
+            self._keep.append(a)
+            return a
+
+        metas = (ctypes.c_void_p * (7 * nl))()
+        values = (ctypes.c_void_p * (7 * nl))()
+        gam = np.zeros(7 * nl, np.float32)
+        ms = np.zeros(7 * nl, np.int32)
+        vs = np.zeros(7 * nl, np.int32)
+        norms = (ctypes.c_void_p * (4 * nl))()
+        for l, d in enumerate(host["layers"]):
+            for k, p in enumerate(self.PROJ):
+                m, v, g, rows, cols, mstr, vstr = d[p]
+                metas[7 * l + k] = arr(m, np.uint32).ctypes.data
+                values[7 * l + k] = arr(v, np.uint32).ctypes.data
+                gam[7 * l + k] = g
+                ms[7 * l + k] = mstr
+                vs[7 * l + k] = vstr
+            for k, t in enumerate(d["norms"]):
+                norms[4 * l + k] = None if t is None else arr(t, np.float32).ctypes.data
+        self._keep += [metas, values, gam, ms, vs, norms]
+        icfg = arr([c.hidden_size, c.num_hidden_layers, c.num_attention_heads,
+                    c.num_key_value_heads, c.intermediate_size, c.vocab_size, c.head_dim,
+                    max_seq], np.int32)
+        fcfg = arr([c.rms_norm_eps, c.rope_theta], np.float32)
+        embed = arr(host["embed"], np.uint16)
+        lm = None if host["lm_head"] is None else arr(host["lm_head"], np.uint16).ctypes.data
+        fn = arr(host["final_norm"], np.float32)
+        self.vocab = c.vocab_size
+        self.hidden_size = c.hidden_size
+        self._e = _elib().spbo_engine_new(icfg.ctypes.data, fcfg.ctypes.data, metas, values,
+                                          gam.ctypes.data, ms.ctypes.data, vs.ctypes.data,
+                                          norms, embed.ctypes.data, lm, fn.ctypes.data)
+
+    def __del__(self):
+        if getattr(self, "_e", None):
+            _elib().spbo_engine_free(self._e)
+            self._e = None
+
+    def reset(self):
+        _elib().spbo_engine_reset(self._e)
+
+    def step(self, token: int):
+        """(argmax, float32 logits) after feeding `token` at the next position."""
+        logits = np.empty(self.vocab, np.float32)
+        t = _elib().spbo_engine_step(self._e, int(token), _p(logits))
+        return int(t), logits
+
+    def hidden(self) -> np.ndarray:
+        out = np.empty(self.hidden_size, np.float32)
+        _elib().spbo_engine_hidden(self._e, _p(out))
+        return out
+
+    def generate(self, prompt, n_new: int, eos: int = -1):
+        """Greedy generation with the convention of src/main.cpp:133-155."""
+        self.reset()
+        for t in prompt[:-1]:
+            self.step(t)
+        tok = prompt[-1]
+        out = []
+        for _ in range(n_new):
+            tok, _ = self.step(tok)
+            out.append(tok)
+            if tok == eos:
+                break
+        return out
+

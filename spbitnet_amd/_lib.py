@@ -42,8 +42,43 @@ SIGNATURES = {
     "spb_sparse_ternary_gemv_planes": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "spb_fused_sparse_bitlinear_planes_f16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
     "spb_fused_sparse_bitlinear_planes_bf16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
+    # decode engine (structs passed by pointer)
+    "spb_engine_create": [_P, _P, _P, _P, _P, _I, _P],
+    "spb_engine_destroy": [_P],
+    "spb_engine_set_stream": [_P, _P],
+    "spb_engine_reset": [_P],
+    "spb_engine_forward": [_P, _I, _P],
+    "spb_engine_seq_len": [_P],
+    "spb_engine_generate": [_P, _P, _I, _I, _I, _P, _P],
+    "spb_engine_decode_steps": [_P, _I],
+    "spb_engine_buffers": [_P, _P, _P],
+    "spb_generate_sparse_ternary": [ctypes.c_uint64, _I, _I, _P, _P, _I, _I, _P, _P, _P],
+    "spb_generate_normal_bf16": [ctypes.c_uint64, ctypes.c_long, _F, _P, _P],
 }
 _RESTYPES = {"spb_last_error_string": ctypes.c_char_p}
+
+
+class SparseLinearC(ctypes.Structure):
+    """spb_sparse_linear (include/spbitnet_amd.h)."""
+    _fields_ = [("meta", _P), ("values", _P), ("gamma", _F), ("rows", _I), ("cols", _I),
+                ("meta_stride", _I), ("values_stride", _I)]
+
+
+class TransformerLayerC(ctypes.Structure):
+    """spb_transformer_layer (include/spbitnet_amd.h)."""
+    _fields_ = [(n, SparseLinearC) for n in
+                ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")] + \
+               [("input_layernorm", _P), ("post_attention_layernorm", _P),
+                ("attn_sub_norm", _P), ("ffn_sub_norm", _P)]
+
+
+class ModelConfigC(ctypes.Structure):
+    """spb_model_config (include/spbitnet_amd.h)."""
+    _fields_ = [(n, _I) for n in ("hidden_size", "num_hidden_layers", "num_attention_heads",
+                                  "num_key_value_heads", "intermediate_size", "vocab_size",
+                                  "max_position_embeddings", "head_dim")] + \
+               [("rms_norm_eps", _F), ("rope_theta", _F), ("bos_token_id", _I),
+                ("eos_token_id", _I)]
 
 _lib = None
 
@@ -72,3 +107,19 @@ def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load().spb_last_error_string() or b""
         raise SpbError(f"{what} failed with status {rc}: {msg.decode(errors='replace')}")
+
+
+_hip = None
+
+
+def memcpy_d2d(dst: int, src: int, nbytes: int, stream) -> None:
+    """Device-to-device copy on `stream` through the HIP runtime torch loaded."""
+    global _hip
+    if _hip is None:
+        path = os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so")
+        _hip = ctypes.CDLL(path if os.path.exists(path) else "libamdhip64.so")
+        _hip.hipMemcpyAsync.argtypes = [_P, _P, ctypes.c_size_t, _I, _P]
+        _hip.hipMemcpyAsync.restype = _I
+    rc = _hip.hipMemcpyAsync(dst, src, nbytes, 3, stream)  # 3 = hipMemcpyDeviceToDevice
+    if rc != 0:
+        raise SpbError(f"hipMemcpyAsync failed with status {rc}")

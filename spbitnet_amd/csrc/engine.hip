@@ -1,0 +1,1068 @@
+// engine.hip -- bs=1 greedy decode of a BitNet b1.58 (2:4 sparse-ternary)
+// transformer on gfx950, as one HIP graph per token.
+//
+// Dataflow and semantics follow the reference engine, InferenceEngine::forward
+// (src/inference.cu:126-283), with bf16 activations / KV cache and the layer
+// order:
+//   x = embed[tok]
+//   per layer: r = x; h = RMSNorm(r; input_ln); q,k,v = BitLinear(h);
+//              RoPE(q, k); cache k, v; a = softmax(q k^T / sqrt(hd)) v;
+//              o = BitLinear(a); o = RMSNorm(o; attn_sub_norm); x = o + r;
+//              r = x; h = RMSNorm(x; post_ln); g,u = BitLinear(h);
+//              m = relu(g)^2 * u (fp32); m = RMSNorm_f32in(m; ffn_sub_norm);
+//              d = BitLinear(m); x = d + r
+//   logits = lm_head . RMSNorm(x; final_norm);  next = argmax(logits)
+//
+// Kernels per layer (the reference launches ~25; here 5):
+//   qkv     bit-plane GEMV over the stacked q/k/v matrices; its prologue
+//           does the embedding lookup (layer 0), input RMSNorm, absmax and
+//           int8 quantisation straight into LDS bit planes; its epilogue
+//           dequantises each projection with its own gamma.
+//   attn    RoPE of q and k, KV-cache write, and split-KV GQA attention
+//           (one block per (kv head, 256-position split)).
+//   o       GEMV; prologue combines the attention splits, absmax, quantise.
+//   gate_up GEMV over stacked gate/up; prologue = attn sub-norm, residual add
+//           (block 0 stores the new residual), post-attention RMSNorm,
+//           absmax, quantise.
+//   down    GEMV; prologue = relu^2 * up in fp32, ffn sub-norm, absmax,
+//           quantise; epilogue = dequantise + residual add.
+// and one LM-head kernel: final RMSNorm, bf16 GEMV to fp32 logits, argmax
+// (last-block reduction), and the token/position update in device memory, so
+// a whole greedy generation is graph replays with no host round trip.
+//
+// Every floating-point reduction has a fixed order (listed at each helper), so
+// the CPU oracle in oracle/ reproduces the logits bit for bit.
+#include <cmath>
+#include <new>
+#include <vector>
+
+#include "bitplane.hpp"
+#include "spbitnet_amd.h"
+
+namespace spb {
+namespace {
+
+constexpr int kAttnChunk = 256;  // positions per attention split = threads per attention block
+constexpr int kAttnMaxGroup = 8;  // q heads per kv head
+constexpr int kAttnMaxHd = 128;   // head_dim limit (even)
+constexpr int kLmBlock = 256;
+constexpr int kLmMaxH = 8192;
+
+struct EngineState {
+    int pos;         // position of the token the next step processes
+    int prompt_len;  // tokens[0 .. prompt_len) are given, later ones generated
+    int limit;       // positions available (KV capacity and token buffer)
+    int done;        // set by EOS (when stop_eos) or when the limit is reached
+    int stop_eos;
+    int eos;
+    unsigned ticket;  // LM-head blocks finished in the current step
+    int generated;
+};
+
+// ---- fixed-order arithmetic shared with the oracle ------------------------------
+
+__device__ __forceinline__ float bf16r(float f) { return BF16::to_float(BF16::from_float(f)); }
+
+// Butterfly sum over the 64 lanes: at distance d = 32, 16, ..., 1 every lane
+// adds its partner's value (lane ^ d).  Each pair computes the same sum, so
+// all lanes finish with identical bits.
+__device__ __forceinline__ float wave_sum_bfly(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Sum over a block of kThreads threads: the wave butterfly, then the wave
+// totals added in wave order (w0 + w1) + w2 ...  red: kThreads/64 floats of
+// LDS.  Every thread returns the same value.
+template <int kThreads>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum_bfly(v);
+    __syncthreads();  // red may still be read by a previous reduction
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / kWave; ++w) s += red[w];
+    return s;
+}
+
+template <int kThreads>
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / kWave; ++w) s = __builtin_fmaxf(s, red[w]);
+    return s;
+}
+
+// exp(x) for x <= 0 (softmax weights): Cody-Waite reduction x = n ln2 + r,
+// |r| <= ln2/2, degree-7 Taylor polynomial in Horner form with fused
+// multiply-adds, scaled by 2^n.  Results below ~2^-124 are returned as 0.
+// Error < 2 ulp against exp.
+__device__ __forceinline__ float exp_neg(float x) {
+    if (!(x >= -86.0f)) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.42860682030941723e-6f, r);
+    float p = 1.98412698412698413e-4f;
+    p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
+    p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
+    p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
+    p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, static_cast<int>(n));
+}
+
+// 1 / sqrt(ss / n + eps) with correctly rounded divide and square root
+// (the reference uses rsqrtf, inference_kernels.cu:50).
+__device__ __forceinline__ float inv_rms(float ss, int n, float eps) {
+    return 1.0f / __builtin_sqrtf(ss / static_cast<float>(n) + eps);
+}
+
+// ---- GEMV prologues: engine activations -> int8 bit planes ---------------------
+
+// Quantising source over a float vector in LDS (values already bf16-rounded).
+struct LdsQuantSrc {
+    const float* v;
+    float scale;
+    __device__ uint32_t q8(float f) const {
+        return static_cast<uint32_t>(quant_round_clamp(f * scale)) & 0xFFu;
+    }
+    __device__ void load8(int c0, uint32_t& lo, uint32_t& hi) const {
+        const float4 a = *reinterpret_cast<const float4*>(v + c0);
+        const float4 b = *reinterpret_cast<const float4*>(v + c0 + 4);
+        lo = q8(a.x) | (q8(a.y) << 8) | (q8(a.z) << 16) | (q8(a.w) << 24);
+        hi = q8(b.x) | (q8(b.y) << 8) | (q8(b.z) << 16) | (q8(b.w) << 24);
+    }
+};
+
+// P::fill(vec, n, tid, red) writes the GEMV input (bf16-rounded, as float) to
+// vec[0..n); then absmax (reference absmax_reduce, inference_kernels.cu:120-148)
+// and the quantised bit planes.  Every block of the launch computes the same
+// values (same inputs, same order).
+template <class P>
+struct ProducerPlanes {
+    P p;
+    const EngineState* st;
+    float amax;
+    static size_t extra_lds(int cols) { return static_cast<size_t>(cols) * 4 + 64; }
+    __device__ bool skip() const { return st->done != 0; }
+    __device__ void offset(long) {}
+    __device__ void prepare() {}
+    __device__ void build(uint32_t* planes, int cols, int tid, float* scratch) {
+        float* vec = scratch;
+        float* red = scratch + cols;
+        p.fill(vec, cols, tid, red, st);
+        __syncthreads();
+        float m = 0.0f;
+        for (int i = tid; i < cols; i += kBlock) m = __builtin_fmaxf(m, __builtin_fabsf(vec[i]));
+        amax = block_max<kBlock>(m, red);
+        BuildPlanes<LdsQuantSrc>{LdsQuantSrc{vec, quant_scale(amax)}}.build(planes, cols, tid,
+                                                                            nullptr);
+    }
+    __device__ float absmax() const { return amax; }
+};
+
+// Layer input: x (or, in layer 0, the embedding row of tokens[pos], which
+// block 0 also stores to x_out as the residual stream), then RMSNorm.
+// Reference: inference.cu:134-138, 147-153; rms_norm_kernel
+// (inference_kernels.cu:15-56): y = bf16((x * inv) * w).
+struct InputNorm {
+    const uint16_t* x;
+    const uint16_t* embed;  // non-null in layer 0
+    const int* tokens;
+    uint16_t* x_out;
+    const float* w;
+    float eps;
+    __device__ void fill(float* vec, int n, int tid, float* red, const EngineState* st) const {
+        const uint16_t* src = x;
+        if (embed) src = embed + static_cast<long>(tokens[st->pos]) * n;
+        float ss = 0.0f;
+        for (int i = tid; i < n; i += kBlock) {
+            const float v = BF16::to_float(src[i]);
+            vec[i] = v;
+            ss = __builtin_fmaf(v, v, ss);
+        }
+        if (embed && blockIdx.x == 0)
+            for (int i = tid; i < n; i += kBlock) x_out[i] = src[i];
+        const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
+        for (int i = tid; i < n; i += kBlock) vec[i] = bf16r((vec[i] * inv) * w[i]);
+    }
+};
+
+// Attention output: combine the splits of every head,
+//   M = max_s m_s, w_s = exp(m_s - M), out = (sum_s w_s acc_s) / (sum_s w_s l_s)
+// (s ascending, fused multiply-adds), rounded to bf16.
+struct AttnCombine {
+    const float* pm;    // [nh][S]
+    const float* pl;    // [nh][S]
+    const float* pacc;  // [nh][S][hd]
+    int hd, S;
+    __device__ void fill(float* vec, int n, int tid, float*, const EngineState* st) const {
+        const int ns = (st->pos + kAttnChunk) / kAttnChunk;  // splits holding positions 0..pos
+        for (int i = tid; i < n; i += kBlock) {
+            const int h = i / hd, d = i - h * hd;
+            const float* m = pm + h * S;
+            float M = m[0];
+            for (int s = 1; s < ns; ++s) M = __builtin_fmaxf(M, m[s]);
+            float l = 0.0f, a = 0.0f;
+            for (int s = 0; s < ns; ++s) {
+                const float w = exp_neg(m[s] - M);
+                l = __builtin_fmaf(w, pl[h * S + s], l);
+                a = __builtin_fmaf(w, pacc[(static_cast<long>(h) * S + s) * hd + d], a);
+            }
+            vec[i] = bf16r(a / l);
+        }
+    }
+};
+
+// gate/up input: o = RMSNorm(o; attn_sub_norm) (skipped when absent),
+// x = bf16(o + r) (block 0 stores it as the new residual), then
+// RMSNorm(x; post_attention_layernorm).  Reference inference.cu:205-230.
+struct SubNormResidualNorm {
+    const uint16_t* o;
+    const uint16_t* res;
+    uint16_t* x_out;
+    const float* w_sub;
+    const float* w_post;
+    float eps;
+    __device__ void fill(float* vec, int n, int tid, float* red, const EngineState*) const {
+        float ss = 0.0f;
+        for (int i = tid; i < n; i += kBlock) {
+            const float v = BF16::to_float(o[i]);
+            vec[i] = v;
+            ss = __builtin_fmaf(v, v, ss);
+        }
+        float inv = 1.0f;
+        if (w_sub) inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
+        float ss2 = 0.0f;
+        for (int i = tid; i < n; i += kBlock) {
+            const float on = w_sub ? bf16r((vec[i] * inv) * w_sub[i]) : vec[i];
+            const float x = bf16r(on + BF16::to_float(res[i]));
+            vec[i] = x;
+            ss2 = __builtin_fmaf(x, x, ss2);
+            if (blockIdx.x == 0) x_out[i] = BF16::from_float(x);
+        }
+        const float inv2 = inv_rms(block_sum<kBlock>(ss2, red), n, eps);
+        for (int i = tid; i < n; i += kBlock) vec[i] = bf16r((vec[i] * inv2) * w_post[i]);
+    }
+};
+
+// down input: m = (relu(g) * relu(g)) * u in fp32 (relu2_mul_f32_kernel,
+// inference_kernels.cu:399-410), then RMSNorm_f32in(m; ffn_sub_norm)
+// (:418-455) or a plain bf16 rounding when the norm is absent (:460-466).
+struct Relu2Norm {
+    const uint16_t* g;
+    const uint16_t* u;
+    const float* w;
+    float eps;
+    __device__ void fill(float* vec, int n, int tid, float* red, const EngineState*) const {
+        float ss = 0.0f;
+        for (int i = tid; i < n; i += kBlock) {
+            const float r = __builtin_fmaxf(0.0f, BF16::to_float(g[i]));
+            const float m = (r * r) * BF16::to_float(u[i]);
+            vec[i] = m;
+            ss = __builtin_fmaf(m, m, ss);
+        }
+        if (w) {
+            const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
+            for (int i = tid; i < n; i += kBlock) vec[i] = bf16r((vec[i] * inv) * w[i]);
+        } else {
+            for (int i = tid; i < n; i += kBlock) vec[i] = bf16r(vec[i]);
+        }
+    }
+};
+
+// ---- GEMV epilogues ----------------------------------------------------------------
+
+// bf16 outputs of up to three stacked projections, each dequantised with its
+// own gamma: out[r] = bf16(float(acc) * ((gamma_s * absmax) / 127)).
+struct SegBf16Sink {
+    uint16_t* out;
+    float g0, g1, g2;
+    int end0, end1;
+    float dq0, dq1, dq2;
+    __device__ void offset(long) {}
+    __device__ void prepare() {}
+    template <class A>
+    __device__ void bind(const A& a) {
+        const float m = a.absmax();
+        dq0 = dequant_scale(g0, m);
+        dq1 = dequant_scale(g1, m);
+        dq2 = dequant_scale(g2, m);
+    }
+    __device__ void store(long r, int acc) const {
+        const float dq = r < end0 ? opaque(dq0) : (r < end1 ? opaque(dq1) : opaque(dq2));
+        out[r] = BF16::from_float(static_cast<float>(acc) * dq);
+    }
+};
+
+// down projection: x_out[r] = bf16(bf16(acc * dq) + res[r])
+// (inference.cu:256-262; residual_add_kernel, inference_kernels.cu:471-479).
+struct ResidualSink {
+    uint16_t* x_out;
+    const uint16_t* res;
+    float gamma;
+    float dq;
+    __device__ void offset(long) {}
+    __device__ void prepare() {}
+    template <class A>
+    __device__ void bind(const A& a) {
+        dq = dequant_scale(gamma, a.absmax());
+    }
+    __device__ void store(long r, int acc) const {
+        const float d = bf16r(static_cast<float>(acc) * dq);
+        x_out[r] = BF16::from_float(d + BF16::to_float(res[r]));
+    }
+};
+
+// ---- attention -----------------------------------------------------------------------
+
+// One block per (256-position split s, kv head): RoPE of the group's q heads
+// and (in the split holding pos) of k, KV-cache write of k and v at pos,
+// scores, per-split softmax numerator and the unnormalised weighted sum of V.
+//   score_j = (sum over lanes l of fma(q[2l+1], k[2l+1], q[2l] * k[2l]),
+//              butterfly order) * scale
+//   m = max_j score_j, e_j = exp(score_j - m), l = block_sum(e) (thread t
+//   holds position j0 + t), acc[d] = sum_j e_j v_j[d] (j ascending, fma).
+// rope: [max_seq][hd/2] (cos, sin) of angle pos * theta^(-2i/hd).
+// Reference: rope_kernel, scatter_kv, attention_scores, softmax,
+// attention_output (inference_kernels.cu:185-371), GQA kv = h * nkv / nh.
+__global__ __launch_bounds__(kAttnChunk) void attention_kernel(
+    const uint16_t* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    const float2* __restrict__ rope, float* __restrict__ pm, float* __restrict__ pl,
+    float* __restrict__ pacc, const EngineState* __restrict__ st, int nh, int nkv, int hd,
+    int max_seq, int S, float scale) {
+    __shared__ float qs[kAttnMaxGroup][kAttnMaxHd];
+    __shared__ float kn[kAttnMaxHd], vn[kAttnMaxHd];
+    __shared__ float sc[kAttnMaxGroup][kAttnChunk];
+    __shared__ float red[kAttnChunk / kWave];
+    if (st->done) return;
+    const int pos = st->pos;
+    const int s = blockIdx.x, kvh = blockIdx.y;
+    const int j0 = s * kAttnChunk;
+    if (j0 > pos) return;
+    const int jn = (pos + 1 - j0) < kAttnChunk ? (pos + 1 - j0) : kAttnChunk;
+    const bool has_pos = j0 + jn - 1 == pos;
+    const int G = nh / nkv;
+    const int half = hd >> 1;
+    const int tid = threadIdx.x;
+    const float2* rp = rope + static_cast<long>(pos) * half;
+
+    for (int idx = tid; idx < G * half; idx += kAttnChunk) {
+        const int g = idx / half, i = idx - g * half;
+        const uint16_t* qh = qkv + (kvh * G + g) * hd;
+        const float x0 = BF16::to_float(qh[2 * i]), x1 = BF16::to_float(qh[2 * i + 1]);
+        const float2 cs = rp[i];
+        qs[g][2 * i] = bf16r(x0 * cs.x - x1 * cs.y);
+        qs[g][2 * i + 1] = bf16r(x0 * cs.y + x1 * cs.x);
+    }
+    if (has_pos) {
+        const uint16_t* kh = qkv + nh * hd + kvh * hd;
+        const uint16_t* vh = qkv + (nh + nkv) * hd + kvh * hd;
+        const long at = (static_cast<long>(kvh) * max_seq + pos) * hd;
+        for (int i = tid; i < half; i += kAttnChunk) {
+            const float x0 = BF16::to_float(kh[2 * i]), x1 = BF16::to_float(kh[2 * i + 1]);
+            const float2 cs = rp[i];
+            const uint16_t k0 = BF16::from_float(x0 * cs.x - x1 * cs.y);
+            const uint16_t k1 = BF16::from_float(x0 * cs.y + x1 * cs.x);
+            kn[2 * i] = BF16::to_float(k0);
+            kn[2 * i + 1] = BF16::to_float(k1);
+            kc[at + 2 * i] = k0;
+            kc[at + 2 * i + 1] = k1;
+        }
+        for (int d = tid; d < hd; d += kAttnChunk) {
+            vn[d] = BF16::to_float(vh[d]);
+            vc[at + d] = vh[d];
+        }
+    }
+    __syncthreads();
+
+    // scores: wave w takes positions j0 + w, j0 + w + 4, ...; lane l dims 2l, 2l+1
+    const int lane = tid & (kWave - 1), wave = tid / kWave;
+    const bool lane_on = 2 * lane < hd;
+    for (int jj = wave; jj < jn; jj += kAttnChunk / kWave) {
+        const int j = j0 + jj;
+        float k0 = 0.0f, k1 = 0.0f;
+        if (lane_on) {
+            if (j == pos) {
+                k0 = kn[2 * lane];
+                k1 = kn[2 * lane + 1];
+            } else {
+                const uint32_t kk = *reinterpret_cast<const uint32_t*>(
+                    kc + (static_cast<long>(kvh) * max_seq + j) * hd + 2 * lane);
+                k0 = BF16::to_float(static_cast<uint16_t>(kk & 0xFFFFu));
+                k1 = BF16::to_float(static_cast<uint16_t>(kk >> 16));
+            }
+        }
+        for (int g = 0; g < G; ++g) {
+            float p = lane_on ? __builtin_fmaf(qs[g][2 * lane + 1], k1, qs[g][2 * lane] * k0) : 0.0f;
+            p = wave_sum_bfly(p);
+            if (lane == 0) sc[g][jj] = p * scale;
+        }
+    }
+    __syncthreads();
+
+    __shared__ float hmax[kAttnMaxGroup], hsum[kAttnMaxGroup];
+    for (int g = 0; g < G; ++g) {
+        const float v = tid < jn ? sc[g][tid] : -INFINITY;
+        const float m = block_max<kAttnChunk>(v, red);
+        const float e = tid < jn ? exp_neg(v - m) : 0.0f;
+        const float l = block_sum<kAttnChunk>(e, red);
+        if (tid < jn) sc[g][tid] = e;
+        if (tid == 0) {
+            hmax[g] = m;
+            hsum[g] = l;
+        }
+    }
+    __syncthreads();
+
+    for (int o = tid; o < G * hd; o += kAttnChunk) {
+        const int g = o / hd, d = o - g * hd;
+        const uint16_t* vcol = vc + static_cast<long>(kvh) * max_seq * hd + d;
+        float acc = 0.0f;
+        for (int jj = 0; jj < jn; ++jj) {
+            const int j = j0 + jj;
+            const float v = j == pos ? vn[d] : BF16::to_float(vcol[static_cast<long>(j) * hd]);
+            acc = __builtin_fmaf(sc[g][jj], v, acc);
+        }
+        const int h = kvh * G + g;
+        pacc[(static_cast<long>(h) * S + s) * hd + d] = acc;
+        if (d == 0) {
+            pm[h * S + s] = hmax[g];
+            pl[h * S + s] = hsum[g];
+        }
+    }
+}
+
+// ---- LM head + greedy argmax ------------------------------------------------------------
+
+// Final RMSNorm (block-sum order over kLmBlock threads), then
+// logits[r] = sum_c W[r][c] * xn[c] in fp32: lane l of the row's wave takes
+// the 8-element chunks l, l+64, ... (fma in element order), then the
+// butterfly.  Argmax = lowest index among the maxima (std::max_element,
+// src/main.cpp:194-200).  The last block to finish reduces the per-block
+// maxima and advances the decode state.  Reference half_gemv_kernel
+// (inference_kernels.cu:488-531) with fp16 -> bf16 weights.
+__global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
+    const float* __restrict__ wn, float eps, float* __restrict__ logits,
+    float* __restrict__ part_v, int* __restrict__ part_i, EngineState* __restrict__ st,
+    int* __restrict__ tokens, int V, int H) {
+    __shared__ float xs[kLmMaxH];
+    __shared__ float red[kLmBlock / kWave];
+    __shared__ float wv[kLmBlock / kWave];
+    __shared__ int wi[kLmBlock / kWave];
+    __shared__ int last;
+    if (st->done) return;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+
+    float ss = 0.0f;
+    for (int i = tid; i < H; i += kLmBlock) {
+        const float v = BF16::to_float(x[i]);
+        xs[i] = v;
+        ss = __builtin_fmaf(v, v, ss);
+    }
+    const float inv = inv_rms(block_sum<kLmBlock>(ss, red), H, eps);
+    for (int i = tid; i < H; i += kLmBlock) xs[i] = bf16r((xs[i] * inv) * wn[i]);
+    __syncthreads();
+
+    const int nch = H >> 3;
+    const long waves = static_cast<long>(gridDim.x) * (kLmBlock / kWave);
+    float best = -INFINITY;
+    int best_i = 0x7FFFFFFF;
+    for (long r = static_cast<long>(blockIdx.x) * (kLmBlock / kWave) + wave; r < V; r += waves) {
+        const uint4* wr = reinterpret_cast<const uint4*>(W + r * H);
+        float acc = 0.0f;
+        for (int c = lane; c < nch; c += kWave) {
+            const uint4 w = wr[c];
+            const float* xv = xs + 8 * c;
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                acc = __builtin_fmaf(BF16::to_float(static_cast<uint16_t>(ww[k] & 0xFFFFu)),
+                                     xv[2 * k], acc);
+                acc = __builtin_fmaf(BF16::to_float(static_cast<uint16_t>(ww[k] >> 16)),
+                                     xv[2 * k + 1], acc);
+            }
+        }
+        acc = wave_sum_bfly(acc);
+        if (lane == 0) logits[r] = acc;
+        if (acc > best) {  // rows ascend within a wave: strict > keeps the first maximum
+            best = acc;
+            best_i = static_cast<int>(r);
+        }
+    }
+    if (lane == 0) {
+        wv[wave] = best;
+        wi[wave] = best_i;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float b = wv[0];
+        int bi = wi[0];
+        for (int w = 1; w < kLmBlock / kWave; ++w)
+            if (wv[w] > b || (wv[w] == b && wi[w] < bi)) {
+                b = wv[w];
+                bi = wi[w];
+            }
+        part_v[blockIdx.x] = b;
+        part_i[blockIdx.x] = bi;
+        __threadfence();
+        const unsigned t = atomicAdd(&st->ticket, 1u);
+        last = t == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    float b = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int k = tid; k < static_cast<int>(gridDim.x); k += kLmBlock) {
+        const float v = __hip_atomic_load(&part_v[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int i = __hip_atomic_load(&part_i[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (v > b || (v == b && i < bi)) {
+            b = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(b, off, kWave);
+        const int oi = __shfl_xor(bi, off, kWave);
+        if (ov > b || (ov == b && oi < bi)) {
+            b = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        wv[wave] = b;
+        wi[wave] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kLmBlock / kWave; ++w)
+            if (wv[w] > b || (wv[w] == b && wi[w] < bi)) {
+                b = wv[w];
+                bi = wi[w];
+            }
+        const int tok = bi == 0x7FFFFFFF ? 0 : bi;  // all-NaN logits: token 0
+        const int nxt = st->pos + 1;
+        if (nxt >= st->prompt_len && nxt < st->limit) {
+            tokens[nxt] = tok;
+            st->generated += 1;
+            if (st->stop_eos && tok == st->eos) st->done = 1;
+        }
+        st->pos = nxt;
+        if (nxt >= st->limit) st->done = 1;
+        st->ticket = 0u;
+    }
+}
+
+// ---- random-init weights (model generation on the device) ------------------------
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// N(0,1) float from the counter (seed, i): Box-Muller on two 24-bit uniforms.
+__device__ __forceinline__ float normal_at(uint64_t seed, uint64_t i) {
+    const uint64_t z = splitmix64(seed ^ splitmix64(i));
+    const float u1 = (static_cast<float>(z >> 40) + 1.0f) * (1.0f / 16777216.0f);
+    const float u2 = static_cast<float>((z >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958648f * u2);
+}
+
+constexpr int kGenBlocks = 1024;
+__device__ double g_gen_partial[kGenBlocks];
+
+// One thread per 64 columns of a row: latent W ~ N(0,1), 2:4 top-2 |W| mask
+// (higher index wins ties), kept value sign(W) (W >= 0 -> +1), packed
+// (python/convert_model.py:88-207, 257-316).  Per-block sums of |W| in double
+// feed gamma = mean|W|.
+__global__ __launch_bounds__(256) void gen_sparse_ternary_kernel(uint64_t seed, int rows,
+                                                                 int cols, uint32_t* meta,
+                                                                 uint32_t* values, int ms,
+                                                                 int vs, float* latent) {
+    __shared__ double part[256 / kWave];
+    const long units = static_cast<long>(rows) * (cols / 64);
+    double sum = 0.0;
+    for (long u = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; u < units;
+         u += static_cast<long>(gridDim.x) * 256) {
+        const long r = u / (cols / 64);
+        const int c0 = static_cast<int>(u - r * (cols / 64)) * 64;
+        uint32_t mw[2] = {0u, 0u}, sw = 0u;
+        for (int g = 0; g < 16; ++g) {
+            float w[4];
+            for (int i = 0; i < 4; ++i) {
+                const long idx = r * cols + c0 + 4 * g + i;
+                w[i] = normal_at(seed, static_cast<uint64_t>(idx));
+                sum += fabs(static_cast<double>(w[i]));
+                if (latent) latent[idx] = w[i];
+            }
+            uint32_t bm = 0u, sg = 0u;
+            int kept = 0;
+            for (int i = 0; i < 4; ++i) {
+                int beaten = 0;
+                for (int j = 0; j < 4; ++j) {
+                    if (j == i) continue;
+                    const float ai = fabsf(w[i]), aj = fabsf(w[j]);
+                    if (aj > ai || (aj == ai && j > i)) ++beaten;
+                }
+                if (beaten < 2) {
+                    bm |= 1u << i;
+                    if (w[i] < 0.0f) sg |= 1u << kept;  // bit 0: lower kept, bit 1: higher
+                    ++kept;
+                }
+            }
+            mw[g >> 3] |= bm << (4 * (g & 7));
+            sw |= sg << (2 * g);
+        }
+        const int w0 = c0 / 32;
+        meta[r * ms + w0] = mw[0];
+        meta[r * ms + w0 + 1] = mw[1];
+        values[r * vs + c0 / 64] = sw;
+    }
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) g_gen_partial[blockIdx.x] = ((part[0] + part[1]) + part[2]) + part[3];
+}
+
+__global__ void gen_gamma_kernel(int nblocks, double count, float* gamma) {
+    double s = 0.0;
+    for (int b = 0; b < nblocks; ++b) s += g_gen_partial[b];
+    *gamma = static_cast<float>(s / count);
+}
+
+__global__ __launch_bounds__(256) void gen_normal_bf16_kernel(uint64_t seed, long n, float std_,
+                                                              uint16_t* out) {
+    for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<long>(gridDim.x) * 256)
+        out[i] = BF16::from_float(normal_at(seed, static_cast<uint64_t>(i)) * std_);
+}
+
+// ---- host side ------------------------------------------------------------------------
+
+bool aligned_to(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+template <class T>
+T* dev_alloc(size_t n, std::vector<void*>& owned) {
+    void* p = nullptr;
+    if (hipMalloc(&p, n * sizeof(T) < 16 ? 16 : n * sizeof(T)) != hipSuccess) return nullptr;
+    owned.push_back(p);
+    return static_cast<T*>(p);
+}
+
+SegWeights seg_weights(const spb_sparse_linear* a, const spb_sparse_linear* b,
+                       const spb_sparse_linear* c) {
+    const spb_sparse_linear* L2 = c ? c : b;
+    SegWeights w{};
+    w.meta = a->meta;
+    w.values = a->values;
+    w.dm1 = b->meta - a->meta;
+    w.dm2 = L2->meta - b->meta;
+    w.dv1 = b->values - a->values;
+    w.dv2 = L2->values - b->values;
+    w.ms = a->meta_stride;
+    w.vs = a->values_stride;
+    w.dms1 = b->meta_stride - a->meta_stride;
+    w.dms2 = L2->meta_stride - b->meta_stride;
+    w.dvs1 = b->values_stride - a->values_stride;
+    w.dvs2 = L2->values_stride - b->values_stride;
+    w.end0 = a->rows;
+    w.rows = a->rows + b->rows + (c ? c->rows : 0);
+    w.end1 = c ? a->rows + b->rows : w.rows;
+    w.cols = a->cols;
+    return w;
+}
+
+Weights single_weights(const spb_sparse_linear& l) {
+    return Weights{l.meta, l.values, l.rows, l.cols, l.meta_stride, l.values_stride};
+}
+
+}  // namespace
+}  // namespace spb
+
+using namespace spb;
+
+struct spb_engine {
+    spb_model_config cfg{};
+    std::vector<spb_transformer_layer> layers;
+    const uint16_t* embed = nullptr;
+    const uint16_t* lm_head = nullptr;
+    const float* final_norm = nullptr;
+    int max_seq = 0;
+    int S = 0;  // attention splits
+    int lm_grid = 0;
+    std::vector<void*> owned;
+    std::vector<uint16_t*> kcache, vcache;
+    uint16_t *xa = nullptr, *xb = nullptr, *qkv = nullptr, *obuf = nullptr, *gu = nullptr;
+    float *pm = nullptr, *pl = nullptr, *pacc = nullptr, *logits = nullptr, *part_v = nullptr;
+    int* part_i = nullptr;
+    int* tokens = nullptr;
+    float2* rope = nullptr;
+    EngineState* st = nullptr;
+    hipStream_t stream = nullptr;      // where graphs are launched (null = legacy stream)
+    hipStream_t cap_stream = nullptr;  // capture stream
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int seq_len = 0;
+
+    ~spb_engine() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (cap_stream) (void)hipStreamDestroy(cap_stream);
+        for (void* p : owned) (void)hipFree(p);
+    }
+
+    // The kernels of one token step, in order, on stream s.
+    void enqueue_step(hipStream_t s) const {
+        const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
+        const int nkv = cfg.num_key_value_heads;
+        const float eps = cfg.rms_norm_eps;
+        const float scale = 1.0f / sqrtf(static_cast<float>(hd));  // inference.cu:182
+        for (size_t l = 0; l < layers.size(); ++l) {
+            const spb_transformer_layer& L = layers[l];
+            {
+                InputNorm p{xa, l == 0 ? embed : nullptr, tokens, xa, L.input_layernorm, eps};
+                SegBf16Sink sink{qkv, L.q_proj.gamma, L.k_proj.gamma, L.v_proj.gamma,
+                                 L.q_proj.rows, L.q_proj.rows + L.k_proj.rows, 0.f, 0.f, 0.f};
+                launch_bitplane(seg_weights(&L.q_proj, &L.k_proj, &L.v_proj),
+                                ProducerPlanes<InputNorm>{p, st, 0.f}, sink, s);
+            }
+            hipLaunchKernelGGL(attention_kernel, dim3(S, nkv), dim3(kAttnChunk), 0, s, qkv,
+                               kcache[l], vcache[l], rope, pm, pl, pacc, st, nh, nkv, hd, max_seq,
+                               S, scale);
+            {
+                AttnCombine p{pm, pl, pacc, hd, S};
+                SegBf16Sink sink{obuf, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma,
+                                 L.o_proj.rows, L.o_proj.rows, 0.f, 0.f, 0.f};
+                launch_bitplane(single_weights(L.o_proj), ProducerPlanes<AttnCombine>{p, st, 0.f},
+                                sink, s);
+            }
+            {
+                SubNormResidualNorm p{obuf, xa, xb, L.attn_sub_norm, L.post_attention_layernorm,
+                                      eps};
+                SegBf16Sink sink{gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
+                                 L.gate_proj.rows, L.gate_proj.rows + L.up_proj.rows, 0.f, 0.f,
+                                 0.f};
+                launch_bitplane(seg_weights(&L.gate_proj, &L.up_proj, nullptr),
+                                ProducerPlanes<SubNormResidualNorm>{p, st, 0.f}, sink, s);
+            }
+            {
+                const int I = cfg.intermediate_size;
+                Relu2Norm p{gu, gu + I, L.ffn_sub_norm, eps};
+                ResidualSink sink{xa, xb, L.down_proj.gamma, 0.f};
+                launch_bitplane(single_weights(L.down_proj), ProducerPlanes<Relu2Norm>{p, st, 0.f},
+                                sink, s);
+            }
+        }
+        hipLaunchKernelGGL(lm_head_kernel, dim3(lm_grid), dim3(kLmBlock), 0, s, lm_head, xa,
+                           final_norm, eps, logits, part_v, part_i, st, tokens,
+                           cfg.vocab_size, cfg.hidden_size);
+    }
+};
+
+namespace {
+
+int check_linear(const char* fn, const char* name, const spb_sparse_linear& l, int rows,
+                 int cols) {
+    if (l.rows != rows || l.cols != cols)
+        return invalid("%s: %s is %dx%d, expected %dx%d", fn, name, l.rows, l.cols, rows, cols);
+    if (!l.meta || !l.values) return invalid("%s: %s has null weights", fn, name);
+    if (!bitplane_ok(l.meta, l.values, l.cols, l.meta_stride, l.values_stride))
+        return invalid("%s: %s must have cols %% 128 == 0, cols <= %d, meta_stride %% 4 == 0, "
+                       "values_stride %% 2 == 0 and 16/8-byte aligned meta/values",
+                       fn, name, kMaxPlaneCols);
+    return 0;
+}
+
+int set_state(spb_engine* e, int pos, int prompt_len, int stop_eos) {
+    EngineState h{};
+    h.pos = pos;
+    h.prompt_len = prompt_len;
+    h.limit = e->max_seq;
+    h.done = 0;
+    h.stop_eos = stop_eos;
+    h.eos = e->cfg.eos_token_id;
+    h.ticket = 0u;
+    h.generated = 0;
+    // Synchronous with respect to the host: h lives on this stack frame.
+    if (hipMemcpyAsync(e->st, &h, sizeof(h), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
+        hipStreamSynchronize(e->stream) != hipSuccess)
+        return launch_status("spb_engine: state upload");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transformer_layer* layers,
+                                 const uint16_t* embed_tokens, const uint16_t* lm_head,
+                                 const float* final_norm, int max_seq, spb_engine** out) {
+    clear_error();
+    const char* fn = "spb_engine_create";
+    if (!cfg || !layers || !embed_tokens || !final_norm || !out)
+        return invalid("%s: null argument", fn);
+    *out = nullptr;
+    const int H = cfg->hidden_size, nh = cfg->num_attention_heads, nkv = cfg->num_key_value_heads;
+    const int hd = cfg->head_dim, I = cfg->intermediate_size, V = cfg->vocab_size;
+    if (cfg->num_hidden_layers <= 0 || H <= 0 || nh <= 0 || nkv <= 0 || hd <= 0 || I <= 0 ||
+        V <= 0)
+        return invalid("%s: non-positive model dimension", fn);
+    if (nh * hd != H) return invalid("%s: num_attention_heads * head_dim != hidden_size", fn);
+    if (nh % nkv || nh / nkv > kAttnMaxGroup)
+        return invalid("%s: heads per kv head must divide evenly and be <= %d", fn,
+                       kAttnMaxGroup);
+    if (hd % 2 || hd > kAttnMaxHd) return invalid("%s: head_dim must be even and <= %d", fn,
+                                                  kAttnMaxHd);
+    if (H > kLmMaxH || H % 8) return invalid("%s: hidden_size must be a multiple of 8, <= %d", fn,
+                                             kLmMaxH);
+    if (max_seq <= 0 || max_seq > cfg->max_position_embeddings)
+        return invalid("%s: max_seq must be in [1, max_position_embeddings]", fn);
+    if (!aligned_to(embed_tokens, 16) || (lm_head && !aligned_to(lm_head, 16)))
+        return invalid("%s: embedding / lm_head must be 16-byte aligned", fn);
+    const int kvdim = nkv * hd;
+    for (int l = 0; l < cfg->num_hidden_layers; ++l) {
+        const spb_transformer_layer& L = layers[l];
+        int rc = 0;
+        if ((rc = check_linear(fn, "q_proj", L.q_proj, H, H)) ||
+            (rc = check_linear(fn, "k_proj", L.k_proj, kvdim, H)) ||
+            (rc = check_linear(fn, "v_proj", L.v_proj, kvdim, H)) ||
+            (rc = check_linear(fn, "o_proj", L.o_proj, H, H)) ||
+            (rc = check_linear(fn, "gate_proj", L.gate_proj, I, H)) ||
+            (rc = check_linear(fn, "up_proj", L.up_proj, I, H)) ||
+            (rc = check_linear(fn, "down_proj", L.down_proj, H, I)))
+            return rc;
+        if (!L.input_layernorm || !L.post_attention_layernorm)
+            return invalid("%s: layer %d lacks its RMSNorm weights", fn, l);
+    }
+    spb_engine* e = new (std::nothrow) spb_engine();
+    if (!e) return invalid("%s: out of host memory", fn);
+    e->cfg = *cfg;
+    e->layers.assign(layers, layers + cfg->num_hidden_layers);
+    e->embed = embed_tokens;
+    e->lm_head = lm_head ? lm_head : embed_tokens;  // tied weights (model.h:131-133)
+    e->final_norm = final_norm;
+    e->max_seq = max_seq;
+    e->S = (max_seq + kAttnChunk - 1) / kAttnChunk;
+    int resident = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, lm_head_kernel, kLmBlock, 0) !=
+            hipSuccess ||
+        resident <= 0)
+        resident = 1;
+    const long lm_need = (static_cast<long>(V) + kLmBlock / kWave - 1) / (kLmBlock / kWave);
+    const long lm_res = static_cast<long>(resident) * device_cu_count();
+    e->lm_grid = static_cast<int>(lm_need < lm_res ? lm_need : lm_res);
+
+    auto& own = e->owned;
+    const size_t kv = static_cast<size_t>(nkv) * max_seq * hd;
+    bool ok = true;
+    for (int l = 0; l < cfg->num_hidden_layers && ok; ++l) {
+        e->kcache.push_back(dev_alloc<uint16_t>(kv, own));
+        e->vcache.push_back(dev_alloc<uint16_t>(kv, own));
+        ok = e->kcache.back() && e->vcache.back();
+    }
+    ok = ok && (e->xa = dev_alloc<uint16_t>(H, own)) && (e->xb = dev_alloc<uint16_t>(H, own)) &&
+         (e->qkv = dev_alloc<uint16_t>(H + 2 * kvdim, own)) &&
+         (e->obuf = dev_alloc<uint16_t>(H, own)) && (e->gu = dev_alloc<uint16_t>(2 * I, own)) &&
+         (e->pm = dev_alloc<float>(static_cast<size_t>(nh) * e->S, own)) &&
+         (e->pl = dev_alloc<float>(static_cast<size_t>(nh) * e->S, own)) &&
+         (e->pacc = dev_alloc<float>(static_cast<size_t>(nh) * e->S * hd, own)) &&
+         (e->logits = dev_alloc<float>(V, own)) &&
+         (e->part_v = dev_alloc<float>(e->lm_grid, own)) &&
+         (e->part_i = dev_alloc<int>(e->lm_grid, own)) &&
+         (e->tokens = dev_alloc<int>(max_seq + 1, own)) &&
+         (e->rope = dev_alloc<float2>(static_cast<size_t>(max_seq) * (hd / 2), own)) &&
+         (e->st = dev_alloc<EngineState>(1, own));
+    if (!ok) {
+        delete e;
+        return invalid("%s: device allocation failed", fn);
+    }
+    // RoPE table (inference_kernels.cu:195-198): freq_i = 1 / theta^(2i/hd) in
+    // float32, angle = float(pos) * freq_i, cos/sin evaluated in double.
+    std::vector<float2> rope(static_cast<size_t>(max_seq) * (hd / 2));
+    for (int p = 0; p < max_seq; ++p)
+        for (int i = 0; i < hd / 2; ++i) {
+            const float freq = 1.0f / powf(cfg->rope_theta,
+                                           static_cast<float>(2 * i) / static_cast<float>(hd));
+            const float angle = static_cast<float>(p) * freq;
+            rope[static_cast<size_t>(p) * (hd / 2) + i] =
+                make_float2(static_cast<float>(cos(static_cast<double>(angle))),
+                            static_cast<float>(sin(static_cast<double>(angle))));
+        }
+    hipError_t err = hipMemcpy(e->rope, rope.data(), rope.size() * sizeof(float2),
+                               hipMemcpyHostToDevice);
+    for (size_t l = 0; l < e->kcache.size() && err == hipSuccess; ++l) {
+        err = hipMemset(e->kcache[l], 0, kv * 2);
+        if (err == hipSuccess) err = hipMemset(e->vcache[l], 0, kv * 2);
+    }
+    if (err == hipSuccess) err = hipStreamCreateWithFlags(&e->cap_stream, hipStreamNonBlocking);
+    if (err != hipSuccess) {
+        delete e;
+        return launch_status(fn);
+    }
+    // Capture one token step.
+    err = hipStreamBeginCapture(e->cap_stream, hipStreamCaptureModeThreadLocal);
+    if (err == hipSuccess) {
+        e->enqueue_step(e->cap_stream);
+        err = hipStreamEndCapture(e->cap_stream, &e->graph);
+    }
+    if (err == hipSuccess) err = hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0);
+    if (err != hipSuccess) {
+        set_error("%s: graph capture failed: %s", fn, hipGetErrorString(err));
+        delete e;
+        return static_cast<int>(err);
+    }
+    if (int rc = set_state(e, 0, 0x7FFFFFFF, 0)) {
+        delete e;
+        return rc;
+    }
+    *out = e;
+    return 0;
+}
+
+extern "C" int spb_engine_destroy(spb_engine* e) {
+    clear_error();
+    if (e) {
+        (void)hipStreamSynchronize(e->stream);
+        delete e;
+    }
+    return 0;
+}
+
+extern "C" int spb_engine_set_stream(spb_engine* e, spb_stream_t stream) {
+    clear_error();
+    if (!e) return invalid("spb_engine_set_stream: null engine");
+    e->stream = as_stream(stream);
+    return 0;
+}
+
+extern "C" int spb_engine_reset(spb_engine* e) {
+    clear_error();
+    if (!e) return invalid("spb_engine_reset: null engine");
+    e->seq_len = 0;
+    const size_t kv = static_cast<size_t>(e->cfg.num_key_value_heads) * e->max_seq *
+                      e->cfg.head_dim * 2;
+    for (size_t l = 0; l < e->kcache.size(); ++l) {
+        if (hipMemsetAsync(e->kcache[l], 0, kv, e->stream) != hipSuccess ||
+            hipMemsetAsync(e->vcache[l], 0, kv, e->stream) != hipSuccess)
+            return launch_status("spb_engine_reset");
+    }
+    return set_state(e, 0, 0x7FFFFFFF, 0);
+}
+
+extern "C" int spb_engine_seq_len(const spb_engine* e) { return e ? e->seq_len : -1; }
+
+extern "C" int spb_engine_forward(spb_engine* e, int token_id, const float** d_logits) {
+    clear_error();
+    const char* fn = "spb_engine_forward";
+    if (!e) return invalid("%s: null engine", fn);
+    if (token_id < 0 || token_id >= e->cfg.vocab_size)
+        return invalid("%s: token %d outside [0, %d)", fn, token_id, e->cfg.vocab_size);
+    if (e->seq_len >= e->max_seq) return invalid("%s: sequence is full (%d)", fn, e->max_seq);
+    const int pos = e->seq_len;
+    if (hipMemcpyAsync(e->tokens + pos, &token_id, sizeof(int), hipMemcpyHostToDevice,
+                       e->stream) != hipSuccess)
+        return launch_status(fn);
+    // The host copy above is pageable: wait until it has been consumed.
+    if (hipStreamSynchronize(e->stream) != hipSuccess) return launch_status(fn);
+    if (hipGraphLaunch(e->exec, e->stream) != hipSuccess) return launch_status(fn);
+    e->seq_len = pos + 1;
+    if (d_logits) *d_logits = e->logits;
+    return 0;
+}
+
+extern "C" int spb_engine_generate(spb_engine* e, const int* prompt, int n_prompt, int n_new,
+                                   int stop_at_eos, int* out_tokens, int* n_generated) {
+    clear_error();
+    const char* fn = "spb_engine_generate";
+    if (!e || !prompt || (!out_tokens && n_new > 0)) return invalid("%s: null argument", fn);
+    if (n_prompt <= 0 || n_new < 0) return invalid("%s: need n_prompt >= 1, n_new >= 0", fn);
+    if (static_cast<long>(n_prompt) + n_new > e->max_seq)
+        return invalid("%s: prompt + new tokens (%d) exceed max_seq %d", fn, n_prompt + n_new,
+                       e->max_seq);
+    for (int i = 0; i < n_prompt; ++i)
+        if (prompt[i] < 0 || prompt[i] >= e->cfg.vocab_size)
+            return invalid("%s: prompt token %d outside [0, %d)", fn, prompt[i],
+                           e->cfg.vocab_size);
+    if (int rc = spb_engine_reset(e)) return rc;
+    if (hipMemcpyAsync(e->tokens, prompt, sizeof(int) * n_prompt, hipMemcpyHostToDevice,
+                       e->stream) != hipSuccess)
+        return launch_status(fn);
+    if (int rc = set_state(e, 0, n_prompt, stop_at_eos ? 1 : 0)) return rc;
+    // Steps 0 .. n_prompt-2 prefill; step n_prompt-1+t produces token t.
+    const int steps = n_prompt - 1 + n_new;
+    for (int i = 0; i < steps; ++i)
+        if (hipGraphLaunch(e->exec, e->stream) != hipSuccess) return launch_status(fn);
+    EngineState h{};
+    if (hipMemcpyAsync(&h, e->st, sizeof(h), hipMemcpyDeviceToHost, e->stream) != hipSuccess)
+        return launch_status(fn);
+    if (hipStreamSynchronize(e->stream) != hipSuccess) return launch_status(fn);
+    const int got = h.generated < n_new ? h.generated : n_new;
+    if (got > 0 && hipMemcpy(out_tokens, e->tokens + n_prompt, sizeof(int) * got,
+                             hipMemcpyDeviceToHost) != hipSuccess)
+        return launch_status(fn);
+    if (n_generated) *n_generated = got;
+    e->seq_len = h.pos;
+    return 0;
+}
+
+extern "C" int spb_engine_decode_steps(spb_engine* e, int steps) {
+    clear_error();
+    if (!e) return invalid("spb_engine_decode_steps: null engine");
+    for (int i = 0; i < steps; ++i)
+        if (hipGraphLaunch(e->exec, e->stream) != hipSuccess)
+            return launch_status("spb_engine_decode_steps");
+    return 0;
+}
+
+extern "C" int spb_engine_buffers(const spb_engine* e, const float** logits, const int** tokens) {
+    clear_error();
+    if (!e) return invalid("spb_engine_buffers: null engine");
+    if (logits) *logits = e->logits;
+    if (tokens) *tokens = e->tokens;
+    return 0;
+}
+
+extern "C" int spb_generate_sparse_ternary(uint64_t seed, int rows, int cols, uint32_t* meta,
+                                           uint32_t* values, int meta_stride, int values_stride,
+                                           float* d_gamma, float* latent, spb_stream_t stream) {
+    clear_error();
+    const char* fn = "spb_generate_sparse_ternary";
+    if (rows <= 0 || cols <= 0 || cols % 64) return invalid("%s: need rows > 0, cols %% 64 == 0", fn);
+    if (meta_stride < cols / 32 || values_stride < cols / 64)
+        return invalid("%s: strides smaller than the format requires", fn);
+    if (!meta || !values || !d_gamma) return invalid("%s: null pointer", fn);
+    const long units = static_cast<long>(rows) * (cols / 64);
+    long blocks = (units + 255) / 256;
+    if (blocks > kGenBlocks) blocks = kGenBlocks;
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(gen_sparse_ternary_kernel, dim3(blocks), dim3(256), 0, s, seed, rows, cols,
+                       meta, values, meta_stride, values_stride, latent);
+    hipLaunchKernelGGL(gen_gamma_kernel, dim3(1), dim3(1), 0, s, static_cast<int>(blocks),
+                       static_cast<double>(rows) * cols, d_gamma);
+    return launch_status(fn);
+}
+
+extern "C" int spb_generate_normal_bf16(uint64_t seed, long n, float std_, uint16_t* out,
+                                        spb_stream_t stream) {
+    clear_error();
+    const char* fn = "spb_generate_normal_bf16";
+    if (n < 0) return invalid("%s: negative size", fn);
+    if (n == 0) return 0;
+    if (!out) return invalid("%s: null pointer", fn);
+    long blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(gen_normal_bf16_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
+                       seed, n, std_, out);
+    return launch_status(fn);
+}

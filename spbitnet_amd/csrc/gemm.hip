@@ -43,7 +43,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kGemmBlock = 512;  // 8 waves splitting K
 
 template <uint32_t kTable>
 __device__ __forceinline__ uint32_t bitop3(uint32_t a, uint32_t b, uint32_t c) {
@@ -80,12 +79,12 @@ __device__ __forceinline__ v4i smfmac_values(uint32_t s16) {
 // 128-column steps s = w, w + kWaves, ...  Each wave decodes its A operands
 // once per step and reuses every B tile for kStrips SMFMACs.  The waves'
 // int32 partial sums meet in LDS (integer atomics, exact in any order).
-template <int kStrips, int kTiles>
-__global__ __launch_bounds__(kGemmBlock) void gemm_smfmac_kernel(
+template <int kStrips, int kTiles, int kWaves>
+__global__ __launch_bounds__(kWaves * kWave) void gemm_smfmac_kernel(
     const uint32_t* __restrict__ meta, const uint32_t* __restrict__ values,
     const int8_t* __restrict__ X, int32_t* __restrict__ Y, int rows, int cols, int n, int ms,
     int vs) {
-    constexpr int kWaves = kGemmBlock / kWave;
+    constexpr int kBlock = kWaves * kWave;
     constexpr int kAcc = kStrips * kTiles * 4;  // int32 accumulators per lane
     __shared__ int red[kAcc * kWave];
     const int lane = threadIdx.x & (kWave - 1);
@@ -95,7 +94,7 @@ __global__ __launch_bounds__(kGemmBlock) void gemm_smfmac_kernel(
     const int q = lane >> 4;   // lane group
     const int li = lane & 15;  // A row / B,C token within a tile
 
-    for (int i = threadIdx.x; i < kAcc * kWave; i += kGemmBlock) red[i] = 0;
+    for (int i = threadIdx.x; i < kAcc * kWave; i += kBlock) red[i] = 0;
 
     v4i acc[kStrips][kTiles];
 #pragma unroll
@@ -148,17 +147,18 @@ __global__ __launch_bounds__(kGemmBlock) void gemm_smfmac_kernel(
             for (int v = 0; v < 4; ++v)
                 atomicAdd(&red[((st * kTiles + t) * 4 + v) * kWave + lane], acc[st][t][v]);
     __syncthreads();
-    // Write-out: entry (st, t, v) of lane l is token tok0 + 16t + l%16, row
-    // r0 + 16st + 4(l/16) + v.  Waves share the entries.
-    for (int e = threadIdx.x; e < kAcc * kWave; e += kGemmBlock) {
-        const int l = e % kWave;
-        const int sv = e / kWave;  // (st * kTiles + t) * 4 + v
-        const int v = sv & 3;
-        const int t = (sv >> 2) % kTiles;
-        const int st = (sv >> 2) / kTiles;
-        const int tok = tok0 + 16 * t + (l & 15);
-        const long row = r0 + 16 * st + 4 * (l >> 4) + v;
-        if (tok < n && row < rows) Y[static_cast<long>(tok) * rows + row] = red[e];
+    // Write-out, row-fastest so each token's kStrips*16 outputs are one
+    // contiguous run of Y.  Entry (st, t, v) of lane l holds token
+    // tok0 + 16t + l%16 and row r0 + 16st + 4(l/16) + v.
+    constexpr int kRows = kStrips * 16;
+    for (int e = threadIdx.x; e < kAcc * kWave; e += kBlock) {
+        const int rl = e % kRows, tl = e / kRows;  // local row, local token
+        const int st = rl >> 4, q = (rl >> 2) & 3, v = rl & 3;
+        const int t = tl >> 4, l = q * 16 + (tl & 15);
+        const int tok = tok0 + tl;
+        const long row = r0 + rl;
+        if (tok < n && row < rows)
+            Y[static_cast<long>(tok) * rows + row] = red[((st * kTiles + t) * 4 + v) * kWave + l];
     }
 }
 
@@ -192,6 +192,14 @@ __global__ __launch_bounds__(256) void gemm_general_kernel(const uint32_t* __res
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+template <int kStrips, int kTiles, int kWaves>
+void launch_smfmac(const uint32_t* meta, const uint32_t* values, const int8_t* X, int32_t* Y,
+                   int rows, int cols, int n, int ms, int vs, hipStream_t st) {
+    const dim3 grid((rows + kStrips * 16 - 1) / (kStrips * 16), (n + kTiles * 16 - 1) / (kTiles * 16));
+    hipLaunchKernelGGL((gemm_smfmac_kernel<kStrips, kTiles, kWaves>), grid, dim3(kWaves * kWave),
+                       0, st, meta, values, X, Y, rows, cols, n, ms, vs);
+}
+
 }  // namespace
 }  // namespace spb
 
@@ -222,24 +230,17 @@ extern "C" int spb_sparse_ternary_gemm(const uint32_t* meta, const uint32_t* val
     if (!meta || !values || !X || !Y) return invalid("%s: null pointer", fn);
     hipStream_t st = as_stream(stream);
     if (spb_sparse_ternary_gemm_kernel_id(meta, values, X, rows, cols, n, ms, vs)) {
-        // Rows per block (16 * strips) and tokens per pass (16 * tiles): more
-        // rows per block when there are many tokens, so each activation tile
-        // read from L2 feeds more matrix-core operations.
+        // Rows per block (16 * strips), tokens per pass (16 * tiles) and waves
+        // per block, chosen by measurement at 6912x2560: larger tiles as the
+        // batch grows, so each activation tile read from L2 feeds more
+        // matrix-core operations.
         if (n <= 16) {
-            const int bx = (rows + 15) / 16;
-            hipLaunchKernelGGL((gemm_smfmac_kernel<1, 1>), dim3(bx, 1), dim3(kGemmBlock), 0, st,
-                               meta, values, X, Y, rows, cols, n, ms, vs);
+            launch_smfmac<2, 1, 4>(meta, values, X, Y, rows, cols, n, ms, vs, st);
         } else if (n <= 64) {
-            const int bx = (rows + 31) / 32;
-            const int by = (n + 63) / 64;
-            hipLaunchKernelGGL((gemm_smfmac_kernel<2, 4>), dim3(bx, by), dim3(kGemmBlock), 0, st,
-                               meta, values, X, Y, rows, cols, n, ms, vs);
+            launch_smfmac<2, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
         } else {
-            const int bx = (rows + 63) / 64;
-            const int by = (n + 63) / 64;
-            if (by > 65535) return invalid("%s: batch %d too large", fn, n);
-            hipLaunchKernelGGL((gemm_smfmac_kernel<4, 4>), dim3(bx, by), dim3(kGemmBlock), 0, st,
-                               meta, values, X, Y, rows, cols, n, ms, vs);
+            if ((n + 63) / 64 > 65535) return invalid("%s: batch %d too large", fn, n);
+            launch_smfmac<8, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
         }
     } else {
         if (n > 65535) return invalid("%s: batch %d exceeds 65535", fn, n);

@@ -37,383 +37,12 @@
 //     a large matrix is streamed by a grid sized to the resident capacity.
 // Shapes the bit-plane kernel does not take (cols % 128 != 0, cols > 32768,
 // unaligned rows or activations) go to a general wave-per-row kernel.
-#include "common.hpp"
+#include "bitplane.hpp"
 #include "spbitnet_amd.h"
 
 namespace spb {
 
 namespace {
-
-constexpr int kBlock = 512;
-constexpr int kChunk = 128;           // columns per thread per row (bit-plane kernel)
-constexpr int kMaxPlaneCols = 32768;  // bit-plane kernel column limit (C <= kBlock/2)
-
-struct Weights {
-    const uint32_t* meta;
-    const uint32_t* values;
-    int rows, cols, ms, vs;
-};
-
-// ---- SWAR helpers ----------------------------------------------------------------
-
-// v_bitop3_b32 truth tables: bit i of the table is f(a, b, c) with a, b, c
-// the bits of 0xF0, 0xCC, 0xAA at position i (a = first operand).
-constexpr uint32_t kOrAnd = 0xC8;       // (a | c) & b
-constexpr uint32_t kXorAnd = 0x28;      // (a ^ b) & c
-constexpr uint32_t kSelectKeep = 0x4A;  // a ? (b & ~c) : c
-constexpr uint32_t kXor3 = 0x96;        // a ^ b ^ c
-
-template <uint32_t kTable>
-__device__ __forceinline__ uint32_t bitop3(uint32_t a, uint32_t b, uint32_t c) {
-    return __builtin_amdgcn_bitop3_b32(a, b, c, kTable);
-}
-
-// popcount(v) + acc in one v_bcnt_u32_b32 (the compiler otherwise sums
-// separate popcounts with extra adds).
-__device__ __forceinline__ int bcnt_acc(uint32_t v, int acc) {
-    int r;
-    asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(v), "v"(acc));
-    return r;
-}
-
-// 7 * v on each 16-bit half (one v_pk_mul_lo_u16).  Used on words whose set
-// bits sit at nibble bases (or bit 1 of nibbles), where 7*v copies each bit
-// to the two bits above it without carries.
-__device__ __forceinline__ uint32_t times7_halves(uint32_t v) {
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    u16x2 h = __builtin_bit_cast(u16x2, v);
-    h = h * (u16x2){7, 7};
-    return __builtin_bit_cast(uint32_t, h);
-}
-
-// 8x8 bit transpose of 8 int8 columns (lo = columns 0..3, hi = 4..7, byte i =
-// column i): afterwards byte b of lo (b < 4) or of hi (b >= 4) holds plane b,
-// bit i = bit b of column i.  Three delta swaps (Hacker's Delight, 7-13).
-__device__ __forceinline__ void transpose8x8(uint32_t& lo, uint32_t& hi) {
-    uint32_t t;
-    t = bitop3<kXorAnd>(lo, lo >> 7, 0x00AA00AAu);
-    lo = bitop3<kXor3>(lo, t, t << 7);
-    t = bitop3<kXorAnd>(hi, hi >> 7, 0x00AA00AAu);
-    hi = bitop3<kXor3>(hi, t, t << 7);
-    t = bitop3<kXorAnd>(lo, lo >> 14, 0x0000CCCCu);
-    lo = bitop3<kXor3>(lo, t, t << 14);
-    t = bitop3<kXorAnd>(hi, hi >> 14, 0x0000CCCCu);
-    hi = bitop3<kXor3>(hi, t, t << 14);
-    t = bitop3<kXorAnd>(lo, hi << 4, 0xF0F0F0F0u);
-    lo ^= t;
-    hi ^= t >> 4;
-}
-
-// ---- activation sources ----------------------------------------------------------
-
-// int8 activations.
-struct Int8Src {
-    const int8_t* x;
-    long token_stride = 0;  // batched use: token t reads x + t * token_stride
-    __device__ void offset(long t) { x += t * token_stride; }
-    __device__ void prepare() {}
-    __device__ int load(int c) const { return x[c]; }
-    // Columns c0..c7 as two little-endian dwords (c0 % 8 == 0, x 8-byte aligned).
-    __device__ void load8(int c0, uint32_t& lo, uint32_t& hi) const {
-        const uint2 v = *reinterpret_cast<const uint2*>(x + c0);
-        lo = v.x;
-        hi = v.y;
-    }
-};
-
-// fp16 / bf16 activations quantised on the fly with the reference's rule.
-template <class T>
-struct QuantSrc {
-    const uint16_t* x;
-    const float* d_absmax;
-    float scale;
-    __device__ void offset(long) {}
-    __device__ void prepare() { scale = quant_scale(*d_absmax); }
-    __device__ int load(int c) const { return quant_round_clamp(T::to_float(x[c]) * scale); }
-    __device__ uint32_t q8(uint32_t h) const {
-        return static_cast<uint32_t>(
-                   quant_round_clamp(T::to_float(static_cast<uint16_t>(h)) * scale)) &
-               0xFFu;
-    }
-    // Columns c0..c7 (c0 % 8 == 0, x 16-byte aligned), quantised, as two dwords.
-    __device__ void load8(int c0, uint32_t& lo, uint32_t& hi) const {
-        const uint4 v = *reinterpret_cast<const uint4*>(x + c0);  // 8 x 16-bit
-        lo = q8(v.x & 0xFFFF) | (q8(v.x >> 16) << 8) | (q8(v.y & 0xFFFF) << 16) |
-             (q8(v.y >> 16) << 24);
-        hi = q8(v.z & 0xFFFF) | (q8(v.z >> 16) << 8) | (q8(v.w & 0xFFFF) << 16) |
-             (q8(v.w >> 16) << 24);
-    }
-};
-
-// Activations already in the plane layout (global memory), for the general
-// kernel: column c's int8 value reassembled from its 8 plane bits.
-struct PlaneSrc {
-    const uint32_t* p;
-    __device__ void prepare() {}
-    __device__ int load(int c) const {
-        const uint32_t* g = p + (c >> 5) * 8;
-        int v = 0;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) v |= static_cast<int>((g[b] >> (c & 31)) & 1u) << b;
-        return static_cast<int>(static_cast<int8_t>(v));
-    }
-};
-
-// ---- how a bit-plane block obtains its activation planes ----------------------
-
-// Planes built in LDS by the block itself from an activation source.
-template <class Src>
-struct BuildPlanes {
-    Src src;
-    __device__ void offset(long t) { src.offset(t); }
-    __device__ void prepare() { src.prepare(); }
-    // Transposes the activations, 8 columns per thread, into LDS planes
-    // (bytes of word [w*8+b]).  The loads of up to two units are issued
-    // before either is transposed.
-    __device__ void build(uint32_t* planes, int cols, int tid) const {
-        const int units = cols >> 3;
-        uint8_t* pb = reinterpret_cast<uint8_t*>(planes);
-        for (int u0 = tid; u0 < units; u0 += 2 * kBlock) {
-            const int u1 = u0 + kBlock;
-            uint32_t lo0, hi0, lo1 = 0, hi1 = 0;
-            src.load8(u0 * 8, lo0, hi0);
-            if (u1 < units) src.load8(u1 * 8, lo1, hi1);
-            transpose8x8(lo0, hi0);
-            const int w0 = u0 >> 2, q0 = u0 & 3;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                pb[(w0 * 8 + b) * 4 + q0] = static_cast<uint8_t>(lo0 >> (8 * b));
-                pb[(w0 * 8 + b + 4) * 4 + q0] = static_cast<uint8_t>(hi0 >> (8 * b));
-            }
-            if (u1 < units) {
-                transpose8x8(lo1, hi1);
-                const int w1 = u1 >> 2, q1 = u1 & 3;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    pb[(w1 * 8 + b) * 4 + q1] = static_cast<uint8_t>(lo1 >> (8 * b));
-                    pb[(w1 * 8 + b + 4) * 4 + q1] = static_cast<uint8_t>(hi1 >> (8 * b));
-                }
-            }
-        }
-    }
-};
-
-// Planes precomputed in global memory (spb_activation_planes or
-// spb_absmax_quantize_planes_*): the block copies the cols bytes into LDS with
-// 16-byte loads (every thread of the block then reads its chunk from LDS; a
-// direct global read per thread would request 128 B x 512 threads per block
-// from L2 for cols bytes of data).
-struct GlobalPlanes {
-    const uint32_t* p;
-    __device__ void offset(long) {}
-    __device__ void prepare() {}
-    __device__ void build(uint32_t* planes, int cols, int tid) const {
-        const uint4* src = reinterpret_cast<const uint4*>(p);
-        uint4* dst = reinterpret_cast<uint4*>(planes);
-        for (int i = tid; i < (cols >> 4); i += kBlock) dst[i] = src[i];
-    }
-};
-
-// ---- output sinks ------------------------------------------------------------------
-
-struct Int32Sink {
-    int32_t* y;
-    long token_stride = 0;  // batched use: token t writes y + t * token_stride
-    __device__ void offset(long t) { y += t * token_stride; }
-    __device__ void prepare() {}
-    __device__ void store(long r, int acc) const { y[r] = acc; }
-};
-
-template <class T>
-struct DequantSink {
-    uint16_t* out;
-    const float* d_absmax;
-    float gamma;
-    float dq;
-    __device__ void offset(long) {}
-    __device__ void prepare() { dq = dequant_scale(gamma, *d_absmax); }
-    __device__ void store(long r, int acc) const {
-        out[r] = T::from_float(static_cast<float>(acc) * dq);
-    }
-};
-
-// ---- bit-plane decode of one 128-column chunk ----------------------------------
-
-// Mask of the columns holding -1 in one meta word (8 groups, 32 columns).
-// k: the meta word; vw: the values word holding these groups' sign pairs,
-// in its low (upper_half = false) or high 16 bits.
-__device__ __forceinline__ uint32_t neg_mask(uint32_t k, uint32_t vw, bool upper_half) {
-    // Spread group g's sign pair to nibble g: s_lo -> bit 4g, s_hi -> bit 4g+1.
-    // perm gives bytes [b0, 0, b1, 0] (or [b2, 0, b3, 0]); selector 0x0C is 0x00.
-    uint32_t t = __builtin_amdgcn_perm(vw, vw, upper_half ? 0x0C030C02u : 0x0C010C00u);
-    t = bitop3<kOrAnd>(t << 4, 0x0F0F0F0Fu, t);
-    const uint32_t a0 = bitop3<kOrAnd>(t << 2, 0x11111111u, t);  // s_lo at nibble bit 0
-    const uint32_t a1 = bitop3<kOrAnd>(t << 2, 0x22222222u, t);  // s_hi at nibble bit 1
-    const uint32_t s_lo = times7_halves(a0);                      // over nibble bits 0..2
-    const uint32_t s_hi = times7_halves(a1);                      // over nibble bits 1..3
-    // Each nibble of k holds exactly two set bits, so subtracting 1 per nibble
-    // never borrows across nibbles: hi = higher kept column, k ^ hi = lower.
-    const uint32_t hi = k & (k - 0x11111111u);
-    return (hi & s_hi) | bitop3<kXorAnd>(k, hi, s_lo);
-}
-
-// X[w][b]: plane b of the chunk's meta word w.
-__device__ __forceinline__ int chunk_dot(const uint4 K, const uint2 V, const uint32_t (&X)[4][8]) {
-    const uint32_t kw[4] = {K.x, K.y, K.z, K.w};
-    int cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int cneg = 0;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const uint32_t neg = neg_mask(kw[w], w < 2 ? V.x : V.y, (w & 1) != 0);
-        // (X & P) | (~X & N) with P = k & ~N, as one 3-input op of (X, k, N)
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-            cnt[b] = bcnt_acc(bitop3<kSelectKeep>(X[w][b], kw[w], neg), cnt[b]);
-        cneg = bcnt_acc(neg, cneg);
-    }
-    int s = cneg - (cnt[7] << 7);
-#pragma unroll
-    for (int b = 0; b < 7; ++b) s += cnt[b] << b;
-    return s;
-}
-
-// Work item of one thread: the 128-column chunk c of one row.
-struct ChunkLoad {
-    uint4 k;
-    uint2 v;
-    bool ok;
-};
-
-__device__ __forceinline__ ChunkLoad load_chunk(const Weights& wt, long r, int c, bool active) {
-    ChunkLoad L;
-    L.ok = active && r < wt.rows;
-    if (L.ok) {
-        L.k = *reinterpret_cast<const uint4*>(wt.meta + r * wt.ms + 4 * c);
-        L.v = *reinterpret_cast<const uint2*>(wt.values + r * wt.vs + 2 * c);
-    } else {
-        L.k = make_uint4(0, 0, 0, 0);
-        L.v = make_uint2(0, 0);
-    }
-    return L;
-}
-
-// The 32 plane words of one 128-column chunk (128 contiguous bytes).
-__device__ __forceinline__ void load_x(const uint32_t* src, uint32_t (&X)[4][8]) {
-    const uint4* p = reinterpret_cast<const uint4*>(src);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const uint4 a = p[2 * w], b = p[2 * w + 1];
-        X[w][0] = a.x;
-        X[w][1] = a.y;
-        X[w][2] = a.z;
-        X[w][3] = a.w;
-        X[w][4] = b.x;
-        X[w][5] = b.y;
-        X[w][6] = b.z;
-        X[w][7] = b.w;
-    }
-}
-
-// Rows are processed in tiles of RS * tile_steps rows (RS = rows per step:
-// kBlock / C threads per row).  Block b takes tiles b, b + gridDim.x, ...; a
-// thread visits its chunk of row tile*tile_rows + s*RS + ro for each step s.
-// The first weight load is issued before the activation prologue, the next
-// item's weights are loaded before the current one is reduced (prefetch
-// distance 1), and per-row sums collect in two LDS buffers used by alternate
-// tiles, so one barrier per tile orders accumulation and write-out.
-template <class Act, class Sink>
-__global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(Weights wt, Act act, Sink sink,
-                                                               int tile_steps, long ntiles) {
-    extern __shared__ uint32_t smem[];
-    const int nwords = wt.cols >> 5;
-    const int C = wt.cols / kChunk;
-    const int RS = kBlock / C;
-    const int tile_rows = RS * tile_steps;
-    uint32_t* planes = smem;  // word [w * 8 + b]
-    int* acc0 = reinterpret_cast<int*>(smem + 8 * nwords);
-    int* acc1 = acc0 + tile_rows;
-
-    const int tid = threadIdx.x;
-    const int c = tid % C;
-    const int ro = tid / C;
-    const bool active = ro < RS;
-
-    // (tile, step) advance uniformly across the block (scalar registers); each
-    // thread's row follows from them without divisions.
-    long tile = blockIdx.x;
-    int step = 0;
-    long row = tile * tile_rows + ro;
-    int parity = 0;
-
-    act.offset(blockIdx.y);
-    sink.offset(blockIdx.y);
-    ChunkLoad cur = load_chunk(wt, row, c, active);
-    act.prepare();
-    sink.prepare();
-    uint32_t X[4][8];
-    act.build(planes, wt.cols, tid);
-    for (int i = tid; i < 2 * tile_rows; i += kBlock) acc0[i] = 0;
-    __syncthreads();
-    if (active) load_x(planes + c * 32, X);
-
-    for (;;) {
-        int step_n = step + 1;
-        long tile_n = tile;
-        long row_n = row + RS;
-        if (step_n == tile_steps) {
-            step_n = 0;
-            tile_n = tile + gridDim.x;
-            row_n = tile_n * tile_rows + ro;
-        }
-        const bool more = tile_n < ntiles;
-        const ChunkLoad nxt = more ? load_chunk(wt, row_n, c, active) : ChunkLoad{};
-        int* acc = parity ? acc1 : acc0;
-        if (cur.ok) atomicAdd(&acc[step * RS + ro], chunk_dot(cur.k, cur.v, X));
-        if (step == tile_steps - 1) {
-            __syncthreads();  // uniform: (tile, step) are the same in every thread
-            const long row0 = tile * tile_rows;
-            for (int j = tid; j < tile_rows; j += kBlock) {
-                if (row0 + j < wt.rows) sink.store(row0 + j, acc[j]);
-                acc[j] = 0;
-            }
-            parity ^= 1;
-        }
-        if (!more) break;
-        cur = nxt;
-        step = step_n;
-        tile = tile_n;
-        row = row_n;
-    }
-}
-
-// ---- general kernel: one wave per row, any cols % 4 == 0, any strides ---------
-
-template <class Src, class Sink>
-__global__ __launch_bounds__(256) void gemv_general_kernel(Weights wt, Src src, Sink sink) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const long row = static_cast<long>(blockIdx.x) * (256 / kWave) + (threadIdx.x / kWave);
-    src.prepare();
-    sink.prepare();
-    if (row >= wt.rows) return;
-    const uint32_t* mr = wt.meta + row * wt.ms;
-    const uint32_t* vr = wt.values + row * wt.vs;
-    int acc = 0;
-    for (int g = lane; g < (wt.cols >> 2); g += kWave) {
-        const uint32_t bm = (mr[g >> 3] >> ((g & 7) * 4)) & 0xFu;
-        const uint32_t sg = (vr[g >> 4] >> ((g & 15) * 2)) & 0x3u;
-        // Lower / higher set bit; a bitmap without exactly two bits decodes to
-        // positions (0, 0), as the reference's table does (sparse_ternary.cu:34-51).
-        const bool ok = __builtin_popcount(bm) == 2;
-        const int p0 = ok ? __builtin_ctz(bm) : 0;
-        const int p1 = ok ? __builtin_ctz(bm & (bm - 1)) : 0;
-        const int x0 = src.load(4 * g + p0);
-        const int x1 = src.load(4 * g + p1);
-        acc += (sg & 1u) ? -x0 : x0;
-        acc += (sg & 2u) ? -x1 : x1;
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) sink.store(row, acc);
-}
 
 // ---- activation planes in global memory ------------------------------------------
 
@@ -497,78 +126,6 @@ __global__ __launch_bounds__(256) void unpack_kernel(Weights wt, int8_t* out) {
     } else {
         for (int i = 0; i < 4; ++i) dst[i] = v[i];
     }
-}
-
-// ---- host side ------------------------------------------------------------------
-
-int check_weights(const char* fn, const uint32_t* meta, const uint32_t* values, int rows,
-                  int cols, int ms, int vs) {
-    if (rows < 0 || cols < 0) return invalid("%s: negative shape (%d, %d)", fn, rows, cols);
-    if (cols % 4) return invalid("%s: cols=%d is not a multiple of 4", fn, cols);
-    const int need_m = (cols / 4 + 7) / 8, need_v = (cols / 4 + 15) / 16;
-    if (ms < need_m)
-        return invalid("%s: meta_row_stride=%d < ceil(cols/32)=%d", fn, ms, need_m);
-    if (vs < need_v)
-        return invalid("%s: values_row_stride=%d < ceil(cols/64)=%d", fn, vs, need_v);
-    if (rows && cols && (!meta || !values)) return invalid("%s: null weight pointer", fn);
-    return 0;
-}
-
-bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
-
-bool bitplane_ok(const uint32_t* meta, const uint32_t* values, int cols, int ms, int vs) {
-    return cols > 0 && cols % kChunk == 0 && cols <= kMaxPlaneCols && ms % 4 == 0 &&
-           vs % 2 == 0 && aligned(meta, 16) && aligned(values, 8);
-}
-
-// Resident blocks per CU for one bit-plane instantiation (cached per LDS size).
-template <class Act, class Sink>
-int bitplane_blocks_per_cu(size_t lds) {
-    static size_t cached_lds[4] = {0, 0, 0, 0};
-    static int cached_n[4] = {0, 0, 0, 0};
-    for (int i = 0; i < 4; ++i)
-        if (cached_lds[i] == lds && cached_n[i] > 0) return cached_n[i];
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_bitplane_kernel<Act, Sink>, kBlock,
-                                                     lds) != hipSuccess ||
-        n <= 0)
-        n = 1;
-    for (int i = 0; i < 4; ++i)
-        if (cached_n[i] == 0) {
-            cached_lds[i] = lds;
-            cached_n[i] = n;
-            break;
-        }
-    return n;
-}
-
-template <class Act, class Sink>
-void launch_bitplane(const Weights& wt, Act act, Sink sink, hipStream_t stream, int tokens = 1) {
-    const int C = wt.cols / kChunk;
-    const long RS = kBlock / C;
-    const long steps_max = 8;
-    const size_t plane_lds = static_cast<size_t>(wt.cols);
-    const size_t lds_max = plane_lds + 2 * RS * steps_max * 4;
-    long resident =
-        static_cast<long>(bitplane_blocks_per_cu<Act, Sink>(lds_max)) * device_cu_count();
-    resident = (resident + tokens - 1) / tokens;  // tokens share the resident capacity
-    // Enough tiles for every resident block; longer tiles once the matrix
-    // is several times the resident capacity.
-    long steps = (static_cast<long>(wt.rows) + RS * resident - 1) / (RS * resident);
-    steps = steps < 1 ? 1 : (steps > steps_max ? steps_max : steps);
-    const long tile_rows = RS * steps;
-    const long tiles = (wt.rows + tile_rows - 1) / tile_rows;
-    const int grid = static_cast<int>(tiles < resident ? tiles : resident);
-    const size_t lds = plane_lds + 2 * static_cast<size_t>(tile_rows) * 4;
-    hipLaunchKernelGGL((gemv_bitplane_kernel<Act, Sink>), dim3(grid, tokens), dim3(kBlock), lds,
-                       stream, wt, act, sink, static_cast<int>(steps), tiles);
-}
-
-template <class Src, class Sink>
-void launch_general(const Weights& wt, Src src, Sink sink, hipStream_t stream) {
-    const long blocks = (static_cast<long>(wt.rows) + 3) / 4;
-    hipLaunchKernelGGL((gemv_general_kernel<Src, Sink>), dim3(blocks), dim3(256), 0, stream, wt,
-                       src, sink);
 }
 
 template <class T>

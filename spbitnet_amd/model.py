@@ -1,0 +1,280 @@
+"""Model and decode-engine API over the C ABI, mirroring the reference's
+include/spbitnet/model.h (ModelConfig, SparseLinear, TransformerLayer, Model)
+and include/spbitnet/inference.h (InferenceEngine): same names and meaning,
+torch device tensors in place of raw device pointers.
+
+Weights live in torch tensors (device memory owned by torch); the engine
+borrows them, as the reference engine borrows ``const Model&``
+(include/spbitnet/inference.h:44), so the Model must outlive its engines.
+Activations, the KV cache and the embedding / LM head are bf16.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from .weights import seed_for
+
+
+@dataclass
+class ModelConfig:
+    """ModelConfig (reference include/spbitnet/model.h:23-40)."""
+    hidden_size: int
+    num_hidden_layers: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    intermediate_size: int
+    vocab_size: int
+    max_position_embeddings: int
+    head_dim: int = 0
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    bos_token_id: int = 1
+    eos_token_id: int = 2
+    model_type: str = "bitnet"
+    hidden_act: str = "relu2"
+    tie_word_embeddings: bool = True
+
+    def __post_init__(self):
+        if not self.head_dim:
+            self.head_dim = self.hidden_size // self.num_attention_heads
+
+    @staticmethod
+    def bitnet_b158_2b4t(max_position_embeddings: int = 4096) -> "ModelConfig":
+        """The BitNet b1.58 2B-4T shape (30 layers, hidden 2560, 20 / 5 heads,
+        head_dim 128, FFN 6912, vocab 128256, RoPE theta 500000)."""
+        return ModelConfig(hidden_size=2560, num_hidden_layers=30, num_attention_heads=20,
+                           num_key_value_heads=5, intermediate_size=6912, vocab_size=128256,
+                           max_position_embeddings=max_position_embeddings, head_dim=128,
+                           rms_norm_eps=1e-5, rope_theta=500000.0, bos_token_id=128000,
+                           eos_token_id=128001)
+
+    def c_struct(self) -> _lib.ModelConfigC:
+        return _lib.ModelConfigC(self.hidden_size, self.num_hidden_layers,
+                                 self.num_attention_heads, self.num_key_value_heads,
+                                 self.intermediate_size, self.vocab_size,
+                                 self.max_position_embeddings, self.head_dim,
+                                 float(self.rms_norm_eps), float(self.rope_theta),
+                                 self.bos_token_id, self.eos_token_id)
+
+
+@dataclass
+class SparseLinear:
+    """SparseLinear (reference include/spbitnet/model.h:46-60)."""
+    meta: torch.Tensor    # int32 [rows, meta_stride]
+    values: torch.Tensor  # int32 [rows, values_stride]
+    gamma: float
+    rows: int
+    cols: int
+    meta_stride: int
+    values_stride: int
+
+    def gpu_bytes(self) -> int:
+        return 4 * self.rows * (self.meta_stride + self.values_stride)
+
+    def c_struct(self) -> _lib.SparseLinearC:
+        return _lib.SparseLinearC(self.meta.data_ptr(), self.values.data_ptr(),
+                                  float(self.gamma), self.rows, self.cols, self.meta_stride,
+                                  self.values_stride)
+
+
+PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+@dataclass
+class TransformerLayer:
+    """TransformerLayer (reference include/spbitnet/model.h:63-82)."""
+    q_proj: SparseLinear
+    k_proj: SparseLinear
+    v_proj: SparseLinear
+    o_proj: SparseLinear
+    gate_proj: SparseLinear
+    up_proj: SparseLinear
+    down_proj: SparseLinear
+    input_layernorm: torch.Tensor           # float32 [hidden]
+    post_attention_layernorm: torch.Tensor  # float32 [hidden]
+    attn_sub_norm: Optional[torch.Tensor] = None  # float32 [hidden]
+    ffn_sub_norm: Optional[torch.Tensor] = None   # float32 [intermediate]
+
+    def c_struct(self) -> _lib.TransformerLayerC:
+        def ptr(t):
+            return t.data_ptr() if t is not None else None
+        return _lib.TransformerLayerC(*[getattr(self, n).c_struct() for n in PROJECTIONS],
+                                      ptr(self.input_layernorm),
+                                      ptr(self.post_attention_layernorm),
+                                      ptr(self.attn_sub_norm), ptr(self.ffn_sub_norm))
+
+
+@dataclass
+class Model:
+    """Model (reference include/spbitnet/model.h:88-145): all weights on the
+    GPU.  embed_tokens and lm_head are bf16 [vocab, hidden]; lm_head None
+    means tied to the embedding (model.h:131-133)."""
+    config: ModelConfig
+    layers: List[TransformerLayer]
+    embed_tokens: torch.Tensor
+    final_norm: torch.Tensor
+    lm_head_weight: Optional[torch.Tensor] = None
+    _keep: list = field(default_factory=list, repr=False)
+
+    def lm_head(self) -> torch.Tensor:
+        return self.lm_head_weight if self.lm_head_weight is not None else self.embed_tokens
+
+    def layer(self, i: int) -> TransformerLayer:
+        return self.layers[i]
+
+    def total_gpu_bytes(self) -> int:
+        n = sum(getattr(l, p).gpu_bytes() for l in self.layers for p in PROJECTIONS)
+        n += self.embed_tokens.numel() * 2 + self.final_norm.numel() * 4
+        if self.lm_head_weight is not None:
+            n += self.lm_head_weight.numel() * 2
+        for l in self.layers:
+            for t in (l.input_layernorm, l.post_attention_layernorm, l.attn_sub_norm,
+                      l.ffn_sub_norm):
+                if t is not None:
+                    n += t.numel() * 4
+        return n
+
+    @staticmethod
+    def random(config: ModelConfig, seed: int = 0, device="cuda", embed_std: float = 0.02,
+               sub_norms: bool = True) -> "Model":
+        """Random-init model generated on the device: every projection from
+        latent W ~ N(0,1) through the 2:4 top-2 mask and ternary signs
+        (convert_model.py's recipe), embedding ~ N(0, embed_std^2) in bf16
+        (tied LM head), every RMSNorm weight 1.0."""
+        c = config
+        dev = torch.device(device)
+        H, I, kvd = c.hidden_size, c.intermediate_size, c.num_key_value_heads * c.head_dim
+        shapes = {"q_proj": (H, H), "k_proj": (kvd, H), "v_proj": (kvd, H), "o_proj": (H, H),
+                  "gate_proj": (I, H), "up_proj": (I, H), "down_proj": (H, I)}
+        L = _lib.load()
+        stream = torch.cuda.current_stream(dev).cuda_stream or None
+        gammas = torch.zeros(c.num_hidden_layers * len(PROJECTIONS), dtype=torch.float32,
+                             device=dev)
+        raw = []
+        for li in range(c.num_hidden_layers):
+            row = {}
+            for pi, name in enumerate(PROJECTIONS):
+                rows, cols = shapes[name]
+                ms, vs = cols // 32, cols // 64
+                meta = torch.empty((rows, ms), dtype=torch.int32, device=dev)
+                values = torch.empty((rows, vs), dtype=torch.int32, device=dev)
+                g = gammas[li * len(PROJECTIONS) + pi:]
+                _lib.check(L.spb_generate_sparse_ternary(
+                    seed_for("model", seed, li, name) & 0xFFFFFFFFFFFFFFFF, rows, cols,
+                    meta.data_ptr(), values.data_ptr(), ms, vs, g.data_ptr(), None, stream),
+                    "spb_generate_sparse_ternary")
+                row[name] = (meta, values, rows, cols, ms, vs)
+            raw.append(row)
+        embed = torch.empty((c.vocab_size, H), dtype=torch.bfloat16, device=dev)
+        _lib.check(L.spb_generate_normal_bf16(seed_for("model", seed, "embed") & 0xFFFFFFFFFFFFFFFF,
+                                              embed.numel(), float(embed_std), embed.data_ptr(),
+                                              stream), "spb_generate_normal_bf16")
+        g_host = gammas.cpu().numpy()
+        layers = []
+        for li, row in enumerate(raw):
+            lin = {}
+            for pi, name in enumerate(PROJECTIONS):
+                meta, values, rows, cols, ms, vs = row[name]
+                lin[name] = SparseLinear(meta, values, float(g_host[li * len(PROJECTIONS) + pi]),
+                                         rows, cols, ms, vs)
+            ones_h = torch.ones(H, dtype=torch.float32, device=dev)
+            layers.append(TransformerLayer(
+                **lin, input_layernorm=ones_h, post_attention_layernorm=ones_h.clone(),
+                attn_sub_norm=ones_h.clone() if sub_norms else None,
+                ffn_sub_norm=torch.ones(I, dtype=torch.float32, device=dev) if sub_norms else None))
+        return Model(config, layers, embed, torch.ones(H, dtype=torch.float32, device=dev))
+
+    def to_host(self) -> dict:
+        """Host (numpy) copies of every weight, for the CPU oracle."""
+        def npf(t):
+            return None if t is None else t.detach().cpu().numpy()
+        out = {"config": self.config, "layers": []}
+        for l in self.layers:
+            d = {}
+            for p in PROJECTIONS:
+                s = getattr(l, p)
+                d[p] = (s.meta.cpu().numpy().view(np.uint32), s.values.cpu().numpy().view(np.uint32),
+                        s.gamma, s.rows, s.cols, s.meta_stride, s.values_stride)
+            d["norms"] = [npf(l.input_layernorm), npf(l.post_attention_layernorm),
+                          npf(l.attn_sub_norm), npf(l.ffn_sub_norm)]
+            out["layers"].append(d)
+        out["embed"] = self.embed_tokens.cpu().view(torch.int16).numpy().view(np.uint16)
+        out["lm_head"] = (None if self.lm_head_weight is None else
+                          self.lm_head_weight.cpu().view(torch.int16).numpy().view(np.uint16))
+        out["final_norm"] = npf(self.final_norm)
+        return out
+
+
+class InferenceEngine:
+    """InferenceEngine (reference include/spbitnet/inference.h:23-70) over the
+    HIP decode engine: forward() one token at a time, reset(), seq_len(), plus
+    generate(), which runs a whole greedy generation on the device."""
+
+    def __init__(self, model: Model, max_seq: Optional[int] = None, stream=None):
+        self.model = model
+        c = model.config
+        self.max_seq = int(max_seq or c.max_position_embeddings)
+        self._L = _lib.load()
+        self._layers = (_lib.TransformerLayerC * c.num_hidden_layers)(
+            *[l.c_struct() for l in model.layers])
+        self._cfg = c.c_struct()
+        h = ctypes.c_void_p()
+        lm = model.lm_head_weight.data_ptr() if model.lm_head_weight is not None else None
+        _lib.check(self._L.spb_engine_create(ctypes.byref(self._cfg), self._layers,
+                                             model.embed_tokens.data_ptr(), lm,
+                                             model.final_norm.data_ptr(), self.max_seq,
+                                             ctypes.byref(h)), "spb_engine_create")
+        self._h = h
+        self._stream = stream if stream is not None else torch.cuda.current_stream()
+        _lib.check(self._L.spb_engine_set_stream(self._h, self._stream.cuda_stream or None),
+                   "spb_engine_set_stream")
+        lp, tp = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.check(self._L.spb_engine_buffers(self._h, ctypes.byref(lp), ctypes.byref(tp)),
+                   "spb_engine_buffers")
+        self._logits_ptr = lp.value
+        self._logits = torch.empty(c.vocab_size, dtype=torch.float32,
+                                   device=model.embed_tokens.device)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._L.spb_engine_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def reset(self) -> None:
+        _lib.check(self._L.spb_engine_reset(self._h), "spb_engine_reset")
+
+    def seq_len(self) -> int:
+        return self._L.spb_engine_seq_len(self._h)
+
+    def forward(self, token_id: int) -> torch.Tensor:
+        """Logits (float32 [vocab], on the device) for the next token."""
+        _lib.check(self._L.spb_engine_forward(self._h, int(token_id), None),
+                   "spb_engine_forward")
+        _lib.memcpy_d2d(self._logits.data_ptr(), self._logits_ptr, self._logits.numel() * 4,
+                        self._stream.cuda_stream or None)
+        return self._logits
+
+    def generate(self, prompt: Sequence[int], n_new: int, stop_at_eos: bool = True) -> List[int]:
+        """Greedy generation (src/main.cpp:133-155): prefill prompt[:-1], then
+        n_new steps from the last prompt token."""
+        p = (ctypes.c_int * len(prompt))(*[int(t) for t in prompt])
+        out = (ctypes.c_int * max(1, n_new))()
+        got = ctypes.c_int(0)
+        _lib.check(self._L.spb_engine_generate(self._h, p, len(prompt), int(n_new),
+                                               1 if stop_at_eos else 0, out, ctypes.byref(got)),
+                   "spb_engine_generate")
+        return list(out[:got.value])
+
+    def decode_steps(self, steps: int) -> None:
+        """Enqueue `steps` more greedy steps (no host synchronisation)."""
+        _lib.check(self._L.spb_engine_decode_steps(self._h, int(steps)),
+                   "spb_engine_decode_steps")

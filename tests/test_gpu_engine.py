@@ -1,0 +1,155 @@
+"""GPU parity of the decode engine (spb_engine_*) and the device weight
+generator against the CPU oracle (oracle/spb_engine_oracle.c): logits bit
+for bit and greedy token ids exactly, the bar of the reference's own
+generate loop (src/main.cpp:133-155) on random-init weights."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from spbitnet_amd import weights as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _small_config(**kw):
+    from spbitnet_amd.model import ModelConfig
+    base = dict(hidden_size=512, num_hidden_layers=2, num_attention_heads=8,
+                num_key_value_heads=2, intermediate_size=1536, vocab_size=4096,
+                max_position_embeddings=1024, head_dim=64, rms_norm_eps=1e-5,
+                rope_theta=500000.0, bos_token_id=1, eos_token_id=2)
+    base.update(kw)
+    return ModelConfig(**base)
+
+
+def _prompt(n, vocab, seed):
+    return [int(t) for t in np.random.default_rng(seed).integers(0, vocab, n)]
+
+
+def test_generator_matches_host_packing(gpu):
+    from spbitnet_amd import _lib
+    L = _lib.load()
+    for rows, cols, seed in [(64, 256, 1), (33, 640, 2), (7, 64, 3)]:
+        ms, vs = cols // 32, cols // 64
+        meta = torch.empty((rows, ms), dtype=torch.int32, device="cuda")
+        values = torch.empty((rows, vs), dtype=torch.int32, device="cuda")
+        gamma = torch.zeros(1, dtype=torch.float32, device="cuda")
+        latent = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+        print(f"generator rows={rows} cols={cols}", flush=True)
+        _lib.check(L.spb_generate_sparse_ternary(seed, rows, cols, meta.data_ptr(),
+                                                 values.data_ptr(), ms, vs, gamma.data_ptr(),
+                                                 latent.data_ptr(), None), "generate")
+        torch.cuda.synchronize()
+        w = latent.cpu().numpy()
+        assert np.isfinite(w).all() and 0.6 < np.abs(w).mean() < 1.0
+        want = W.make_layer_from_latent(w)
+        assert np.array_equal(meta.cpu().numpy().view(np.uint32), want.meta)
+        assert np.array_equal(values.cpu().numpy().view(np.uint32), want.values)
+        g = float(gamma.item())
+        assert abs(g - O.absmean(w)) <= 1e-6 * O.absmean(w)
+
+
+def _engine_pair(cfg, seed, max_seq, **kw):
+    from spbitnet_amd.model import InferenceEngine, Model
+    model = Model.random(cfg, seed=seed, **kw)
+    torch.cuda.synchronize()
+    eng = InferenceEngine(model, max_seq=max_seq)
+    ora = O.EngineOracle(model.to_host(), max_seq)
+    return model, eng, ora
+
+
+def test_engine_forward_logits_bit_exact(gpu):
+    cfg = _small_config()
+    model, eng, ora = _engine_pair(cfg, seed=11, max_seq=128)
+    for i, t in enumerate(_prompt(24, cfg.vocab_size, 5)):
+        print(f"forward step {i}", flush=True)
+        got = eng.forward(t).cpu().numpy()
+        want_tok, want = ora.step(t)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+            f"step {i}: max |diff| {np.abs(got - want).max()}"
+        assert int(np.argmax(got)) == want_tok
+    assert eng.seq_len() == 24
+    eng.reset()
+    ora.reset()
+    got = eng.forward(7).cpu().numpy()
+    assert np.array_equal(got, ora.step(7)[1])
+    eng.close()
+
+
+def test_engine_greedy_128_matches_oracle(gpu):
+    cfg = _small_config()
+    model, eng, ora = _engine_pair(cfg, seed=3, max_seq=256)
+    prompt = _prompt(33, cfg.vocab_size, 9)
+    print("generate 128", flush=True)
+    got = eng.generate(prompt, 128, stop_at_eos=False)
+    want = ora.generate(prompt, 128)
+    assert len(got) == 128
+    assert got == want
+    # a second generation on the same engine starts from a clean state
+    again = eng.generate(prompt, 16, stop_at_eos=False)
+    assert again == want[:16]
+    eng.close()
+
+
+def test_engine_attention_splits(gpu):
+    """Prompt longer than one 256-position attention split."""
+    cfg = _small_config(num_hidden_layers=1)
+    model, eng, ora = _engine_pair(cfg, seed=21, max_seq=700)
+    prompt = _prompt(600, cfg.vocab_size, 13)
+    print("generate long", flush=True)
+    got = eng.generate(prompt, 40, stop_at_eos=False)
+    assert got == ora.generate(prompt, 40)
+    eng.close()
+
+
+def test_engine_without_sub_norms_and_gqa_variants(gpu):
+    for kw, nkv in [(dict(sub_norms=False), 2), ({}, 8), ({}, 1)]:
+        cfg = _small_config(num_key_value_heads=nkv)
+        print(f"variant {kw} nkv={nkv}", flush=True)
+        model, eng, ora = _engine_pair(cfg, seed=31 + nkv, max_seq=96, **kw)
+        prompt = _prompt(9, cfg.vocab_size, nkv)
+        assert eng.generate(prompt, 40, stop_at_eos=False) == ora.generate(prompt, 40)
+        eng.close()
+
+
+def test_engine_stops_at_eos(gpu):
+    cfg = _small_config(num_hidden_layers=1)
+    model, eng, ora = _engine_pair(cfg, seed=41, max_seq=128)
+    prompt = _prompt(5, cfg.vocab_size, 1)
+    free = ora.generate(prompt, 30)
+    eos = free[11]
+    first = free.index(eos)
+    eng.close()
+    from spbitnet_amd.model import InferenceEngine
+    cfg2 = _small_config(num_hidden_layers=1, eos_token_id=eos)
+    model.config = cfg2
+    eng = InferenceEngine(model, max_seq=128)
+    got = eng.generate(prompt, 30, stop_at_eos=True)
+    assert got == free[:first + 1]
+    eng.close()
+
+
+def test_engine_rejects_bad_input(gpu):
+    from spbitnet_amd import _lib
+    cfg = _small_config(num_hidden_layers=1)
+    model, eng, ora = _engine_pair(cfg, seed=5, max_seq=16)
+    with pytest.raises(_lib.SpbError):
+        eng.forward(cfg.vocab_size)
+    with pytest.raises(_lib.SpbError):
+        eng.generate([1, 2, 3], 20)  # exceeds max_seq
+    eng.close()
+
+
+def test_engine_bitnet_2b4t_shape(gpu):
+    """Full config-3 shape: first decode steps bit-exact against the oracle."""
+    from spbitnet_amd.model import ModelConfig
+    cfg = ModelConfig.bitnet_b158_2b4t(max_position_embeddings=4096)
+    print("generating the 2.4B-parameter random model", flush=True)
+    model, eng, ora = _engine_pair(cfg, seed=2025, max_seq=64)
+    for i, t in enumerate(_prompt(3, cfg.vocab_size, 2025)):
+        print(f"config3 step {i}", flush=True)
+        got = eng.forward(t).cpu().numpy()
+        want_tok, want = ora.step(t)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+            f"step {i}: max |diff| {np.abs(got - want).max()}"
+    eng.close()
