@@ -12,11 +12,12 @@
  * Floating-point order: float32 arithmetic in the order the HIP kernels use
  * (fma where they fuse, the same reduction trees), so that logits agree bit
  * for bit and greedy token ids agree exactly:
- *   block sums over T threads: thread t accumulates elements t, t+T, ...
- *     (fma(v, v, acc) for sums of squares), then per 64-thread wave the
- *     butterfly at distances 32..1, then the wave totals in wave order;
- *   dot products of attention: lane l holds fma(q[2l+1], k[2l+1],
- *     q[2l] * k[2l]), butterfly over 64 lanes;
+ *   block sums over T threads: thread t accumulates the 8-element units
+ *     t, t+T, ... (fma(v, v, acc) for sums of squares, element order inside
+ *     a unit), then per 64-thread wave the butterfly at distances 32..1,
+ *     then the wave totals in wave order;
+ *   attention scores: fma over d ascending; softmax sums: butterfly over the
+ *     64 positions of a split;
  *   LM head: lane l accumulates the 8-element chunks l, l+64, ... with fma in
  *     element order, butterfly over 64 lanes;
  *   1/sqrt with correctly rounded divide and sqrt (reference: rsqrtf);
@@ -41,7 +42,7 @@ void spbo_gemv(const uint32_t* meta, const uint32_t* values, const int8_t* x, in
 uint16_t spbo_bf16_round(float f);
 
 #define GEMV_THREADS 512 /* threads of the GEMV blocks whose prologues normalise */
-#define ATTN_CHUNK 256   /* positions per attention split = its threads */
+#define ATTN_SPLIT 64    /* positions per attention split (one per lane) */
 #define LM_THREADS 256
 
 static float bf2f(uint16_t b) {
@@ -72,11 +73,15 @@ static float block_sum(float* p, int T) {
     return s;
 }
 
-/* sum of squares of v[0..n) in the block order of T threads */
+/* Sum of squares of v[0..n) in the unit order of T threads: thread t owns
+ * the 8-element units t, t+T, ... and accumulates their elements in order
+ * with fma; then block_sum. */
 static float sumsq(const float* v, int n, int T) {
     float* p = (float*)calloc((size_t)T, sizeof(float));
+    const int units = n / 8;
     for (int t = 0; t < T; ++t)
-        for (int i = t; i < n; i += T) p[t] = fmaf(v[i], v[i], p[t]);
+        for (int u = t; u < units; u += T)
+            for (int e = 0; e < 8; ++e) p[t] = fmaf(v[8 * u + e], v[8 * u + e], p[t]);
     float s = block_sum(p, T);
     free(p);
     return s;
@@ -247,17 +252,17 @@ void spbo_engine_reset(spbo_engine* e) {
 }
 
 /* attention of one layer (inference.cu:166-202; inference_kernels.cu:185-371)
- * in 256-position splits, combined as in the o-projection prologue. */
+ * in 64-position splits, combined as in the o-projection prologue. */
 static void attention(spbo_engine* e, int l) {
     const int nh = e->nh, nkv = e->nkv, hd = e->hd, G = nh / nkv, half = hd / 2;
-    const int pos = e->pos, S = (pos + ATTN_CHUNK) / ATTN_CHUNK;
+    const int pos = e->pos, S = pos / ATTN_SPLIT + 1;
     const float scale = 1.0f / sqrtf((float)hd);
     const float* rp = e->rope + (size_t)pos * hd;
     float* pm = (float*)malloc(sizeof(float) * nh * S);
     float* pl = (float*)malloc(sizeof(float) * nh * S);
     float* pacc = (float*)malloc(sizeof(float) * nh * S * hd);
-    float qs[8][256], kn[256], vn[256];
-    static float sc[8][ATTN_CHUNK];
+    float qs[8][128];
+    float sc[8][ATTN_SPLIT];
     for (int kvh = 0; kvh < nkv; ++kvh) {
         for (int g = 0; g < G; ++g)
             for (int i = 0; i < half; ++i) {
@@ -276,35 +281,26 @@ static void attention(spbo_engine* e, int l) {
             kc[(size_t)pos * hd + 2 * i + 1] = spbo_bf16_round(x0 * s + x1 * c);
         }
         for (int d = 0; d < hd; ++d) vc[(size_t)pos * hd + d] = spbo_bf16_round(vh[d]);
-        (void)kn;
-        (void)vn;
         for (int s = 0; s < S; ++s) {
-            const int j0 = s * ATTN_CHUNK;
-            const int jn = (pos + 1 - j0) < ATTN_CHUNK ? (pos + 1 - j0) : ATTN_CHUNK;
+            const int j0 = s * ATTN_SPLIT;
+            const int jn = (pos + 1 - j0) < ATTN_SPLIT ? (pos + 1 - j0) : ATTN_SPLIT;
             for (int jj = 0; jj < jn; ++jj) {
                 const uint16_t* kj = kc + (size_t)(j0 + jj) * hd;
                 for (int g = 0; g < G; ++g) {
-                    float lanes[64];
-                    for (int ln = 0; ln < 64; ++ln) {
-                        if (2 * ln < hd) {
-                            const float k0 = bf2f(kj[2 * ln]), k1 = bf2f(kj[2 * ln + 1]);
-                            lanes[ln] = fmaf(qs[g][2 * ln + 1], k1, qs[g][2 * ln] * k0);
-                        } else {
-                            lanes[ln] = 0.0f;
-                        }
-                    }
-                    sc[g][jj] = bfly64(lanes) * scale;
+                    float a = 0.0f;
+                    for (int d = 0; d < hd; ++d) a = fmaf(qs[g][d], bf2f(kj[d]), a);
+                    sc[g][jj] = a * scale;
                 }
             }
             for (int g = 0; g < G; ++g) {
                 float m = -INFINITY;
                 for (int jj = 0; jj < jn; ++jj) m = fmaxf(m, sc[g][jj]);
-                float p[ATTN_CHUNK];
-                for (int t = 0; t < ATTN_CHUNK; ++t) {
+                float p[64];
+                for (int t = 0; t < 64; ++t) {
                     p[t] = t < jn ? spbo_exp_neg(sc[g][t] - m) : 0.0f;
                     if (t < jn) sc[g][t] = p[t];
                 }
-                const float lsum = block_sum(p, ATTN_CHUNK);
+                const float lsum = bfly64(p);
                 const int h = kvh * G + g;
                 pm[h * S + s] = m;
                 pl[h * S + s] = lsum;

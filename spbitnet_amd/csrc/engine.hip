@@ -42,9 +42,9 @@
 namespace spb {
 namespace {
 
-constexpr int kAttnChunk = 256;  // positions per attention split = threads per attention block
+constexpr int kAttnSplit = 64;    // positions per attention split (one per lane)
+constexpr int kAttnThreads = 256;
 constexpr int kAttnMaxGroup = 8;  // q heads per kv head
-constexpr int kAttnMaxHd = 128;   // head_dim limit (even)
 constexpr int kLmBlock = 256;
 constexpr int kLmMaxH = 8192;
 
@@ -126,6 +126,90 @@ __device__ __forceinline__ float inv_rms(float ss, int n, float eps) {
 }
 
 // ---- GEMV prologues: engine activations -> int8 bit planes ---------------------
+//
+// Vectors are handled in 16-byte units of 8 elements; thread t of a block of T
+// threads owns units t, t + T, t + 2T, ...  A pass issues the loads of up to
+// kUnits units before using any of them.  Sums of squares accumulate per
+// thread in unit order (element order inside a unit) with fma, then
+// block_sum: this "unit order" is what the oracle restates.
+
+constexpr int kUnits = 2;  // units per thread per pass
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4 r, float (&f)[8]) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        f[2 * k] = BF16::to_float(static_cast<uint16_t>(w[k] & 0xFFFFu));
+        f[2 * k + 1] = BF16::to_float(static_cast<uint16_t>(w[k] >> 16));
+    }
+}
+
+__device__ __forceinline__ void load_f8(const float* p, float (&f)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w, f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
+}
+
+__device__ __forceinline__ void store_f8(float* p, const float (&f)[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(f[0], f[1], f[2], f[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(f[4], f[5], f[6], f[7]);
+}
+
+// vec[i] = bf16((vec[i] * inv) * w[i]) over units (rms_norm_kernel's output
+// expression, inference_kernels.cu:53-55).
+template <int T>
+__device__ __forceinline__ void scale_by_weight(float* vec, const float* w, float inv, int units,
+                                                int tid) {
+    for (int base = 0; base < units; base += kUnits * T) {
+        float wf[kUnits][8];
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = base + tid + k * T;
+            if (u < units) load_f8(w + 8 * u, wf[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = base + tid + k * T;
+            if (u < units) {
+                float f[8];
+                load_f8(vec + 8 * u, f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) f[e] = bf16r((f[e] * inv) * wf[k][e]);
+                store_f8(vec + 8 * u, f);
+            }
+        }
+    }
+}
+
+// bf16 vector src -> vec (as float), returning this thread's sum of squares;
+// copy (nullable) receives the raw bf16 units.
+template <int T>
+__device__ __forceinline__ float load_bf16_sumsq(const uint16_t* src, float* vec, int units,
+                                                 int tid, uint16_t* copy) {
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+    float ss = 0.0f;
+    for (int base = 0; base < units; base += kUnits * T) {
+        uint4 r[kUnits];
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = base + tid + k * T;
+            if (u < units) r[k] = s4[u];
+        }
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = base + tid + k * T;
+            if (u < units) {
+                float f[8];
+                unpack_bf16x8(r[k], f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+                store_f8(vec + 8 * u, f);
+                if (copy) reinterpret_cast<uint4*>(copy)[u] = r[k];
+            }
+        }
+    }
+    return ss;
+}
 
 // Quantising source over a float vector in LDS (values already bf16-rounded).
 struct LdsQuantSrc {
@@ -142,23 +226,26 @@ struct LdsQuantSrc {
     }
 };
 
-// P::fill(vec, n, tid, red) writes the GEMV input (bf16-rounded, as float) to
-// vec[0..n); then absmax (reference absmax_reduce, inference_kernels.cu:120-148)
-// and the quantised bit planes.  Every block of the launch computes the same
-// values (same inputs, same order).
+// P::fill(vec, aux, n, tid, red, st) writes the GEMV input (bf16-rounded, as
+// float) to vec[0..n) (aux: P::kAux further floats of LDS per element); then
+// absmax (reference absmax_reduce, inference_kernels.cu:120-148) and the
+// quantised bit planes.  Every block of the launch computes the same values.
 template <class P>
 struct ProducerPlanes {
     P p;
     const EngineState* st;
     float amax;
-    static size_t extra_lds(int cols) { return static_cast<size_t>(cols) * 4 + 64; }
+    static size_t extra_lds(int cols) {
+        return static_cast<size_t>(cols) * 4 * (1 + P::kAux) + 64;
+    }
     __device__ bool skip() const { return st->done != 0; }
     __device__ void offset(long) {}
     __device__ void prepare() {}
     __device__ void build(uint32_t* planes, int cols, int tid, float* scratch) {
         float* vec = scratch;
-        float* red = scratch + cols;
-        p.fill(vec, cols, tid, red, st);
+        float* aux = scratch + cols;
+        float* red = scratch + cols * (1 + P::kAux);
+        p.fill(vec, aux, cols, tid, red, st);
         __syncthreads();
         float m = 0.0f;
         for (int i = tid; i < cols; i += kBlock) m = __builtin_fmaxf(m, __builtin_fabsf(vec[i]));
@@ -174,50 +261,55 @@ struct ProducerPlanes {
 // Reference: inference.cu:134-138, 147-153; rms_norm_kernel
 // (inference_kernels.cu:15-56): y = bf16((x * inv) * w).
 struct InputNorm {
+    static constexpr int kAux = 0;
     const uint16_t* x;
     const uint16_t* embed;  // non-null in layer 0
     const int* tokens;
     uint16_t* x_out;
     const float* w;
     float eps;
-    __device__ void fill(float* vec, int n, int tid, float* red, const EngineState* st) const {
+    __device__ void fill(float* vec, float*, int n, int tid, float* red,
+                         const EngineState* st) const {
         const uint16_t* src = x;
         if (embed) src = embed + static_cast<long>(tokens[st->pos]) * n;
-        float ss = 0.0f;
-        for (int i = tid; i < n; i += kBlock) {
-            const float v = BF16::to_float(src[i]);
-            vec[i] = v;
-            ss = __builtin_fmaf(v, v, ss);
-        }
-        if (embed && blockIdx.x == 0)
-            for (int i = tid; i < n; i += kBlock) x_out[i] = src[i];
+        const float ss = load_bf16_sumsq<kBlock>(src, vec, n >> 3, tid,
+                                                 embed && blockIdx.x == 0 ? x_out : nullptr);
         const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
-        for (int i = tid; i < n; i += kBlock) vec[i] = bf16r((vec[i] * inv) * w[i]);
+        scale_by_weight<kBlock>(vec, w, inv, n >> 3, tid);
     }
 };
 
 // Attention output: combine the splits of every head,
 //   M = max_s m_s, w_s = exp(m_s - M), out = (sum_s w_s acc_s) / (sum_s w_s l_s)
-// (s ascending, fused multiply-adds), rounded to bf16.
+// (s ascending, fused multiply-adds), rounded to bf16.  A unit (8 dims)
+// never straddles heads (head_dim % 8 == 0).
 struct AttnCombine {
+    static constexpr int kAux = 0;
     const float* pm;    // [nh][S]
     const float* pl;    // [nh][S]
     const float* pacc;  // [nh][S][hd]
-    int hd, S;
-    __device__ void fill(float* vec, int n, int tid, float*, const EngineState* st) const {
-        const int ns = (st->pos + kAttnChunk) / kAttnChunk;  // splits holding positions 0..pos
-        for (int i = tid; i < n; i += kBlock) {
-            const int h = i / hd, d = i - h * hd;
+    int hd, S, chunk;
+    __device__ void fill(float* vec, float*, int n, int tid, float*,
+                         const EngineState* st) const {
+        const int ns = st->pos / chunk + 1;  // splits holding positions 0..pos
+        const int units = n >> 3;
+        for (int u = tid; u < units; u += kBlock) {
+            const int h = (8 * u) / hd, d0 = 8 * u - h * hd;
             const float* m = pm + h * S;
             float M = m[0];
             for (int s = 1; s < ns; ++s) M = __builtin_fmaxf(M, m[s]);
-            float l = 0.0f, a = 0.0f;
+            float l = 0.0f, a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             for (int s = 0; s < ns; ++s) {
+                float p[8];
+                load_f8(pacc + (static_cast<long>(h) * S + s) * hd + d0, p);
                 const float w = exp_neg(m[s] - M);
                 l = __builtin_fmaf(w, pl[h * S + s], l);
-                a = __builtin_fmaf(w, pacc[(static_cast<long>(h) * S + s) * hd + d], a);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) a[e] = __builtin_fmaf(w, p[e], a[e]);
             }
-            vec[i] = bf16r(a / l);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = bf16r(a[e] / l);
+            store_f8(vec + 8 * u, a);
         }
     }
 };
@@ -226,31 +318,69 @@ struct AttnCombine {
 // x = bf16(o + r) (block 0 stores it as the new residual), then
 // RMSNorm(x; post_attention_layernorm).  Reference inference.cu:205-230.
 struct SubNormResidualNorm {
+    static constexpr int kAux = 1;
     const uint16_t* o;
     const uint16_t* res;
     uint16_t* x_out;
     const float* w_sub;
     const float* w_post;
     float eps;
-    __device__ void fill(float* vec, int n, int tid, float* red, const EngineState*) const {
+    __device__ void fill(float* vec, float* aux, int n, int tid, float* red,
+                         const EngineState*) const {
+        const int units = n >> 3;
+        // o -> vec (sum of squares), residual -> aux
         float ss = 0.0f;
-        for (int i = tid; i < n; i += kBlock) {
-            const float v = BF16::to_float(o[i]);
-            vec[i] = v;
-            ss = __builtin_fmaf(v, v, ss);
+        for (int base = 0; base < units; base += kUnits * kBlock) {
+            uint4 ro[kUnits], rr[kUnits];
+#pragma unroll
+            for (int k = 0; k < kUnits; ++k) {
+                const int u = base + tid + k * kBlock;
+                if (u < units) {
+                    ro[k] = reinterpret_cast<const uint4*>(o)[u];
+                    rr[k] = reinterpret_cast<const uint4*>(res)[u];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kUnits; ++k) {
+                const int u = base + tid + k * kBlock;
+                if (u < units) {
+                    float f[8], g[8];
+                    unpack_bf16x8(ro[k], f);
+                    unpack_bf16x8(rr[k], g);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+                    store_f8(vec + 8 * u, f);
+                    store_f8(aux + 8 * u, g);
+                }
+            }
         }
-        float inv = 1.0f;
-        if (w_sub) inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
+        if (w_sub) {
+            const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
+            scale_by_weight<kBlock>(vec, w_sub, inv, units, tid);
+        }
+        // x = bf16(o + r)
         float ss2 = 0.0f;
-        for (int i = tid; i < n; i += kBlock) {
-            const float on = w_sub ? bf16r((vec[i] * inv) * w_sub[i]) : vec[i];
-            const float x = bf16r(on + BF16::to_float(res[i]));
-            vec[i] = x;
-            ss2 = __builtin_fmaf(x, x, ss2);
-            if (blockIdx.x == 0) x_out[i] = BF16::from_float(x);
+        for (int u = tid; u < units; u += kBlock) {
+            float f[8], g[8];
+            load_f8(vec + 8 * u, f);
+            load_f8(aux + 8 * u, g);
+            uint32_t packed[4];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                f[e] = bf16r(f[e] + g[e]);
+                ss2 = __builtin_fmaf(f[e], f[e], ss2);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                packed[k] = static_cast<uint32_t>(BF16::from_float(f[2 * k])) |
+                            (static_cast<uint32_t>(BF16::from_float(f[2 * k + 1])) << 16);
+            store_f8(vec + 8 * u, f);
+            if (blockIdx.x == 0)
+                reinterpret_cast<uint4*>(x_out)[u] =
+                    make_uint4(packed[0], packed[1], packed[2], packed[3]);
         }
         const float inv2 = inv_rms(block_sum<kBlock>(ss2, red), n, eps);
-        for (int i = tid; i < n; i += kBlock) vec[i] = bf16r((vec[i] * inv2) * w_post[i]);
+        scale_by_weight<kBlock>(vec, w_post, inv2, units, tid);
     }
 };
 
@@ -258,23 +388,46 @@ struct SubNormResidualNorm {
 // inference_kernels.cu:399-410), then RMSNorm_f32in(m; ffn_sub_norm)
 // (:418-455) or a plain bf16 rounding when the norm is absent (:460-466).
 struct Relu2Norm {
+    static constexpr int kAux = 0;
     const uint16_t* g;
     const uint16_t* u;
     const float* w;
     float eps;
-    __device__ void fill(float* vec, int n, int tid, float* red, const EngineState*) const {
+    __device__ void fill(float* vec, float*, int n, int tid, float* red,
+                         const EngineState*) const {
+        const int units = n >> 3;
         float ss = 0.0f;
-        for (int i = tid; i < n; i += kBlock) {
-            const float r = __builtin_fmaxf(0.0f, BF16::to_float(g[i]));
-            const float m = (r * r) * BF16::to_float(u[i]);
-            vec[i] = m;
-            ss = __builtin_fmaf(m, m, ss);
+        for (int base = 0; base < units; base += kUnits * kBlock) {
+            uint4 rg[kUnits], ru[kUnits];
+#pragma unroll
+            for (int k = 0; k < kUnits; ++k) {
+                const int q = base + tid + k * kBlock;
+                if (q < units) {
+                    rg[k] = reinterpret_cast<const uint4*>(g)[q];
+                    ru[k] = reinterpret_cast<const uint4*>(u)[q];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kUnits; ++k) {
+                const int q = base + tid + k * kBlock;
+                if (q < units) {
+                    float fg[8], fu[8];
+                    unpack_bf16x8(rg[k], fg);
+                    unpack_bf16x8(ru[k], fu);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float r = __builtin_fmaxf(0.0f, fg[e]);
+                        fg[e] = (r * r) * fu[e];
+                        ss = __builtin_fmaf(fg[e], fg[e], ss);
+                        if (!w) fg[e] = bf16r(fg[e]);  // no sub-norm: plain rounding
+                    }
+                    store_f8(vec + 8 * q, fg);
+                }
+            }
         }
         if (w) {
             const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
-            for (int i = tid; i < n; i += kBlock) vec[i] = bf16r((vec[i] * inv) * w[i]);
-        } else {
-            for (int i = tid; i < n; i += kBlock) vec[i] = bf16r(vec[i]);
+            scale_by_weight<kBlock>(vec, w, inv, units, tid);
         }
     }
 };
@@ -324,50 +477,53 @@ struct ResidualSink {
 
 // ---- attention -----------------------------------------------------------------------
 
-// One block per (256-position split s, kv head): RoPE of the group's q heads
+// One block per (64-position split s, kv head): RoPE of the group's q heads
 // and (in the split holding pos) of k, KV-cache write of k and v at pos,
-// scores, per-split softmax numerator and the unnormalised weighted sum of V.
-//   score_j = (sum over lanes l of fma(q[2l+1], k[2l+1], q[2l] * k[2l]),
-//              butterfly order) * scale
-//   m = max_j score_j, e_j = exp(score_j - m), l = block_sum(e) (thread t
-//   holds position j0 + t), acc[d] = sum_j e_j v_j[d] (j ascending, fma).
+// scores, the split's softmax numerator and unnormalised weighted sum of V.
+//   score_j = (sum over d ascending of fma(q[d], k_j[d], .)) * scale
+//   per head: m = max_j score_j, e_j = exp(score_j - m),
+//   l = butterfly sum of e over the 64 lanes (lane = position in the split),
+//   acc[d] = sum_j e_j v_j[d] (j ascending, fma).
 // rope: [max_seq][hd/2] (cos, sin) of angle pos * theta^(-2i/hd).
 // Reference: rope_kernel, scatter_kv, attention_scores, softmax,
 // attention_output (inference_kernels.cu:185-371), GQA kv = h * nkv / nh.
-__global__ __launch_bounds__(kAttnChunk) void attention_kernel(
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     const uint16_t* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
     const float2* __restrict__ rope, float* __restrict__ pm, float* __restrict__ pl,
-    float* __restrict__ pacc, const EngineState* __restrict__ st, int nh, int nkv, int hd,
-    int max_seq, int S, float scale) {
-    __shared__ float qs[kAttnMaxGroup][kAttnMaxHd];
-    __shared__ float kn[kAttnMaxHd], vn[kAttnMaxHd];
-    __shared__ float sc[kAttnMaxGroup][kAttnChunk];
-    __shared__ float red[kAttnChunk / kWave];
+    float* __restrict__ pacc, const EngineState* __restrict__ st, int nh, int nkv, int max_seq,
+    int S, float scale) {
+    constexpr int kHalf = HD / 2, kU = HD / 8;
+    __shared__ float qs[kAttnMaxGroup][HD];
+    __shared__ float kn[HD];
+    __shared__ __align__(16) float vs[kAttnSplit][HD];
+    __shared__ float sc[kAttnMaxGroup][kAttnSplit];
+    __shared__ float hmax[kAttnMaxGroup], hsum[kAttnMaxGroup];
     if (st->done) return;
     const int pos = st->pos;
     const int s = blockIdx.x, kvh = blockIdx.y;
-    const int j0 = s * kAttnChunk;
+    const int j0 = s * kAttnSplit;
     if (j0 > pos) return;
-    const int jn = (pos + 1 - j0) < kAttnChunk ? (pos + 1 - j0) : kAttnChunk;
+    const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
     const bool has_pos = j0 + jn - 1 == pos;
     const int G = nh / nkv;
-    const int half = hd >> 1;
-    const int tid = threadIdx.x;
-    const float2* rp = rope + static_cast<long>(pos) * half;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const float2* rp = rope + static_cast<long>(pos) * kHalf;
+    const uint16_t* vh = qkv + (nh + nkv) * HD + kvh * HD;
+    const long cache0 = static_cast<long>(kvh) * max_seq * HD;
 
-    for (int idx = tid; idx < G * half; idx += kAttnChunk) {
-        const int g = idx / half, i = idx - g * half;
-        const uint16_t* qh = qkv + (kvh * G + g) * hd;
+    for (int idx = tid; idx < G * kHalf; idx += kAttnThreads) {
+        const int g = idx / kHalf, i = idx - g * kHalf;
+        const uint16_t* qh = qkv + (kvh * G + g) * HD;
         const float x0 = BF16::to_float(qh[2 * i]), x1 = BF16::to_float(qh[2 * i + 1]);
         const float2 cs = rp[i];
         qs[g][2 * i] = bf16r(x0 * cs.x - x1 * cs.y);
         qs[g][2 * i + 1] = bf16r(x0 * cs.y + x1 * cs.x);
     }
     if (has_pos) {
-        const uint16_t* kh = qkv + nh * hd + kvh * hd;
-        const uint16_t* vh = qkv + (nh + nkv) * hd + kvh * hd;
-        const long at = (static_cast<long>(kvh) * max_seq + pos) * hd;
-        for (int i = tid; i < half; i += kAttnChunk) {
+        const uint16_t* kh = qkv + nh * HD + kvh * HD;
+        const long at = cache0 + static_cast<long>(pos) * HD;
+        for (int i = tid; i < kHalf; i += kAttnThreads) {
             const float x0 = BF16::to_float(kh[2 * i]), x1 = BF16::to_float(kh[2 * i + 1]);
             const float2 cs = rp[i];
             const uint16_t k0 = BF16::from_float(x0 * cs.x - x1 * cs.y);
@@ -377,63 +533,66 @@ __global__ __launch_bounds__(kAttnChunk) void attention_kernel(
             kc[at + 2 * i] = k0;
             kc[at + 2 * i + 1] = k1;
         }
-        for (int d = tid; d < hd; d += kAttnChunk) {
-            vn[d] = BF16::to_float(vh[d]);
-            vc[at + d] = vh[d];
-        }
+        for (int d = tid; d < HD; d += kAttnThreads) vc[at + d] = vh[d];
+    }
+    // V rows of the split -> LDS (the row at pos straight from this step's v)
+    for (int idx = tid; idx < jn * kU; idx += kAttnThreads) {
+        const int jj = idx / kU, c = idx - jj * kU;
+        const int j = j0 + jj;
+        const uint4 r = j == pos ? reinterpret_cast<const uint4*>(vh)[c]
+                                 : reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
+        float f[8];
+        unpack_bf16x8(r, f);
+        store_f8(&vs[jj][8 * c], f);
     }
     __syncthreads();
 
-    // scores: wave w takes positions j0 + w, j0 + w + 4, ...; lane l dims 2l, 2l+1
-    const int lane = tid & (kWave - 1), wave = tid / kWave;
-    const bool lane_on = 2 * lane < hd;
-    for (int jj = wave; jj < jn; jj += kAttnChunk / kWave) {
-        const int j = j0 + jj;
-        float k0 = 0.0f, k1 = 0.0f;
-        if (lane_on) {
-            if (j == pos) {
-                k0 = kn[2 * lane];
-                k1 = kn[2 * lane + 1];
-            } else {
-                const uint32_t kk = *reinterpret_cast<const uint32_t*>(
-                    kc + (static_cast<long>(kvh) * max_seq + j) * hd + 2 * lane);
-                k0 = BF16::to_float(static_cast<uint16_t>(kk & 0xFFFFu));
-                k1 = BF16::to_float(static_cast<uint16_t>(kk >> 16));
+    // scores: lane = position, wave w takes heads w, w + 4
+    if (lane < jn) {
+        const int j = j0 + lane;
+        float k[HD];
+        if (j == pos) {
+#pragma unroll
+            for (int d = 0; d < HD; ++d) k[d] = kn[d];
+        } else {
+            const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD);
+            uint4 raw[kU];
+#pragma unroll
+            for (int c = 0; c < kU; ++c) raw[c] = kr[c];
+#pragma unroll
+            for (int c = 0; c < kU; ++c) {
+                float f[8];
+                unpack_bf16x8(raw[c], f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) k[8 * c + e] = f[e];
             }
         }
-        for (int g = 0; g < G; ++g) {
-            float p = lane_on ? __builtin_fmaf(qs[g][2 * lane + 1], k1, qs[g][2 * lane] * k0) : 0.0f;
-            p = wave_sum_bfly(p);
-            if (lane == 0) sc[g][jj] = p * scale;
+        for (int g = wave; g < G; g += kAttnThreads / kWave) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int d = 0; d < HD; ++d) acc = __builtin_fmaf(qs[g][d], k[d], acc);
+            sc[g][lane] = acc * scale;
         }
     }
     __syncthreads();
-
-    __shared__ float hmax[kAttnMaxGroup], hsum[kAttnMaxGroup];
-    for (int g = 0; g < G; ++g) {
-        const float v = tid < jn ? sc[g][tid] : -INFINITY;
-        const float m = block_max<kAttnChunk>(v, red);
-        const float e = tid < jn ? exp_neg(v - m) : 0.0f;
-        const float l = block_sum<kAttnChunk>(e, red);
-        if (tid < jn) sc[g][tid] = e;
-        if (tid == 0) {
+    for (int g = wave; g < G; g += kAttnThreads / kWave) {
+        const float v = lane < jn ? sc[g][lane] : -INFINITY;
+        const float m = wave_max(v);
+        const float e = lane < jn ? exp_neg(v - m) : 0.0f;
+        const float l = wave_sum_bfly(e);
+        sc[g][lane] = e;
+        if (lane == 0) {
             hmax[g] = m;
             hsum[g] = l;
         }
     }
     __syncthreads();
-
-    for (int o = tid; o < G * hd; o += kAttnChunk) {
-        const int g = o / hd, d = o - g * hd;
-        const uint16_t* vcol = vc + static_cast<long>(kvh) * max_seq * hd + d;
+    for (int o = tid; o < G * HD; o += kAttnThreads) {
+        const int g = o / HD, d = o - g * HD;
         float acc = 0.0f;
-        for (int jj = 0; jj < jn; ++jj) {
-            const int j = j0 + jj;
-            const float v = j == pos ? vn[d] : BF16::to_float(vcol[static_cast<long>(j) * hd]);
-            acc = __builtin_fmaf(sc[g][jj], v, acc);
-        }
+        for (int jj = 0; jj < jn; ++jj) acc = __builtin_fmaf(sc[g][jj], vs[jj][d], acc);
         const int h = kvh * G + g;
-        pacc[(static_cast<long>(h) * S + s) * hd + d] = acc;
+        pacc[(static_cast<long>(h) * S + s) * HD + d] = acc;
         if (d == 0) {
             pm[h * S + s] = hmax[g];
             pl[h * S + s] = hsum[g];
@@ -443,19 +602,21 @@ __global__ __launch_bounds__(kAttnChunk) void attention_kernel(
 
 // ---- LM head + greedy argmax ------------------------------------------------------------
 
-// Final RMSNorm (block-sum order over kLmBlock threads), then
+// Final RMSNorm (unit order over kLmBlock threads), then
 // logits[r] = sum_c W[r][c] * xn[c] in fp32: lane l of the row's wave takes
 // the 8-element chunks l, l+64, ... (fma in element order), then the
-// butterfly.  Argmax = lowest index among the maxima (std::max_element,
+// butterfly.  Each wave keeps RR rows (NC 16-byte chunks per lane each) in
+// flight.  Argmax = lowest index among the maxima (std::max_element,
 // src/main.cpp:194-200).  The last block to finish reduces the per-block
 // maxima and advances the decode state.  Reference half_gemv_kernel
 // (inference_kernels.cu:488-531) with fp16 -> bf16 weights.
+template <int NC, int RR>
 __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
     const float* __restrict__ wn, float eps, float* __restrict__ logits,
     float* __restrict__ part_v, int* __restrict__ part_i, EngineState* __restrict__ st,
     int* __restrict__ tokens, int V, int H) {
-    __shared__ float xs[kLmMaxH];
+    __shared__ __align__(16) float xs[kLmMaxH];
     __shared__ float red[kLmBlock / kWave];
     __shared__ float wv[kLmBlock / kWave];
     __shared__ int wi[kLmBlock / kWave];
@@ -463,40 +624,51 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     if (st->done) return;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
 
-    float ss = 0.0f;
-    for (int i = tid; i < H; i += kLmBlock) {
-        const float v = BF16::to_float(x[i]);
-        xs[i] = v;
-        ss = __builtin_fmaf(v, v, ss);
-    }
+    const float ss = load_bf16_sumsq<kLmBlock>(x, xs, H >> 3, tid, nullptr);
     const float inv = inv_rms(block_sum<kLmBlock>(ss, red), H, eps);
-    for (int i = tid; i < H; i += kLmBlock) xs[i] = bf16r((xs[i] * inv) * wn[i]);
+    scale_by_weight<kLmBlock>(xs, wn, inv, H >> 3, tid);
     __syncthreads();
 
     const int nch = H >> 3;
     const long waves = static_cast<long>(gridDim.x) * (kLmBlock / kWave);
     float best = -INFINITY;
     int best_i = 0x7FFFFFFF;
-    for (long r = static_cast<long>(blockIdx.x) * (kLmBlock / kWave) + wave; r < V; r += waves) {
-        const uint4* wr = reinterpret_cast<const uint4*>(W + r * H);
-        float acc = 0.0f;
-        for (int c = lane; c < nch; c += kWave) {
-            const uint4 w = wr[c];
-            const float* xv = xs + 8 * c;
-            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    for (long r0 = static_cast<long>(blockIdx.x) * (kLmBlock / kWave) + wave; r0 < V;
+         r0 += RR * waves) {
+        uint4 w[RR][NC];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                acc = __builtin_fmaf(BF16::to_float(static_cast<uint16_t>(ww[k] & 0xFFFFu)),
-                                     xv[2 * k], acc);
-                acc = __builtin_fmaf(BF16::to_float(static_cast<uint16_t>(ww[k] >> 16)),
-                                     xv[2 * k + 1], acc);
+        for (int q = 0; q < RR; ++q) {
+            const long r = r0 + q * waves;
+            const uint4* wr = reinterpret_cast<const uint4*>(W + r * H);
+#pragma unroll
+            for (int k = 0; k < NC; ++k) {
+                const int c = lane + k * kWave;
+                w[q][k] = (r < V && c < nch) ? wr[c] : make_uint4(0, 0, 0, 0);
             }
         }
-        acc = wave_sum_bfly(acc);
-        if (lane == 0) logits[r] = acc;
-        if (acc > best) {  // rows ascend within a wave: strict > keeps the first maximum
-            best = acc;
-            best_i = static_cast<int>(r);
+#pragma unroll
+        for (int q = 0; q < RR; ++q) {
+            const long r = r0 + q * waves;
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NC; ++k) {
+                const int c = lane + k * kWave;
+                if (c < nch) {
+                    float f[8], xv[8];
+                    unpack_bf16x8(w[q][k], f);
+                    load_f8(xs + 8 * c, xv);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(f[e], xv[e], acc);
+                }
+            }
+            acc = wave_sum_bfly(acc);
+            if (r < V) {
+                if (lane == 0) logits[r] = acc;
+                if (acc > best) {  // rows ascend within a wave: strict > keeps the first maximum
+                    best = acc;
+                    best_i = static_cast<int>(r);
+                }
+            }
         }
     }
     if (lane == 0) {
@@ -561,6 +733,33 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
         st->pos = nxt;
         if (nxt >= st->limit) st->done = 1;
         st->ticket = 0u;
+    }
+}
+
+typedef void (*LmKernel)(const uint16_t*, const uint16_t*, const float*, float, float*, float*,
+                         int*, EngineState*, int*, int, int);
+
+// Instantiation for H: NC = ceil(H / 512) chunks per lane (H <= 8192).
+LmKernel lm_head_for(int H, int* rows_in_flight) {
+    const int nc = (H / 8 + kWave - 1) / kWave;
+    *rows_in_flight = nc <= 4 ? 4 : (nc <= 8 ? 2 : 1);
+    switch (nc) {
+        case 1: return lm_head_kernel<1, 4>;
+        case 2: return lm_head_kernel<2, 4>;
+        case 3: return lm_head_kernel<3, 4>;
+        case 4: return lm_head_kernel<4, 4>;
+        case 5: return lm_head_kernel<5, 2>;
+        case 6: return lm_head_kernel<6, 2>;
+        case 7: return lm_head_kernel<7, 2>;
+        case 8: return lm_head_kernel<8, 2>;
+        case 9: return lm_head_kernel<9, 1>;
+        case 10: return lm_head_kernel<10, 1>;
+        case 11: return lm_head_kernel<11, 1>;
+        case 12: return lm_head_kernel<12, 1>;
+        case 13: return lm_head_kernel<13, 1>;
+        case 14: return lm_head_kernel<14, 1>;
+        case 15: return lm_head_kernel<15, 1>;
+        default: return lm_head_kernel<16, 1>;
     }
 }
 
@@ -703,6 +902,7 @@ struct spb_engine {
     int max_seq = 0;
     int S = 0;  // attention splits
     int lm_grid = 0;
+    LmKernel lm_kernel = nullptr;
     std::vector<void*> owned;
     std::vector<uint16_t*> kcache, vcache;
     uint16_t *xa = nullptr, *xb = nullptr, *qkv = nullptr, *obuf = nullptr, *gu = nullptr;
@@ -739,11 +939,16 @@ struct spb_engine {
                 launch_bitplane(seg_weights(&L.q_proj, &L.k_proj, &L.v_proj),
                                 ProducerPlanes<InputNorm>{p, st, 0.f}, sink, s);
             }
-            hipLaunchKernelGGL(attention_kernel, dim3(S, nkv), dim3(kAttnChunk), 0, s, qkv,
-                               kcache[l], vcache[l], rope, pm, pl, pacc, st, nh, nkv, hd, max_seq,
-                               S, scale);
+            if (hd == 64)
+                hipLaunchKernelGGL(attention_kernel<64>, dim3(S, nkv), dim3(kAttnThreads), 0, s,
+                                   qkv, kcache[l], vcache[l], rope, pm, pl, pacc, st, nh, nkv,
+                                   max_seq, S, scale);
+            else
+                hipLaunchKernelGGL(attention_kernel<128>, dim3(S, nkv), dim3(kAttnThreads), 0, s,
+                                   qkv, kcache[l], vcache[l], rope, pm, pl, pacc, st, nh, nkv,
+                                   max_seq, S, scale);
             {
-                AttnCombine p{pm, pl, pacc, hd, S};
+                AttnCombine p{pm, pl, pacc, hd, S, kAttnSplit};
                 SegBf16Sink sink{obuf, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma,
                                  L.o_proj.rows, L.o_proj.rows, 0.f, 0.f, 0.f};
                 launch_bitplane(single_weights(L.o_proj), ProducerPlanes<AttnCombine>{p, st, 0.f},
@@ -766,7 +971,7 @@ struct spb_engine {
                                 sink, s);
             }
         }
-        hipLaunchKernelGGL(lm_head_kernel, dim3(lm_grid), dim3(kLmBlock), 0, s, lm_head, xa,
+        hipLaunchKernelGGL(lm_kernel, dim3(lm_grid), dim3(kLmBlock), 0, s, lm_head, xa,
                            final_norm, eps, logits, part_v, part_i, st, tokens,
                            cfg.vocab_size, cfg.hidden_size);
     }
@@ -822,8 +1027,7 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
     if (nh % nkv || nh / nkv > kAttnMaxGroup)
         return invalid("%s: heads per kv head must divide evenly and be <= %d", fn,
                        kAttnMaxGroup);
-    if (hd % 2 || hd > kAttnMaxHd) return invalid("%s: head_dim must be even and <= %d", fn,
-                                                  kAttnMaxHd);
+    if (hd != 64 && hd != 128) return invalid("%s: head_dim must be 64 or 128", fn);
     if (H > kLmMaxH || H % 8) return invalid("%s: hidden_size must be a multiple of 8, <= %d", fn,
                                              kLmMaxH);
     if (max_seq <= 0 || max_seq > cfg->max_position_embeddings)
@@ -853,9 +1057,11 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
     e->lm_head = lm_head ? lm_head : embed_tokens;  // tied weights (model.h:131-133)
     e->final_norm = final_norm;
     e->max_seq = max_seq;
-    e->S = (max_seq + kAttnChunk - 1) / kAttnChunk;
+    e->S = (max_seq + kAttnSplit - 1) / kAttnSplit;
+    int rr = 1;
+    e->lm_kernel = lm_head_for(H, &rr);
     int resident = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, lm_head_kernel, kLmBlock, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, e->lm_kernel, kLmBlock, 0) !=
             hipSuccess ||
         resident <= 0)
         resident = 1;
