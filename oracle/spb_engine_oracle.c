@@ -14,12 +14,12 @@
  * for bit and greedy token ids agree exactly:
  *   block sums over T threads: thread t accumulates the 8-element units
  *     t, t+T, ... (fma(v, v, acc) for sums of squares, element order inside
- *     a unit), then per 64-thread wave the butterfly at distances 32..1,
- *     then the wave totals in wave order;
- *   attention scores: fma over d ascending; softmax sums: butterfly over the
- *     64 positions of a split;
+ *     a unit), then per 64-thread wave the pairwise tree over adjacent
+ *     lanes, then the wave totals in wave order;
+ *   attention scores: fma over d ascending; softmax sums: the 64-lane tree
+ *     over the positions of a split;
  *   LM head: lane l accumulates the 8-element chunks l, l+64, ... with fma in
- *     element order, butterfly over 64 lanes;
+ *     element order, then the 64-lane tree;
  *   1/sqrt with correctly rounded divide and sqrt (reference: rsqrtf);
  *   exp of softmax by exp_neg() below (reference: expf).
  * These differ from the reference's CUDA order only by float32 rounding,
@@ -53,21 +53,21 @@ static float bf2f(uint16_t b) {
 }
 static float bfr(float f) { return bf2f(spbo_bf16_round(f)); }
 
-/* Butterfly over 64 lanes: distance 32, 16, ..., 1; returns lane 0's value. */
-static float bfly64(float* a) {
+/* Sum over 64 lanes as the balanced pairwise tree over adjacent lanes
+ * (lanes 2i and 2i+1, then pairs of pairs, ...). */
+static float tree64(const float* a) {
     float t[64];
-    for (int off = 32; off > 0; off >>= 1) {
-        for (int l = 0; l < 64; ++l) t[l] = a[l] + a[l ^ off];
-        memcpy(a, t, sizeof(t));
-    }
-    return a[0];
+    memcpy(t, a, sizeof(t));
+    for (int n = 32; n >= 1; n >>= 1)
+        for (int i = 0; i < n; ++i) t[i] = t[2 * i] + t[2 * i + 1];
+    return t[0];
 }
 
 /* Block sum over T threads of per-thread partials p[0..T). */
 static float block_sum(float* p, int T) {
     float s = 0.0f;
     for (int w = 0; w < T / 64; ++w) {
-        float v = bfly64(p + 64 * w);
+        float v = tree64(p + 64 * w);
         s = (w == 0) ? v : s + v;
     }
     return s;
@@ -300,7 +300,7 @@ static void attention(spbo_engine* e, int l) {
                     p[t] = t < jn ? spbo_exp_neg(sc[g][t] - m) : 0.0f;
                     if (t < jn) sc[g][t] = p[t];
                 }
-                const float lsum = bfly64(p);
+                const float lsum = tree64(p);
                 const int h = kvh * G + g;
                 pm[h * S + s] = m;
                 pl[h * S + s] = lsum;
@@ -403,7 +403,7 @@ int spbo_engine_step(spbo_engine* e, int token, float* logits) {
                 for (int k = 0; k < 8; ++k) a = fmaf(bf2f(w[8 * c + k]), vec[8 * c + k], a);
             lanes[ln] = a;
         }
-        const float lg = bfly64(lanes);
+        const float lg = tree64(lanes);
         if (logits) logits[r] = lg;
         if (lg > bv) {
             bv = lg;

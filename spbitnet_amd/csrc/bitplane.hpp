@@ -200,8 +200,13 @@ struct BuildPlanes {
     // Transposes the activations, 8 columns per thread, into LDS planes
     // (bytes of word [w*8+b]).  The loads of up to two units are issued
     // before either is transposed.
+    struct Regs {};
     static size_t extra_lds(int) { return 0; }
     __device__ bool skip() const { return false; }
+    __device__ void issue(int, Regs&) {}
+    __device__ void build(uint32_t* planes, int cols, int tid, float* s, Regs&) const {
+        build(planes, cols, tid, s);
+    }
     __device__ void build(uint32_t* planes, int cols, int tid, float*) const {
         const int units = cols >> 3;
         uint8_t* pb = reinterpret_cast<uint8_t*>(planes);
@@ -239,9 +244,11 @@ struct GlobalPlanes {
     const uint32_t* p;
     __device__ void offset(long) {}
     __device__ void prepare() {}
+    struct Regs {};
     static size_t extra_lds(int) { return 0; }
     __device__ bool skip() const { return false; }
-    __device__ void build(uint32_t* planes, int cols, int tid, float*) const {
+    __device__ void issue(int, Regs&) {}
+    __device__ void build(uint32_t* planes, int cols, int tid, float*, Regs&) const {
         const uint4* src = reinterpret_cast<const uint4*>(p);
         uint4* dst = reinterpret_cast<uint4*>(planes);
         for (int i = tid; i < (cols >> 4); i += kBlock) dst[i] = src[i];
@@ -341,8 +348,10 @@ __device__ __forceinline__ void load_x(const uint32_t* src, uint32_t (&X)[4][8])
 // tiles, so one barrier per tile orders accumulation and write-out.
 //
 // Act (activation planes) and Sink (output epilogue) are policies:
-//   act.skip() (uniform early exit), act.prepare(),
-//   act.build(planes, cols, tid, scratch)  -- scratch: the
+//   act.skip() (uniform early exit), act.issue(tid, regs) (loads issued
+//   before the first weight loads into Act::Regs, a kernel-local register
+//   block), act.prepare(), act.build(planes, cols, tid, scratch, regs)
+//   -- scratch: the
 //   Act::extra_lds(cols) bytes of LDS after the row sums;
 //   sink.prepare() before the prologue, sink.bind(act) after it (a sink may
 //   take a scale the prologue computed), sink.store(row, acc).
@@ -373,13 +382,15 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Si
 
     act.offset(blockIdx.y);
     sink.offset(blockIdx.y);
+    typename Act::Regs regs;
+    act.issue(tid, regs);  // activation loads first: they head the critical path
     ChunkLoad cur = wt.load(row, c, active);
     act.prepare();
     sink.prepare();
     uint32_t X[4][8];
     // prologue scratch after the row sums, 16-byte aligned
     act.build(planes, wt.cols, tid,
-              reinterpret_cast<float*>(smem + ((8 * nwords + 2 * tile_rows + 3) & ~3)));
+              reinterpret_cast<float*>(smem + ((8 * nwords + 2 * tile_rows + 3) & ~3)), regs);
     for (int i = tid; i < 2 * tile_rows; i += kBlock) acc0[i] = 0;
     __syncthreads();
     sink.bind(act);

@@ -63,39 +63,65 @@ struct EngineState {
 
 __device__ __forceinline__ float bf16r(float f) { return BF16::to_float(BF16::from_float(f)); }
 
-// Butterfly sum over the 64 lanes: at distance d = 32, 16, ..., 1 every lane
-// adds its partner's value (lane ^ d).  Each pair computes the same sum, so
-// all lanes finish with identical bits.
-__device__ __forceinline__ float wave_sum_bfly(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+// Sum over the 64 lanes as the balanced pairwise tree over adjacent lanes
+// (lanes 2i and 2i+1 first, then pairs of pairs, ...): DPP steps inside each
+// 16-lane row (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror: each adds the partner group's partial sum), then the four row
+// sums as (r0 + r1) + (r2 + r3).  Every lane gets the same value.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
 }
 
-// Sum over a block of kThreads threads: the wave butterfly, then the wave
-// totals added in wave order (w0 + w1) + w2 ...  red: kThreads/64 floats of
-// LDS.  Every thread returns the same value.
+__device__ __forceinline__ float wave_sum_tree(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// Maximum over the 64 lanes (exact in any order), same pattern.
+__device__ __forceinline__ float wave_max_tree(float v) {
+    v = __builtin_fmaxf(v, dpp_f<0xB1>(v));
+    v = __builtin_fmaxf(v, dpp_f<0x4E>(v));
+    v = __builtin_fmaxf(v, dpp_f<0x141>(v));
+    v = __builtin_fmaxf(v, dpp_f<0x140>(v));
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return __builtin_fmaxf(__builtin_fmaxf(r0, r1), __builtin_fmaxf(r2, r3));
+}
+
+// Sum over a block of kThreads threads: the wave tree, then the wave
+// totals added in wave order (w0 + w1) + w2 ...  slot: kThreads/64 floats of
+// LDS that no other reduction of the same kernel phase uses (so one barrier
+// suffices).  Every thread returns the same value.
 template <int kThreads>
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum_bfly(v);
-    __syncthreads();  // red may still be read by a previous reduction
-    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+__device__ __forceinline__ float block_sum(float v, float* slot) {
+    v = wave_sum_tree(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) slot[threadIdx.x / kWave] = v;
     __syncthreads();
-    float s = red[0];
+    float s = slot[0];
 #pragma unroll
-    for (int w = 1; w < kThreads / kWave; ++w) s += red[w];
+    for (int w = 1; w < kThreads / kWave; ++w) s += slot[w];
     return s;
 }
 
 template <int kThreads>
-__device__ __forceinline__ float block_max(float v, float* red) {
-    v = wave_max(v);
+__device__ __forceinline__ float block_max(float v, float* slot) {
+    v = wave_max_tree(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) slot[threadIdx.x / kWave] = v;
     __syncthreads();
-    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
-    __syncthreads();
-    float s = red[0];
+    float s = slot[0];
 #pragma unroll
-    for (int w = 1; w < kThreads / kWave; ++w) s = __builtin_fmaxf(s, red[w]);
+    for (int w = 1; w < kThreads / kWave; ++w) s = __builtin_fmaxf(s, slot[w]);
     return s;
 }
 
@@ -156,10 +182,12 @@ __device__ __forceinline__ void store_f8(float* p, const float (&f)[8]) {
 }
 
 // vec[i] = bf16((vec[i] * inv) * w[i]) over units (rms_norm_kernel's output
-// expression, inference_kernels.cu:53-55).
+// expression, inference_kernels.cu:53-55); returns max |result| of the
+// thread's elements.
 template <int T>
-__device__ __forceinline__ void scale_by_weight(float* vec, const float* w, float inv, int units,
-                                                int tid) {
+__device__ __forceinline__ float scale_by_weight(float* vec, const float* w, float inv, int units,
+                                                 int tid) {
+    float m = 0.0f;
     for (int base = 0; base < units; base += kUnits * T) {
         float wf[kUnits][8];
 #pragma unroll
@@ -174,18 +202,72 @@ __device__ __forceinline__ void scale_by_weight(float* vec, const float* w, floa
                 float f[8];
                 load_f8(vec + 8 * u, f);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) f[e] = bf16r((f[e] * inv) * wf[k][e]);
+                for (int e = 0; e < 8; ++e) {
+                    f[e] = bf16r((f[e] * inv) * wf[k][e]);
+                    m = __builtin_fmaxf(m, __builtin_fabsf(f[e]));
+                }
                 store_f8(vec + 8 * u, f);
             }
         }
     }
+    return m;
 }
 
+// Norm weights of the thread's units, loaded together with the activations
+// when the vector fits one pass (units <= kUnits * T), else read at use.
+template <int T>
+struct HeldWeights {
+    float f[kUnits][8];
+    __device__ void load(const float* w, int units, int tid) {
+        if (units > kUnits * T) return;
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = tid + k * T;
+            if (u < units) load_f8(w + 8 * u, f[k]);
+        }
+    }
+    __device__ float apply(float* vec, const float* w, float inv, int units, int tid) const {
+        if (units > kUnits * T) return scale_by_weight<T>(vec, w, inv, units, tid);
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = tid + k * T;
+            if (u < units) {
+                float v[8];
+                load_f8(vec + 8 * u, v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    v[e] = bf16r((v[e] * inv) * f[k][e]);
+                    m = __builtin_fmaxf(m, __builtin_fabsf(v[e]));
+                }
+                store_f8(vec + 8 * u, v);
+            }
+        }
+        return m;
+    }
+};
+
+// The first pass of a bf16 vector's units, loaded into registers.
+template <int T>
+struct HeldUnits {
+    uint4 r[kUnits];
+    __device__ void load(const uint16_t* src, int units, int tid) {
+        const uint4* s4 = reinterpret_cast<const uint4*>(src);
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = tid + k * T;
+            if (u < units) r[k] = s4[u];
+        }
+    }
+};
+
 // bf16 vector src -> vec (as float), returning this thread's sum of squares;
-// copy (nullable) receives the raw bf16 units.
+// copy (nullable) receives the raw bf16 units.  first: the first pass,
+// already loaded.
 template <int T>
 __device__ __forceinline__ float load_bf16_sumsq(const uint16_t* src, float* vec, int units,
-                                                 int tid, uint16_t* copy) {
+                                                 int tid, uint16_t* copy,
+                                                 const HeldUnits<T>& first) {
     const uint4* s4 = reinterpret_cast<const uint4*>(src);
     float ss = 0.0f;
     for (int base = 0; base < units; base += kUnits * T) {
@@ -193,7 +275,10 @@ __device__ __forceinline__ float load_bf16_sumsq(const uint16_t* src, float* vec
 #pragma unroll
         for (int k = 0; k < kUnits; ++k) {
             const int u = base + tid + k * T;
-            if (u < units) r[k] = s4[u];
+            if (base == 0)
+                r[k] = first.r[k];
+            else if (u < units)
+                r[k] = s4[u];
         }
 #pragma unroll
         for (int k = 0; k < kUnits; ++k) {
@@ -226,30 +311,36 @@ struct LdsQuantSrc {
     }
 };
 
-// P::fill(vec, aux, n, tid, red, st) writes the GEMV input (bf16-rounded, as
-// float) to vec[0..n) (aux: P::kAux further floats of LDS per element); then
-// absmax (reference absmax_reduce, inference_kernels.cu:120-148) and the
-// quantised bit planes.  Every block of the launch computes the same values.
+constexpr int kRedSlot = 16;  // floats per reduction slot (>= kBlock / 64)
+
+// P::issue(tid, st) issues the first pass of loads into registers (before the
+// GEMV's weight loads); P::fill(vec, aux, n, tid, red, st) writes the GEMV input (bf16-rounded, as
+// float) to vec[0..n) (aux: P::kAux further floats of LDS per element; red:
+// reduction slots 0 and 1) and returns max |value| over the thread's
+// elements; then absmax (reference absmax_reduce, inference_kernels.cu:120-148)
+// and the quantised bit planes.  Every block of the launch computes the same
+// values.  The GEMVs run even after the decode state is done (their reads
+// stay in bounds and their outputs are scratch), so no kernel waits on the
+// state before its first loads.
 template <class P>
 struct ProducerPlanes {
     P p;
     const EngineState* st;
     float amax;
     static size_t extra_lds(int cols) {
-        return static_cast<size_t>(cols) * 4 * (1 + P::kAux) + 64;
+        return static_cast<size_t>(cols) * 4 * (1 + P::kAux) + 4 * 3 * kRedSlot;
     }
-    __device__ bool skip() const { return st->done != 0; }
+    using Regs = typename P::Regs;
+    __device__ bool skip() const { return false; }
+    __device__ void issue(int tid, Regs& r) const { p.issue(tid, st, r); }
     __device__ void offset(long) {}
     __device__ void prepare() {}
-    __device__ void build(uint32_t* planes, int cols, int tid, float* scratch) {
+    __device__ void build(uint32_t* planes, int cols, int tid, float* scratch, Regs& r) {
         float* vec = scratch;
         float* aux = scratch + cols;
         float* red = scratch + cols * (1 + P::kAux);
-        p.fill(vec, aux, cols, tid, red, st);
-        __syncthreads();
-        float m = 0.0f;
-        for (int i = tid; i < cols; i += kBlock) m = __builtin_fmaxf(m, __builtin_fabsf(vec[i]));
-        amax = block_max<kBlock>(m, red);
+        const float m = p.fill(vec, aux, cols, tid, red, st, r);
+        amax = block_max<kBlock>(m, red + 2 * kRedSlot);  // its barrier also orders vec
         BuildPlanes<LdsQuantSrc>{LdsQuantSrc{vec, quant_scale(amax)}}.build(planes, cols, tid,
                                                                             nullptr);
     }
@@ -268,49 +359,87 @@ struct InputNorm {
     uint16_t* x_out;
     const float* w;
     float eps;
-    __device__ void fill(float* vec, float*, int n, int tid, float* red,
-                         const EngineState* st) const {
-        const uint16_t* src = x;
-        if (embed) src = embed + static_cast<long>(tokens[st->pos]) * n;
-        const float ss = load_bf16_sumsq<kBlock>(src, vec, n >> 3, tid,
-                                                 embed && blockIdx.x == 0 ? x_out : nullptr);
+    int n;
+    struct Regs {
+        const uint16_t* src;
+        HeldUnits<kBlock> hx;
+        HeldWeights<kBlock> hw;
+    };
+    __device__ void issue(int tid, const EngineState* st, Regs& r) const {
+        r.src = embed ? embed + static_cast<long>(tokens[st->pos]) * n : x;
+        r.hx.load(r.src, n >> 3, tid);
+        r.hw.load(w, n >> 3, tid);
+    }
+    __device__ float fill(float* vec, float*, int, int tid, float* red, const EngineState*,
+                          Regs& r) const {
+        const float ss = load_bf16_sumsq<kBlock>(r.src, vec, n >> 3, tid,
+                                                 embed && blockIdx.x == 0 ? x_out : nullptr, r.hx);
         const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
-        scale_by_weight<kBlock>(vec, w, inv, n >> 3, tid);
+        return r.hw.apply(vec, w, inv, n >> 3, tid);
     }
 };
 
 // Attention output: combine the splits of every head,
 //   M = max_s m_s, w_s = exp(m_s - M), out = (sum_s w_s acc_s) / (sum_s w_s l_s)
 // (s ascending, fused multiply-adds), rounded to bf16.  A unit (8 dims)
-// never straddles heads (head_dim % 8 == 0).
+// never straddles heads (head_dim % 8 == 0).  Loads are issued in batches of
+// kBatch splits.
 struct AttnCombine {
     static constexpr int kAux = 0;
+    static constexpr int kBatch = 4;
     const float* pm;    // [nh][S]
     const float* pl;    // [nh][S]
     const float* pacc;  // [nh][S][hd]
     int hd, S, chunk;
-    __device__ void fill(float* vec, float*, int n, int tid, float*,
-                         const EngineState* st) const {
-        const int ns = st->pos / chunk + 1;  // splits holding positions 0..pos
+    struct Regs {};
+    __device__ void issue(int, const EngineState*, Regs&) const {}
+    __device__ float fill(float* vec, float*, int n, int tid, float*, const EngineState* st,
+                          Regs&) const {
+        int ns = st->pos / chunk + 1;  // splits holding positions 0..pos
+        ns = ns < S ? ns : S;
         const int units = n >> 3;
+        float mx = 0.0f;
         for (int u = tid; u < units; u += kBlock) {
             const int h = (8 * u) / hd, d0 = 8 * u - h * hd;
             const float* m = pm + h * S;
-            float M = m[0];
-            for (int s = 1; s < ns; ++s) M = __builtin_fmaxf(M, m[s]);
-            float l = 0.0f, a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            for (int s = 0; s < ns; ++s) {
-                float p[8];
-                load_f8(pacc + (static_cast<long>(h) * S + s) * hd + d0, p);
-                const float w = exp_neg(m[s] - M);
-                l = __builtin_fmaf(w, pl[h * S + s], l);
+            float M = -INFINITY;
+            for (int s0 = 0; s0 < ns; s0 += kBatch) {
+                float mv[kBatch];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) a[e] = __builtin_fmaf(w, p[e], a[e]);
+                for (int b = 0; b < kBatch; ++b) mv[b] = s0 + b < ns ? m[s0 + b] : -INFINITY;
+#pragma unroll
+                for (int b = 0; b < kBatch; ++b) M = __builtin_fmaxf(M, mv[b]);
+            }
+            float l = 0.0f, a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int s0 = 0; s0 < ns; s0 += kBatch) {
+                float pv[kBatch][8], lv[kBatch], mv[kBatch];
+#pragma unroll
+                for (int b = 0; b < kBatch; ++b) {
+                    const int s = s0 + b;
+                    if (s < ns) {
+                        load_f8(pacc + (static_cast<long>(h) * S + s) * hd + d0, pv[b]);
+                        lv[b] = pl[h * S + s];
+                        mv[b] = m[s];
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < kBatch; ++b) {
+                    if (s0 + b < ns) {
+                        const float w = exp_neg(mv[b] - M);
+                        l = __builtin_fmaf(w, lv[b], l);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) a[e] = __builtin_fmaf(w, pv[b][e], a[e]);
+                    }
+                }
             }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) a[e] = bf16r(a[e] / l);
+            for (int e = 0; e < 8; ++e) {
+                a[e] = bf16r(a[e] / l);
+                mx = __builtin_fmaxf(mx, __builtin_fabsf(a[e]));
+            }
             store_f8(vec + 8 * u, a);
         }
+        return mx;
     }
 };
 
@@ -325,9 +454,22 @@ struct SubNormResidualNorm {
     const float* w_sub;
     const float* w_post;
     float eps;
-    __device__ void fill(float* vec, float* aux, int n, int tid, float* red,
-                         const EngineState*) const {
+    int n;
+    struct Regs {
+        HeldUnits<kBlock> ho, hr;
+        HeldWeights<kBlock> hs, hp;
+    };
+    __device__ void issue(int tid, const EngineState*, Regs& r) const {
         const int units = n >> 3;
+        r.ho.load(o, units, tid);
+        r.hr.load(res, units, tid);
+        if (w_sub) r.hs.load(w_sub, units, tid);
+        r.hp.load(w_post, units, tid);
+    }
+    __device__ float fill(float* vec, float* aux, int, int tid, float* red, const EngineState*,
+                          Regs& r) const {
+        const int units = n >> 3;
+        const bool held = units <= kUnits * kBlock;
         // o -> vec (sum of squares), residual -> aux
         float ss = 0.0f;
         for (int base = 0; base < units; base += kUnits * kBlock) {
@@ -335,7 +477,10 @@ struct SubNormResidualNorm {
 #pragma unroll
             for (int k = 0; k < kUnits; ++k) {
                 const int u = base + tid + k * kBlock;
-                if (u < units) {
+                if (base == 0) {
+                    ro[k] = r.ho.r[k];
+                    rr[k] = r.hr.r[k];
+                } else if (u < units) {
                     ro[k] = reinterpret_cast<const uint4*>(o)[u];
                     rr[k] = reinterpret_cast<const uint4*>(res)[u];
                 }
@@ -354,33 +499,45 @@ struct SubNormResidualNorm {
                 }
             }
         }
-        if (w_sub) {
-            const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
-            scale_by_weight<kBlock>(vec, w_sub, inv, units, tid);
-        }
-        // x = bf16(o + r)
+        const float inv = w_sub ? inv_rms(block_sum<kBlock>(ss, red), n, eps) : 1.0f;
+        // o = bf16((o * inv) * w_sub) (when present); x = bf16(o + r)
         float ss2 = 0.0f;
-        for (int u = tid; u < units; u += kBlock) {
-            float f[8], g[8];
-            load_f8(vec + 8 * u, f);
-            load_f8(aux + 8 * u, g);
-            uint32_t packed[4];
+        for (int base = 0; base < units; base += kUnits * kBlock) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                f[e] = bf16r(f[e] + g[e]);
-                ss2 = __builtin_fmaf(f[e], f[e], ss2);
+            for (int k = 0; k < kUnits; ++k) {
+                const int u = base + tid + k * kBlock;
+                if (u >= units) continue;
+                float f[8], g[8], ws[8];
+                load_f8(vec + 8 * u, f);
+                load_f8(aux + 8 * u, g);
+                if (w_sub) {
+                    if (held) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) ws[e] = r.hs.f[k][e];
+                    } else {
+                        load_f8(w_sub + 8 * u, ws);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) f[e] = bf16r((f[e] * inv) * ws[e]);
+                }
+                uint32_t packed[4];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    f[e] = bf16r(f[e] + g[e]);
+                    ss2 = __builtin_fmaf(f[e], f[e], ss2);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    packed[q] = static_cast<uint32_t>(BF16::from_float(f[2 * q])) |
+                                (static_cast<uint32_t>(BF16::from_float(f[2 * q + 1])) << 16);
+                store_f8(vec + 8 * u, f);
+                if (blockIdx.x == 0)
+                    reinterpret_cast<uint4*>(x_out)[u] =
+                        make_uint4(packed[0], packed[1], packed[2], packed[3]);
             }
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                packed[k] = static_cast<uint32_t>(BF16::from_float(f[2 * k])) |
-                            (static_cast<uint32_t>(BF16::from_float(f[2 * k + 1])) << 16);
-            store_f8(vec + 8 * u, f);
-            if (blockIdx.x == 0)
-                reinterpret_cast<uint4*>(x_out)[u] =
-                    make_uint4(packed[0], packed[1], packed[2], packed[3]);
         }
-        const float inv2 = inv_rms(block_sum<kBlock>(ss2, red), n, eps);
-        scale_by_weight<kBlock>(vec, w_post, inv2, units, tid);
+        const float inv2 = inv_rms(block_sum<kBlock>(ss2, red + kRedSlot), n, eps);
+        return r.hp.apply(vec, w_post, inv2, units, tid);
     }
 };
 
@@ -393,16 +550,30 @@ struct Relu2Norm {
     const uint16_t* u;
     const float* w;
     float eps;
-    __device__ void fill(float* vec, float*, int n, int tid, float* red,
-                         const EngineState*) const {
+    int n;
+    struct Regs {
+        HeldUnits<kBlock> hg, hu;
+        HeldWeights<kBlock> hw;
+    };
+    __device__ void issue(int tid, const EngineState*, Regs& r) const {
         const int units = n >> 3;
-        float ss = 0.0f;
+        r.hg.load(g, units, tid);
+        r.hu.load(u, units, tid);
+        if (w) r.hw.load(w, units, tid);
+    }
+    __device__ float fill(float* vec, float*, int, int tid, float* red, const EngineState*,
+                          Regs& r) const {
+        const int units = n >> 3;
+        float ss = 0.0f, mx = 0.0f;
         for (int base = 0; base < units; base += kUnits * kBlock) {
             uint4 rg[kUnits], ru[kUnits];
 #pragma unroll
             for (int k = 0; k < kUnits; ++k) {
                 const int q = base + tid + k * kBlock;
-                if (q < units) {
+                if (base == 0) {
+                    rg[k] = r.hg.r[k];
+                    ru[k] = r.hu.r[k];
+                } else if (q < units) {
                     rg[k] = reinterpret_cast<const uint4*>(g)[q];
                     ru[k] = reinterpret_cast<const uint4*>(u)[q];
                 }
@@ -419,16 +590,18 @@ struct Relu2Norm {
                         const float r = __builtin_fmaxf(0.0f, fg[e]);
                         fg[e] = (r * r) * fu[e];
                         ss = __builtin_fmaf(fg[e], fg[e], ss);
-                        if (!w) fg[e] = bf16r(fg[e]);  // no sub-norm: plain rounding
+                        if (!w) {  // no sub-norm: plain rounding
+                            fg[e] = bf16r(fg[e]);
+                            mx = __builtin_fmaxf(mx, __builtin_fabsf(fg[e]));
+                        }
                     }
                     store_f8(vec + 8 * q, fg);
                 }
             }
         }
-        if (w) {
-            const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
-            scale_by_weight<kBlock>(vec, w, inv, units, tid);
-        }
+        if (!w) return mx;
+        const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
+        return r.hw.apply(vec, w, inv, units, tid);
     }
 };
 
@@ -482,7 +655,7 @@ struct ResidualSink {
 // scores, the split's softmax numerator and unnormalised weighted sum of V.
 //   score_j = (sum over d ascending of fma(q[d], k_j[d], .)) * scale
 //   per head: m = max_j score_j, e_j = exp(score_j - m),
-//   l = butterfly sum of e over the 64 lanes (lane = position in the split),
+//   l = tree sum of e over the 64 lanes (lane = position in the split),
 //   acc[d] = sum_j e_j v_j[d] (j ascending, fma).
 // rope: [max_seq][hd/2] (cos, sin) of angle pos * theta^(-2i/hd).
 // Reference: rope_kernel, scatter_kv, attention_scores, softmax,
@@ -577,9 +750,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     __syncthreads();
     for (int g = wave; g < G; g += kAttnThreads / kWave) {
         const float v = lane < jn ? sc[g][lane] : -INFINITY;
-        const float m = wave_max(v);
+        const float m = wave_max_tree(v);
         const float e = lane < jn ? exp_neg(v - m) : 0.0f;
-        const float l = wave_sum_bfly(e);
+        const float l = wave_sum_tree(e);
         sc[g][lane] = e;
         if (lane == 0) {
             hmax[g] = m;
@@ -605,7 +778,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
 // Final RMSNorm (unit order over kLmBlock threads), then
 // logits[r] = sum_c W[r][c] * xn[c] in fp32: lane l of the row's wave takes
 // the 8-element chunks l, l+64, ... (fma in element order), then the
-// butterfly.  Each wave keeps RR rows (NC 16-byte chunks per lane each) in
+// wave tree.  Each wave keeps RR rows (NC 16-byte chunks per lane each) in
 // flight.  Argmax = lowest index among the maxima (std::max_element,
 // src/main.cpp:194-200).  The last block to finish reduces the per-block
 // maxima and advances the decode state.  Reference half_gemv_kernel
@@ -624,9 +797,13 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     if (st->done) return;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
 
-    const float ss = load_bf16_sumsq<kLmBlock>(x, xs, H >> 3, tid, nullptr);
+    HeldWeights<kLmBlock> hw;
+    HeldUnits<kLmBlock> hx;
+    hx.load(x, H >> 3, tid);
+    hw.load(wn, H >> 3, tid);
+    const float ss = load_bf16_sumsq<kLmBlock>(x, xs, H >> 3, tid, nullptr, hx);
     const float inv = inv_rms(block_sum<kLmBlock>(ss, red), H, eps);
-    scale_by_weight<kLmBlock>(xs, wn, inv, H >> 3, tid);
+    hw.apply(xs, wn, inv, H >> 3, tid);
     __syncthreads();
 
     const int nch = H >> 3;
@@ -661,7 +838,7 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
                     for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(f[e], xv[e], acc);
                 }
             }
-            acc = wave_sum_bfly(acc);
+            acc = wave_sum_tree(acc);
             if (r < V) {
                 if (lane == 0) logits[r] = acc;
                 if (acc > best) {  // rows ascend within a wave: strict > keeps the first maximum
@@ -933,7 +1110,8 @@ struct spb_engine {
         for (size_t l = 0; l < layers.size(); ++l) {
             const spb_transformer_layer& L = layers[l];
             {
-                InputNorm p{xa, l == 0 ? embed : nullptr, tokens, xa, L.input_layernorm, eps};
+                InputNorm p{xa, l == 0 ? embed : nullptr, tokens, xa, L.input_layernorm, eps,
+                            cfg.hidden_size};
                 SegBf16Sink sink{qkv, L.q_proj.gamma, L.k_proj.gamma, L.v_proj.gamma,
                                  L.q_proj.rows, L.q_proj.rows + L.k_proj.rows, 0.f, 0.f, 0.f};
                 launch_bitplane(seg_weights(&L.q_proj, &L.k_proj, &L.v_proj),
@@ -956,7 +1134,7 @@ struct spb_engine {
             }
             {
                 SubNormResidualNorm p{obuf, xa, xb, L.attn_sub_norm, L.post_attention_layernorm,
-                                      eps};
+                                      eps, cfg.hidden_size};
                 SegBf16Sink sink{gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
                                  L.gate_proj.rows, L.gate_proj.rows + L.up_proj.rows, 0.f, 0.f,
                                  0.f};
@@ -965,7 +1143,7 @@ struct spb_engine {
             }
             {
                 const int I = cfg.intermediate_size;
-                Relu2Norm p{gu, gu + I, L.ffn_sub_norm, eps};
+                Relu2Norm p{gu, gu + I, L.ffn_sub_norm, eps, I};
                 ResidualSink sink{xa, xb, L.down_proj.gamma, 0.f};
                 launch_bitplane(single_weights(L.down_proj), ProducerPlanes<Relu2Norm>{p, st, 0.f},
                                 sink, s);
