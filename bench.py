@@ -20,8 +20,11 @@ The JSON line reports
              6912x2560 matrix, single thread, on this host
 and under "detail": single-launch times per shape (cold: caches flushed by a
 1 GiB write; warm: back to back), the decode-shaped step (30 layers x
-gate/up/down as 90 separate launches replayed from a HIP graph), and the
-same with precomputed activation planes.
+gate/up/down as 90 separate launches replayed from a HIP graph), the same
+with precomputed activation planes, the config-2 batched GEMM (matrix-core
+kernel against the add/sub kernel), and decode_config3: end-to-end bs=1
+greedy decode of the 2.4B-parameter BitNet-b1.58-2B-4T shape (random-init
+weights) through the HIP engine, tokens/s over 128 decode steps.
 """
 from __future__ import annotations
 
@@ -58,6 +61,67 @@ def read_traffic():
         return None
 
 
+# Bytes one decode step must read at minimum: every packed projection of the
+# 30 layers plus the bf16 LM head (tied embedding), config 3.
+def decode_bytes_per_token(cfg) -> int:
+    H, I, kvd = cfg.hidden_size, cfg.intermediate_size, cfg.num_key_value_heads * cfg.head_dim
+    per_layer = sum(r * c * 3 // 16 for r, c in
+                    [(H, H), (kvd, H), (kvd, H), (H, H), (I, H), (I, H), (H, I)])
+    return cfg.num_hidden_layers * per_layer + cfg.vocab_size * H * 2
+
+
+def decode_config3(args, log, ev, stream):
+    """Config 3: bs=1 greedy decode of the BitNet-b1.58-2B-4T shape with
+    random-init weights (generated on the device), prompt = BOS + 32 seeded
+    token ids, then args.decode_tokens greedy steps, all as graph replays of
+    the engine's token step; tokens/s over the decode steps only (the
+    reference's convention, src/main.cpp:175-215)."""
+    import numpy as np
+    import torch
+    from spbitnet_amd.model import InferenceEngine, Model, ModelConfig
+    cfg = ModelConfig.bitnet_b158_2b4t()
+    log("decode: generating the random 2.4B-parameter model")
+    model = Model.random(cfg, seed=2025)
+    eng = InferenceEngine(model, max_seq=256)
+    prompt = [cfg.bos_token_id] + [int(t) for t in
+                                   np.random.default_rng(2025).integers(0, cfg.vocab_size, 32)]
+    n = args.decode_tokens
+    runs = []
+    for _ in range(3):
+        eng.generate(prompt, 0, stop_at_eos=False)  # reset + prefill
+        torch.cuda.synchronize()
+        a, b = ev(), ev()
+        a.record(stream)
+        eng.decode_steps(n)
+        b.record(stream)
+        torch.cuda.synchronize()
+        runs.append(a.elapsed_time(b))
+    ms = sorted(runs)[len(runs) // 2]
+    toks = eng.generate(prompt, n, stop_at_eos=False)
+    again = eng.generate(prompt, n, stop_at_eos=False)
+    nbytes = decode_bytes_per_token(cfg)
+    out = {
+        "model": "BitNet-b1.58-2B-4T shape, random init (30 layers, hidden 2560, 20/5 heads, "
+                 "FFN 6912, vocab 128256, bf16 tied embedding / LM head, bf16 KV cache)",
+        "prompt_tokens": len(prompt),
+        "decode_tokens": n,
+        "tok_per_s": round(n / (ms * 1e-3), 1),
+        "us_per_token": round(ms * 1e3 / n, 1),
+        "ms_runs": [round(r, 3) for r in runs],
+        "min_bytes_per_token": nbytes,
+        "effective_GBs": round(nbytes * n / (ms * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(nbytes * n / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "kernels_per_token": 5 * cfg.num_hidden_layers + 1,
+        "greedy_repeatable": toks == again,
+        "first_tokens": toks[:8],
+    }
+    log(f"decode: {out['tok_per_s']} tok/s")
+    eng.close()
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -68,6 +132,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the config-3 end-to-end decode measurement")
+    ap.add_argument("--decode-tokens", type=int, default=128)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB once (known bytes, for scaling rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE) and exit")
@@ -313,6 +380,9 @@ def main() -> int:
                 row[f"{name}_dense_equiv_TOPS"] = round(2.0 * L.rows * L.cols * n / (us * 1e-6) / 1e12, 2)
             g2[f"n{n}"] = row
         detail["gemm_config2_6912x2560_warm_b2b"] = g2
+
+    if not args.no_decode:
+        detail["decode_config3"] = decode_config3(args, log, ev, stream)
 
     # ---- CPU baseline: the reference's CPU GEMV on this host, single thread
     cpu = None

@@ -291,6 +291,8 @@ def _elib():
         L.spbo_engine_step.argtypes = [_P, _I, _P]
         L.spbo_engine_step.restype = _I
         L.spbo_engine_hidden.argtypes = [_P, _P]
+        L.spbo_engine_debug.argtypes = [_P, _I, _P]
+        L.spbo_engine_debug.restype = _I
         L.spbo_exp_neg.argtypes = [_F]
         L.spbo_exp_neg.restype = _F
         _engine_lib = L
@@ -359,12 +361,23 @@ class EngineOracle:
         """(argmax, float32 logits) after feeding `token` at the next position."""
         logits = np.empty(self.vocab, np.float32)
         t = _elib().spbo_engine_step(self._e, int(token), _p(logits))
+        if t < 0:
+            raise ValueError("oracle step: KV cache full or token id out of range")
         return int(t), logits
 
     def hidden(self) -> np.ndarray:
         out = np.empty(self.hidden_size, np.float32)
         _elib().spbo_engine_hidden(self._e, _p(out))
         return out
+
+    DEBUG = {"qkv": 0, "attn": 1, "o": 2, "x_mid": 3, "gate_up": 4, "h": 5, "m": 6}
+
+    def debug(self, name: str) -> np.ndarray:
+        """An internal vector of the last step's last layer (see
+        spbo_engine_debug)."""
+        out = np.empty(4 * (self.hidden_size + 32768), np.float32)
+        n = _elib().spbo_engine_debug(self._e, self.DEBUG[name], _p(out))
+        return out[:n].copy()
 
     def generate(self, prompt, n_new: int, eos: int = -1):
         """Greedy generation with the convention of src/main.cpp:133-155."""

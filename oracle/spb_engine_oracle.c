@@ -131,7 +131,7 @@ typedef struct {
     uint16_t** vc;
     int pos;
     /* scratch */
-    float *x, *xb, *vec, *qkv, *o, *gu, *attn;
+    float *x, *xb, *vec, *qkv, *o, *gu, *attn, *h_in, *m_in;
     int8_t* q8;
     int32_t* acc;
 } spbo_engine;
@@ -214,6 +214,8 @@ spbo_engine* spbo_engine_new(const int* icfg, const float* fcfg, const uint32_t*
     e->o = (float*)calloc((size_t)H, 4);
     e->gu = (float*)calloc((size_t)2 * I, 4);
     e->attn = (float*)calloc((size_t)H, 4);
+    e->h_in = (float*)calloc((size_t)H, 4);
+    e->m_in = (float*)calloc((size_t)I, 4);
     e->q8 = (int8_t*)calloc((size_t)mx, 1);
     e->acc = (int32_t*)calloc((size_t)mx, 4);
     e->pos = 0;
@@ -237,6 +239,8 @@ void spbo_engine_free(spbo_engine* e) {
     free(e->o);
     free(e->gu);
     free(e->attn);
+    free(e->h_in);
+    free(e->m_in);
     free(e->q8);
     free(e->acc);
     free(e);
@@ -330,9 +334,11 @@ static void attention(spbo_engine* e, int l) {
     free(pacc);
 }
 
-/* One token: returns argmax(logits) (lowest index among maxima); logits
- * (nullable) receives the float32 logits. */
+/* One token: returns argmax(logits) (lowest index among maxima), or -1 when
+ * the KV cache is full or the token id is out of range; logits (nullable)
+ * receives the float32 logits. */
 int spbo_engine_step(spbo_engine* e, int token, float* logits) {
+    if (e->pos >= e->max_seq || token < 0 || token >= e->V) return -1; /* cache full / bad id */
     const int H = e->H, I = e->I, hd = e->hd, kvd = e->nkv * hd;
     const float eps = e->eps;
     float* vec = e->vec;
@@ -342,6 +348,7 @@ int spbo_engine_step(spbo_engine* e, int token, float* logits) {
         const layer_t* L = &e->layers[l];
         /* input RMSNorm and q/k/v (inference.cu:147-160, 171-177) */
         rmsnorm(e->x, L->norm[0], H, eps, GEMV_THREADS, vec);
+        memcpy(e->h_in, vec, sizeof(float) * H);
         const float a0 = bitlinear_raw(e, &L->p[0], vec, acc);
         {
             const int R[3] = {H, kvd, kvd};
@@ -385,6 +392,7 @@ int spbo_engine_step(spbo_engine* e, int token, float* logits) {
             for (int i = 0; i < I; ++i) vec[i] = bfr(vec[i]);
         }
         /* down projection and residual (:253-262) */
+        memcpy(e->m_in, vec, sizeof(float) * I);
         const float a3 = bitlinear_raw(e, &L->p[6], vec, acc);
         const float dq3 = spbo_dequant_scale(L->p[6].gamma, a3);
         for (int r = 0; r < H; ++r) e->x[r] = bfr(bfr((float)acc[r] * dq3) + e->xb[r]);
@@ -417,9 +425,10 @@ int spbo_engine_step(spbo_engine* e, int token, float* logits) {
 /* Hidden state after the last step (float values of the bf16 residual). */
 void spbo_engine_hidden(const spbo_engine* e, float* out) { memcpy(out, e->x, sizeof(float) * e->H); }
 
-/* Internal vectors of the last step's last layer, for debugging the checker
+/* Internal vectors of the last step's last layer, for checking the checker
  * itself: 0 = q|k|v (pre-RoPE), 1 = attention output, 2 = o (after the
- * sub-norm), 3 = mid-layer residual, 4 = gate|up. */
+ * sub-norm), 3 = mid-layer residual, 4 = gate|up, 5 = normalised layer input,
+ * 6 = normalised down-projection input. */
 int spbo_engine_debug(const spbo_engine* e, int which, float* out) {
     const int H = e->H, kvd = e->nkv * e->hd, I = e->I;
     switch (which) {
@@ -428,6 +437,8 @@ int spbo_engine_debug(const spbo_engine* e, int which, float* out) {
         case 2: memcpy(out, e->o, sizeof(float) * H); return H;
         case 3: memcpy(out, e->xb, sizeof(float) * H); return H;
         case 4: memcpy(out, e->gu, sizeof(float) * 2 * I); return 2 * I;
+        case 5: memcpy(out, e->h_in, sizeof(float) * H); return H;
+        case 6: memcpy(out, e->m_in, sizeof(float) * I); return I;
         default: return 0;
     }
 }

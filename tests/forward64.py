@@ -105,3 +105,35 @@ class Forward64:
         xn = self.rms(x, self.final_norm)
         self.pos += 1
         return self.lm @ xn
+
+
+def host_model(cfg, seed=0, qk_gamma=None, sub_norms=True, norm_jitter=0.0):
+    """A random model as host arrays in the layout Model.to_host() returns,
+    generated on the CPU (spbitnet_amd.weights) for the CPU-only checks.
+    qk_gamma overrides the q/k projection gamma (a well-conditioned softmax);
+    norm_jitter draws RMSNorm weights from 1 + jitter * N(0,1)."""
+    from oracle import oracle as O
+    H, I = cfg.hidden_size, cfg.intermediate_size
+    kvd = cfg.num_key_value_heads * cfg.head_dim
+    shapes = {"q_proj": (H, H), "k_proj": (kvd, H), "v_proj": (kvd, H), "o_proj": (H, H),
+              "gate_proj": (I, H), "up_proj": (I, H), "down_proj": (H, I)}
+
+    def norm(n, *tag):
+        if not norm_jitter:
+            return np.ones(n, np.float32)
+        return (1.0 + norm_jitter * W.normal_f32(W.seed_for("norm", seed, *tag), n)).astype(np.float32)
+
+    layers = []
+    for l in range(cfg.num_hidden_layers):
+        d = {}
+        for p, (r, k) in shapes.items():
+            L = W.random_layer(r, k, W.seed_for("host", seed, l, p))
+            g = L.gamma if (qk_gamma is None or p not in ("q_proj", "k_proj")) else qk_gamma
+            d[p] = (L.meta, L.values, g, r, k, L.meta.shape[1], L.values.shape[1])
+        d["norms"] = [norm(H, l, 0), norm(H, l, 1),
+                      norm(H, l, 2) if sub_norms else None, norm(I, l, 3) if sub_norms else None]
+        layers.append(d)
+    emb = (W.normal_f32(W.seed_for("host", seed, "embed"), cfg.vocab_size * H) * 0.02)
+    return {"config": cfg, "layers": layers,
+            "embed": O.to_bf16_bits(emb.astype(np.float32)).reshape(cfg.vocab_size, H),
+            "lm_head": None, "final_norm": norm(H, "final")}
