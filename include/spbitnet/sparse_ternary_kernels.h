@@ -2,9 +2,9 @@
 // MI355X build, over the C ABI in spbitnet_amd.h.
 //
 // Same namespace, names, argument order and meaning as the reference's
-// include/spbitnet/sparse_ternary_kernels.h:16-48 and the quantiser part of
-// include/spbitnet/inference_kernels.h:19-30, with hipStream_t in place of
-// cudaStream_t.  Error behaviour matches the reference's CUDA_CHECK
+// include/spbitnet/sparse_ternary_kernels.h:16-48, with hipStream_t in place of
+// cudaStream_t (the quantiser and the other per-op wrappers are in
+// spbitnet/inference_kernels.h, as in the reference).  Error behaviour matches the reference's CUDA_CHECK
 // (include/spbitnet/cuda_utils.h:13-21): a failing call prints the error and
 // exits the process; rows == 0 or cols == 0 is a no-op.  Callers that prefer
 // status codes use the C ABI directly.
@@ -80,40 +80,6 @@ inline void fused_sparse_bitlinear_gpu(const uint32_t* meta, const uint32_t* val
                                                        detail::bits(output), d_absmax, gamma,
                                                        rows, cols, meta_row_stride,
                                                        values_row_stride, stream));
-}
-
-// reference include/spbitnet/inference_kernels.h:19-20
-inline void absmax_quantize_gpu(const half* input, int8_t* output, float* d_absmax, int size,
-                                hipStream_t stream = nullptr) {
-    SPBITNET_AMD_CHECK(
-        spb_absmax_quantize_f16(detail::bits(input), output, d_absmax, size, stream));
-}
-inline void absmax_quantize_gpu(const __hip_bfloat16* input, int8_t* output, float* d_absmax,
-                                int size, hipStream_t stream = nullptr) {
-    SPBITNET_AMD_CHECK(
-        spb_absmax_quantize_bf16(detail::bits(input), output, d_absmax, size, stream));
-}
-
-// reference include/spbitnet/inference_kernels.h:24-25
-inline void absmax_reduce_gpu(const half* input, float* d_absmax, int size,
-                              hipStream_t stream = nullptr) {
-    SPBITNET_AMD_CHECK(spb_absmax_reduce_f16(detail::bits(input), d_absmax, size, stream));
-}
-inline void absmax_reduce_gpu(const __hip_bfloat16* input, float* d_absmax, int size,
-                              hipStream_t stream = nullptr) {
-    SPBITNET_AMD_CHECK(spb_absmax_reduce_bf16(detail::bits(input), d_absmax, size, stream));
-}
-
-// reference include/spbitnet/inference_kernels.h:29-30
-inline void dequantize_gpu(const int32_t* input, half* output, const float* d_absmax,
-                           float gamma, int size, hipStream_t stream = nullptr) {
-    SPBITNET_AMD_CHECK(
-        spb_dequantize_f16(input, detail::bits(output), d_absmax, gamma, size, stream));
-}
-inline void dequantize_gpu(const int32_t* input, __hip_bfloat16* output, const float* d_absmax,
-                           float gamma, int size, hipStream_t stream = nullptr) {
-    SPBITNET_AMD_CHECK(
-        spb_dequantize_bf16(input, detail::bits(output), d_absmax, gamma, size, stream));
 }
 
 }  // namespace spbitnet

@@ -182,6 +182,80 @@ int spb_sparse_ternary_gemv_kernel_id(const uint32_t* meta, const uint32_t* valu
                                       int values_row_stride);
 
 
+/* ---- per-op inference kernels ---------------------------------------------
+ * The reference's op-by-op wrappers (include/spbitnet/inference_kernels.h:14-87,
+ * src/kernels/inference_kernels.cu), each for fp16 (_f16) and bf16 (_bf16)
+ * storage; 16-bit tensors are passed as their bit patterns (uint16_t).
+ * float32 arithmetic; outputs rounded once to the storage type.  Sizes of 0
+ * are no-ops; negative sizes, null pointers and inconsistent shapes return
+ * an error (nothing is launched). */
+
+/* rms_norm_gpu (inference_kernels.h:14-15): y = (x * inv) * w,
+ * inv = 1 / sqrt(mean(x^2) + eps); x and y may alias. */
+int spb_rms_norm_f16(const uint16_t* input, const float* weight, uint16_t* output, int size,
+                     float eps, spb_stream_t stream);
+int spb_rms_norm_bf16(const uint16_t* input, const float* weight, uint16_t* output, int size,
+                      float eps, spb_stream_t stream);
+/* rms_norm_f32in_gpu (inference_kernels.h:75-76): float32 input. */
+int spb_rms_norm_f32in_f16(const float* input, const float* weight, uint16_t* output, int size,
+                           float eps, spb_stream_t stream);
+int spb_rms_norm_f32in_bf16(const float* input, const float* weight, uint16_t* output, int size,
+                            float eps, spb_stream_t stream);
+/* rope_gpu (inference_kernels.h:33-34): in place on (num_heads, head_dim). */
+int spb_rope_f16(uint16_t* vec, int num_heads, int head_dim, int pos, float theta,
+                 spb_stream_t stream);
+int spb_rope_bf16(uint16_t* vec, int num_heads, int head_dim, int pos, float theta,
+                  spb_stream_t stream);
+/* scatter_kv_gpu (inference_kernels.h:38-40): cache (num_kv_heads,
+ * max_seq_len, head_dim); 0 <= pos < max_seq_len. */
+int spb_scatter_kv(const uint16_t* src, uint16_t* cache, int num_kv_heads, int head_dim,
+                   int max_seq_len, int pos, spb_stream_t stream);
+/* attention_scores_gpu (inference_kernels.h:45-48): scores (num_heads,
+ * max_seq_len), the first seq_len per head written; kv = h * nkv / nh. */
+int spb_attention_scores_f16(const uint16_t* Q, const uint16_t* K_cache, float* scores,
+                             int num_heads, int num_kv_heads, int head_dim, int max_seq_len,
+                             int seq_len, float scale, spb_stream_t stream);
+int spb_attention_scores_bf16(const uint16_t* Q, const uint16_t* K_cache, float* scores,
+                              int num_heads, int num_kv_heads, int head_dim, int max_seq_len,
+                              int seq_len, float scale, spb_stream_t stream);
+/* softmax_gpu (inference_kernels.h:52-53): in place per head. */
+int spb_softmax(float* scores, int num_heads, int max_seq_len, int seq_len, spb_stream_t stream);
+/* attention_output_gpu (inference_kernels.h:58-61); head_dim <= 256. */
+int spb_attention_output_f16(const float* scores, const uint16_t* V_cache, uint16_t* output,
+                             int num_heads, int num_kv_heads, int head_dim, int max_seq_len,
+                             int seq_len, spb_stream_t stream);
+int spb_attention_output_bf16(const float* scores, const uint16_t* V_cache, uint16_t* output,
+                              int num_heads, int num_kv_heads, int head_dim, int max_seq_len,
+                              int seq_len, spb_stream_t stream);
+/* relu2_mul_gpu / relu2_mul_f32_gpu (inference_kernels.h:64-71):
+ * out = (max(0, g)^2) * u. */
+int spb_relu2_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* output, int size,
+                      spb_stream_t stream);
+int spb_relu2_mul_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* output, int size,
+                       spb_stream_t stream);
+int spb_relu2_mul_f32_f16(const uint16_t* gate, const uint16_t* up, float* output, int size,
+                          spb_stream_t stream);
+int spb_relu2_mul_f32_bf16(const uint16_t* gate, const uint16_t* up, float* output, int size,
+                           spb_stream_t stream);
+/* float_to_half_gpu (inference_kernels.h:79-80). */
+int spb_float_to_f16(const float* input, uint16_t* output, int size, spb_stream_t stream);
+int spb_float_to_bf16(const float* input, uint16_t* output, int size, spb_stream_t stream);
+/* residual_add_gpu (inference_kernels.h:83-84): out = a + b (float32 add). */
+int spb_residual_add_f16(const uint16_t* a, const uint16_t* b, uint16_t* output, int size,
+                         spb_stream_t stream);
+int spb_residual_add_bf16(const uint16_t* a, const uint16_t* b, uint16_t* output, int size,
+                          spb_stream_t stream);
+/* half_gemv_gpu (inference_kernels.h:87-89): y (float32) = W x, W (rows,
+ * cols) 16-bit. */
+int spb_gemv_f16(const uint16_t* W, const uint16_t* x, float* y, int rows, int cols,
+                 spb_stream_t stream);
+int spb_gemv_bf16(const uint16_t* W, const uint16_t* x, float* y, int rows, int cols,
+                  spb_stream_t stream);
+/* Greedy pick on the device: *out_index = index of max(x) (lowest index among
+ * equal maxima); replaces the host std::max_element over copied logits
+ * (src/main.cpp:194-200). */
+int spb_argmax_f32(const float* x, int n, int* out_index, spb_stream_t stream);
+
 /* ---- decode engine --------------------------------------------------------
  * bs=1 greedy decode of a BitNet b1.58 transformer whose linear layers are
  * 2:4 sparse-ternary, with bf16 activations, bf16 KV cache and a bf16 tied or

@@ -42,6 +42,30 @@ SIGNATURES = {
     "spb_sparse_ternary_gemv_planes": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "spb_fused_sparse_bitlinear_planes_f16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
     "spb_fused_sparse_bitlinear_planes_bf16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
+    # per-op inference kernels
+    "spb_rms_norm_f16": [_P, _P, _P, _I, _F, _P],
+    "spb_rms_norm_bf16": [_P, _P, _P, _I, _F, _P],
+    "spb_rms_norm_f32in_f16": [_P, _P, _P, _I, _F, _P],
+    "spb_rms_norm_f32in_bf16": [_P, _P, _P, _I, _F, _P],
+    "spb_rope_f16": [_P, _I, _I, _I, _F, _P],
+    "spb_rope_bf16": [_P, _I, _I, _I, _F, _P],
+    "spb_scatter_kv": [_P, _P, _I, _I, _I, _I, _P],
+    "spb_attention_scores_f16": [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P],
+    "spb_attention_scores_bf16": [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P],
+    "spb_softmax": [_P, _I, _I, _I, _P],
+    "spb_attention_output_f16": [_P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "spb_attention_output_bf16": [_P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "spb_relu2_mul_f16": [_P, _P, _P, _I, _P],
+    "spb_relu2_mul_bf16": [_P, _P, _P, _I, _P],
+    "spb_relu2_mul_f32_f16": [_P, _P, _P, _I, _P],
+    "spb_relu2_mul_f32_bf16": [_P, _P, _P, _I, _P],
+    "spb_float_to_f16": [_P, _P, _I, _P],
+    "spb_float_to_bf16": [_P, _P, _I, _P],
+    "spb_residual_add_f16": [_P, _P, _P, _I, _P],
+    "spb_residual_add_bf16": [_P, _P, _P, _I, _P],
+    "spb_gemv_f16": [_P, _P, _P, _I, _I, _P],
+    "spb_gemv_bf16": [_P, _P, _P, _I, _I, _P],
+    "spb_argmax_f32": [_P, _I, _P, _P],
     # decode engine (structs passed by pointer)
     "spb_engine_create": [_P, _P, _P, _P, _P, _I, _P],
     "spb_engine_destroy": [_P],

@@ -4,6 +4,7 @@
 // no-op rule), which return before touching the HIP runtime.
 #include <cstdio>
 
+#include "spbitnet/inference_kernels.h"
 #include "spbitnet/sparse_ternary_kernels.h"
 
 int main() {
@@ -19,6 +20,11 @@ int main() {
     spbitnet::fused_sparse_bitlinear_gpu(meta, values, bx, bx, nullptr, 1.0f, 2560, 0, 0, 0);
     spbitnet::absmax_reduce_gpu(bx, nullptr, 0);
     spbitnet::dequantize_gpu(y, hx, nullptr, 1.0f, 0);
+    spbitnet::rms_norm_gpu(hx, nullptr, hx, 0, 1e-5f);
+    spbitnet::rope_gpu(bx, 0, 128, 0, 500000.0f);
+    spbitnet::relu2_mul_f32_gpu(hx, hx, nullptr, 0);
+    spbitnet::residual_add_gpu(bx, bx, bx, 0);
+    spbitnet::half_gemv_gpu(hx, hx, nullptr, 0, 2560);
     std::printf("mirror api ok (abi %d)\n", spb_abi_version());
     return 0;
 }
