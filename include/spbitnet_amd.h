@@ -327,6 +327,21 @@ int spb_engine_decode_steps(spb_engine* engine, int steps);
 /* Device buffers: logits float32 [vocab], tokens int32 [max_seq + 1]. */
 int spb_engine_buffers(const spb_engine* engine, const float** logits, const int** tokens);
 
+/* ---- model loading ----------------------------------------------------------
+ * Model::load (reference include/spbitnet/model.h:99-103, src/model.cu:72-311)
+ * for the on-disk format of python/convert_model.py (docs/compression_format.md
+ * section 4): config.json, manifest.json, .meta/.values uint32 files, float32
+ * norm files, fp16 embedding / LM head (converted to bf16 on upload; a
+ * manifest dtype "bfloat16" is taken as is).  The model owns its device
+ * memory; engines created from spb_model_info borrow it. */
+typedef struct spb_model spb_model;
+int spb_model_load(const char* model_dir, spb_model** model);
+int spb_model_destroy(spb_model* model);
+/* Any output pointer may be NULL; *lm_head is NULL for tied weights. */
+int spb_model_info(const spb_model* model, spb_model_config* config,
+                   const spb_transformer_layer** layers, const uint16_t** embed_tokens,
+                   const uint16_t** lm_head, const float** final_norm, size_t* gpu_bytes);
+
 /* ---- random-init weights on the device ------------------------------------
  * Latent W ~ N(0,1) from a counter-based generator (seed, element index),
  * 2:4 top-2 |W| mask (higher index wins ties), kept value sign(W) (W >= 0 ->

@@ -76,6 +76,9 @@ SIGNATURES = {
     "spb_engine_generate": [_P, _P, _I, _I, _I, _P, _P],
     "spb_engine_decode_steps": [_P, _I],
     "spb_engine_buffers": [_P, _P, _P],
+    "spb_model_load": [ctypes.c_char_p, _P],
+    "spb_model_destroy": [_P],
+    "spb_model_info": [_P, _P, _P, _P, _P, _P, _P],
     "spb_generate_sparse_ternary": [ctypes.c_uint64, _I, _I, _P, _P, _I, _I, _P, _P, _P],
     "spb_generate_normal_bf16": [ctypes.c_uint64, ctypes.c_long, _F, _P, _P],
 }

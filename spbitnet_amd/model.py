@@ -190,6 +190,22 @@ class Model:
                 ffn_sub_norm=torch.ones(I, dtype=torch.float32, device=dev) if sub_norms else None))
         return Model(config, layers, embed, torch.ones(H, dtype=torch.float32, device=dev))
 
+    def engine_args(self):
+        """(config, layer array, embed, lm_head, final_norm) for spb_engine_create."""
+        layers = (_lib.TransformerLayerC * self.config.num_hidden_layers)(
+            *[l.c_struct() for l in self.layers])
+        lm = self.lm_head_weight.data_ptr() if self.lm_head_weight is not None else None
+        return (self.config.c_struct(), layers, self.embed_tokens.data_ptr(), lm,
+                self.final_norm.data_ptr())
+
+    @staticmethod
+    def load(model_dir: str, device="cuda") -> "Model":
+        """Model::load (include/spbitnet/model.h:103)."""
+        return load_model(model_dir, device)
+
+    def save(self, model_dir: str) -> None:
+        save_model(self, model_dir)
+
     def to_host(self) -> dict:
         """Host (numpy) copies of every weight, for the CPU oracle."""
         def npf(t):
@@ -211,6 +227,189 @@ class Model:
         return out
 
 
+# ---- on-disk format (python/convert_model.py; docs/compression_format.md sec. 4) ----
+
+_NORM_NAMES = (("input_layernorm", "input_layernorm"),
+               ("post_attention_layernorm", "post_attention_layernorm"),
+               ("attn_sub_norm", "self_attn.attn_sub_norm"),
+               ("ffn_sub_norm", "mlp.ffn_sub_norm"))
+_PROJ_NAMES = {"q_proj": "self_attn.q_proj", "k_proj": "self_attn.k_proj",
+               "v_proj": "self_attn.v_proj", "o_proj": "self_attn.o_proj",
+               "gate_proj": "mlp.gate_proj", "up_proj": "mlp.up_proj",
+               "down_proj": "mlp.down_proj"}
+_CONFIG_KEYS = ("model_type", "hidden_size", "num_hidden_layers", "num_attention_heads",
+                "num_key_value_heads", "intermediate_size", "vocab_size",
+                "max_position_embeddings", "rms_norm_eps", "rope_theta", "head_dim",
+                "hidden_act", "tie_word_embeddings", "bos_token_id", "eos_token_id")
+
+
+def save_model(model: "Model", model_dir: str) -> None:
+    """Write a model in the reference's converted-model layout: config.json,
+    manifest.json and weights/*.meta|.values|.bin (export_sparse_layer and
+    the export loop of python/convert_model.py).  The embedding and a separate
+    LM head are written as float16, the reference's storage type."""
+    import json
+    import os
+    c = model.config
+    os.makedirs(os.path.join(model_dir, "weights"), exist_ok=True)
+    cfg = {k: getattr(c, k) for k in _CONFIG_KEYS}
+    cfg["tie_word_embeddings"] = model.lm_head_weight is None
+    with open(os.path.join(model_dir, "config.json"), "w") as f:
+        json.dump(cfg, f, indent=2)
+    weights = {}
+
+    def write(name, arr):
+        rel = f"weights/{name}"
+        np.ascontiguousarray(arr).tofile(os.path.join(model_dir, rel))
+        return rel
+
+    def dense16(name, t):
+        a = t.detach().to(torch.float16).cpu().numpy()
+        weights[name] = {"file": write(name + ".bin", a), "dtype": "float16",
+                         "shape": list(a.shape), "nbytes": int(a.nbytes)}
+
+    def f32(name, t):
+        a = t.detach().float().cpu().numpy()
+        weights[name] = {"file": write(name + ".bin", a), "dtype": "float32",
+                         "shape": list(a.shape), "nbytes": int(a.nbytes)}
+
+    dense16("embed_tokens", model.embed_tokens)
+    f32("norm", model.final_norm)
+    if model.lm_head_weight is None:
+        weights["lm_head"] = {"tied_to": "embed_tokens", "dtype": "tied"}
+    else:
+        dense16("lm_head", model.lm_head_weight)
+    for li, L in enumerate(model.layers):
+        for attr, name in _NORM_NAMES:
+            t = getattr(L, attr)
+            if t is not None:
+                f32(f"layers.{li}.{name}", t)
+        for attr, name in _PROJ_NAMES.items():
+            s = getattr(L, attr)
+            full = f"layers.{li}.{name}"
+            m = s.meta.cpu().numpy().view(np.uint32)
+            v = s.values.cpu().numpy().view(np.uint32)
+            weights[full] = {"meta_file": write(full + ".meta", m),
+                             "values_file": write(full + ".values", v),
+                             "dtype": "sparse_ternary", "shape": [s.rows, s.cols],
+                             "meta_stride": s.meta_stride, "values_stride": s.values_stride,
+                             "gamma": float(s.gamma), "meta_nbytes": int(m.nbytes),
+                             "values_nbytes": int(v.nbytes)}
+    with open(os.path.join(model_dir, "manifest.json"), "w") as f:
+        json.dump({"format_version": 1, "weights": weights}, f, indent=1)
+
+
+def load_model(model_dir: str, device="cuda") -> "Model":
+    """Model::load (src/model.cu:180-311) in Python: reads the converted-model
+    layout into torch device tensors; the fp16 embedding / LM head become
+    bf16."""
+    import json
+    import os
+    dev = torch.device(device)
+    with open(os.path.join(model_dir, "config.json")) as f:
+        cj = json.load(f)
+    with open(os.path.join(model_dir, "manifest.json")) as f:
+        w = json.load(f)["weights"]
+    nh = cj["num_attention_heads"]
+    c = ModelConfig(hidden_size=cj["hidden_size"], num_hidden_layers=cj["num_hidden_layers"],
+                    num_attention_heads=nh,
+                    num_key_value_heads=cj.get("num_key_value_heads", nh),
+                    intermediate_size=cj["intermediate_size"], vocab_size=cj["vocab_size"],
+                    max_position_embeddings=cj["max_position_embeddings"],
+                    head_dim=cj.get("head_dim", cj["hidden_size"] // nh),
+                    rms_norm_eps=cj.get("rms_norm_eps", 1e-5),
+                    rope_theta=cj.get("rope_theta", 10000.0),
+                    bos_token_id=cj.get("bos_token_id", 1), eos_token_id=cj.get("eos_token_id", 2),
+                    model_type=cj.get("model_type", "bitnet"),
+                    hidden_act=cj.get("hidden_act", "relu2"),
+                    tie_word_embeddings=cj.get("tie_word_embeddings", False))
+
+    def raw(rel, dtype, count):
+        a = np.fromfile(os.path.join(model_dir, rel), dtype=dtype)
+        if a.size != count:
+            raise ValueError(f"{rel}: {a.size} elements, expected {count}")
+        return a
+
+    def f32(name, n):
+        if name not in w:
+            return None
+        return torch.from_numpy(raw(w[name]["file"], "<f4", n).copy()).to(dev)
+
+    def dense16(e, n):
+        if e.get("dtype") == "bfloat16":
+            bits = raw(e["file"], "<u2", n).view(np.int16)
+            return torch.from_numpy(bits.copy()).view(torch.bfloat16).reshape(c.vocab_size, c.hidden_size).to(dev)
+        a = raw(e["file"], "<f2", n)
+        return torch.from_numpy(a.copy()).to(dev).to(torch.bfloat16).reshape(c.vocab_size, c.hidden_size)
+
+    H, I = c.hidden_size, c.intermediate_size
+    kvd = c.num_key_value_heads * c.head_dim
+    shapes = {"q_proj": (H, H), "k_proj": (kvd, H), "v_proj": (kvd, H), "o_proj": (H, H),
+              "gate_proj": (I, H), "up_proj": (I, H), "down_proj": (H, I)}
+    embed = dense16(w["embed_tokens"], c.vocab_size * H)
+    lm = None
+    if "lm_head" in w and w["lm_head"].get("dtype") != "tied":
+        lm = dense16(w["lm_head"], c.vocab_size * H)
+    layers = []
+    for li in range(c.num_hidden_layers):
+        lin = {}
+        for attr, name in _PROJ_NAMES.items():
+            e = w[f"layers.{li}.{name}"]
+            rows, cols = e["shape"]
+            if (rows, cols) != shapes[attr]:
+                raise ValueError(f"layers.{li}.{name}: shape {rows}x{cols}, expected {shapes[attr]}")
+            ms, vs = e["meta_stride"], e["values_stride"]
+            m = torch.from_numpy(raw(e["meta_file"], "<u4", rows * ms).view(np.int32).reshape(rows, ms).copy())
+            v = torch.from_numpy(raw(e["values_file"], "<u4", rows * vs).view(np.int32).reshape(rows, vs).copy())
+            lin[attr] = SparseLinear(m.to(dev), v.to(dev), float(np.float32(e["gamma"])), rows, cols,
+                                     ms, vs)
+        norms = {attr: f32(f"layers.{li}.{name}", I if attr == "ffn_sub_norm" else H)
+                 for attr, name in _NORM_NAMES}
+        layers.append(TransformerLayer(**lin, **norms))
+    return Model(c, layers, embed, f32("norm", H), lm)
+
+
+class NativeModel:
+    """A model loaded by the library's own loader (spb_model_load, C++):
+    the form a C++ host uses; device memory owned by the library."""
+
+    def __init__(self, model_dir: str):
+        self._L = _lib.load()
+        h = ctypes.c_void_p()
+        _lib.check(self._L.spb_model_load(model_dir.encode(), ctypes.byref(h)), "spb_model_load")
+        self._h = h
+        cfg = _lib.ModelConfigC()
+        layers = ctypes.c_void_p()
+        emb, lm, fn, nbytes = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_size_t()
+        _lib.check(self._L.spb_model_info(self._h, ctypes.byref(cfg), ctypes.byref(layers),
+                                          ctypes.byref(emb), ctypes.byref(lm), ctypes.byref(fn),
+                                          ctypes.byref(nbytes)), "spb_model_info")
+        self._cfg, self._layers_ptr = cfg, layers.value
+        self._embed, self._lm, self._final = emb.value, lm.value, fn.value
+        self.gpu_bytes = nbytes.value
+        self.config = ModelConfig(hidden_size=cfg.hidden_size,
+                                  num_hidden_layers=cfg.num_hidden_layers,
+                                  num_attention_heads=cfg.num_attention_heads,
+                                  num_key_value_heads=cfg.num_key_value_heads,
+                                  intermediate_size=cfg.intermediate_size,
+                                  vocab_size=cfg.vocab_size,
+                                  max_position_embeddings=cfg.max_position_embeddings,
+                                  head_dim=cfg.head_dim, rms_norm_eps=cfg.rms_norm_eps,
+                                  rope_theta=cfg.rope_theta, bos_token_id=cfg.bos_token_id,
+                                  eos_token_id=cfg.eos_token_id)
+
+    def engine_args(self):
+        return (self._cfg, ctypes.c_void_p(self._layers_ptr), self._embed, self._lm, self._final)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._L.spb_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+
 class InferenceEngine:
     """InferenceEngine (reference include/spbitnet/inference.h:23-70) over the
     HIP decode engine: forward() one token at a time, reset(), seq_len(), plus
@@ -221,15 +420,11 @@ class InferenceEngine:
         c = model.config
         self.max_seq = int(max_seq or c.max_position_embeddings)
         self._L = _lib.load()
-        self._layers = (_lib.TransformerLayerC * c.num_hidden_layers)(
-            *[l.c_struct() for l in model.layers])
-        self._cfg = c.c_struct()
+        cfg, layers, embed, lm, final = model.engine_args()
+        self._cfg, self._layers = cfg, layers
         h = ctypes.c_void_p()
-        lm = model.lm_head_weight.data_ptr() if model.lm_head_weight is not None else None
-        _lib.check(self._L.spb_engine_create(ctypes.byref(self._cfg), self._layers,
-                                             model.embed_tokens.data_ptr(), lm,
-                                             model.final_norm.data_ptr(), self.max_seq,
-                                             ctypes.byref(h)), "spb_engine_create")
+        _lib.check(self._L.spb_engine_create(ctypes.byref(cfg), layers, embed, lm, final,
+                                             self.max_seq, ctypes.byref(h)), "spb_engine_create")
         self._h = h
         self._stream = stream if stream is not None else torch.cuda.current_stream()
         _lib.check(self._L.spb_engine_set_stream(self._h, self._stream.cuda_stream or None),
@@ -239,7 +434,7 @@ class InferenceEngine:
                    "spb_engine_buffers")
         self._logits_ptr = lp.value
         self._logits = torch.empty(c.vocab_size, dtype=torch.float32,
-                                   device=model.embed_tokens.device)
+                                   device=torch.device("cuda", torch.cuda.current_device()))
 
     def close(self) -> None:
         if getattr(self, "_h", None):
