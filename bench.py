@@ -11,10 +11,12 @@ streams from HBM) reduced by one launch of the drop-in GEMV entry point
 
 The JSON line reports
   value      algorithmic GB/s of the step (packed weight bytes + x + y per
-             launch, divided by the step time; inputs resident in HBM)
-  roofline   the bit-plane GEMV kernel: algorithmic bytes per launch / its
-             average launch duration from HIP events around each launch on
-             the launch stream, against the 8 TB/s HBM peak
+             launch, divided by the step time; inputs resident in HBM; the
+             step is replayed from a HIP graph)
+  roofline   the streaming GEMV kernel: algorithmic bytes per launch / its
+             average launch duration (HIP events on the launch stream around
+             a graph of 10 back-to-back launches per shape), against the
+             8 TB/s HBM peak
   cpu_baseline  the reference's CPU GEMV (its own unpack_to_int8 + int32 MAC,
              built from the reference sources into oracle/_ref) on the
              6912x2560 matrix, single thread, on this host
@@ -51,7 +53,7 @@ def read_traffic():
     """HBM bytes per launch of the streamed GEMV, from the committed rocprofv3
     PMC summary (FETCH_SIZE and WRITE_SIZE runs, scaled by a copy of known
     size); None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", "gemv_bitplane_streamed_config1.pmc.json")
+    path = os.path.join(ROOT, "profiles", "gemv_stream_config1.pmc.json")
     try:
         with open(path) as f:
             d = json.load(f)
@@ -213,8 +215,9 @@ def main() -> int:
     step_bytes = sum(gemv_bytes(r, c) for (_, _, _, _, _, r, c, _, _) in launches)
 
     def launch(item):
+        # torch's current stream: the capture stream inside torch.cuda.graph()
         _, sm, sv, xx, sy, rows, cols, ms, vs = item
-        K.sparse_ternary_gemv_gpu(sm, sv, xx, sy, rows, cols, ms, vs, stream=stream)
+        K.sparse_ternary_gemv_gpu(sm, sv, xx, sy, rows, cols, ms, vs)
 
     def step():
         for item in launches:
@@ -229,36 +232,50 @@ def main() -> int:
             return 1
     log("streamed outputs exact")
 
-    for _ in range(args.warmup):
+    # The step is replayed from a HIP graph (captured once: one launch per
+    # shape), so the host's per-launch cost stays out of the GPU timeline.
+    g_step = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_step):
         step()
+    for _ in range(args.warmup):
+        g_step.replay()
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps")
     e0, e1 = ev(), ev()
     e0.record(stream)
     for _ in range(args.steps):
-        step()
+        g_step.replay()
     e1.record(stream)
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
     value_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    del g_step
 
-    # per-launch durations (events bracketing each launch)
-    per_launch = []
-    for _ in range(max(3, min(args.steps, 10))):
-        for item in launches:
-            a, b = ev(), ev()
-            a.record(stream)
-            launch(item)
-            b.record(stream)
-            torch.cuda.synchronize()
-            per_launch.append((item[0], a.elapsed_time(b) * 1e3))
-    avg_us = sum(t for _, t in per_launch) / len(per_launch)
+    # Average launch duration of the GEMV kernel: HIP events around a graph of
+    # 10 back-to-back launches of one shape on the launch stream (the events
+    # bracket kernels only; consecutive graph kernels start ~1-2 us apart,
+    # which this average includes).
+    per_shape = {}
+    for item in launches:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(10):
+                launch(item)
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = ev(), ev()
+        a.record(stream)
+        for _ in range(3):
+            g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        per_shape[item[0]] = a.elapsed_time(b) * 1e3 / 30
+        del g
+    avg_us = sum(per_shape.values()) / len(per_shape)
     avg_bytes = step_bytes / len(launches)
     kernel_gbs = avg_bytes / (avg_us * 1e-6) / 1e9
     detail = {
-        "streamed_launch_us": {k: round(sum(t for kk, t in per_launch if kk == k) /
-                                        max(1, sum(1 for kk, _ in per_launch if kk == k)), 2)
-                               for k in ("gate", "down")},
+        "streamed_launch_us": {k: round(v, 2) for k, v in per_shape.items()},
         "copies_per_shape": args.copies,
     }
     del launches
@@ -436,7 +453,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_bitplane_kernel",
+            "kernel": "gemv_stream_kernel",
             "achieved": round(kernel_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -88,10 +88,11 @@ struct SegWeights {
 
 // v_bitop3_b32 truth tables: bit i of the table is f(a, b, c) with a, b, c
 // the bits of 0xF0, 0xCC, 0xAA at position i (a = first operand).
-constexpr uint32_t kOrAnd = 0xC8;       // (a | c) & b
-constexpr uint32_t kXorAnd = 0x28;      // (a ^ b) & c
-constexpr uint32_t kSelectKeep = 0x4A;  // a ? (b & ~c) : c
-constexpr uint32_t kXor3 = 0x96;        // a ^ b ^ c
+constexpr uint32_t kOrAnd = 0xC8;    // (a | c) & b
+constexpr uint32_t kXorAnd = 0x28;   // (a ^ b) & c
+constexpr uint32_t kKeptXor = 0x48;  // b & (a ^ c)
+constexpr uint32_t kSelect = 0xCA;   // a ? b : c
+constexpr uint32_t kXor3 = 0x96;     // a ^ b ^ c
 
 template <uint32_t kTable>
 __device__ __forceinline__ uint32_t bitop3(uint32_t a, uint32_t b, uint32_t c) {
@@ -284,41 +285,49 @@ struct DequantSink {
 
 // ---- bit-plane decode of one 128-column chunk ----------------------------------
 
-// Mask of the columns holding -1 in one meta word (8 groups, 32 columns).
-// k: the meta word; vw: the values word holding these groups' sign pairs,
-// in its low (upper_half = false) or high 16 bits.
-__device__ __forceinline__ uint32_t neg_mask(uint32_t k, uint32_t vw, bool upper_half) {
-    // Spread group g's sign pair to nibble g: s_lo -> bit 4g, s_hi -> bit 4g+1.
+// A mask that holds, at each kept column of one meta word (8 groups, 32
+// columns), that column's sign bit; its other bits are unspecified.
+// k: the meta word; vw: the values word holding these groups' sign pairs, in
+// its low (upper_half = false) or high 16 bits.
+//   * The 2-bit sign pairs are spread to nibble g: s_lo of group g to bit 4g,
+//     s_hi to bit 4g+1 (perm, then two shift-and-mask steps), and each is
+//     copied over three bits by one packed 16-bit multiply by 7 (set bits at
+//     nibble bases or nibble bit 1, so no carries): s_lo over bits 0..2 of the
+//     nibble (where the lower kept column can be), s_hi over bits 1..3.
+//   * d = k - 0x11111111 subtracts 1 from every nibble without borrows (each
+//     nibble holds two set bits): it clears the lower kept bit and keeps the
+//     higher one, so "d ? s_hi : s_lo" is s_lo at the lower kept column and
+//     s_hi at the higher.
+__device__ __forceinline__ uint32_t sign_mask(uint32_t k, uint32_t vw, bool upper_half) {
     // perm gives bytes [b0, 0, b1, 0] (or [b2, 0, b3, 0]); selector 0x0C is 0x00.
     uint32_t t = __builtin_amdgcn_perm(vw, vw, upper_half ? 0x0C030C02u : 0x0C010C00u);
     t = bitop3<kOrAnd>(t << 4, 0x0F0F0F0Fu, t);
     const uint32_t a0 = bitop3<kOrAnd>(t << 2, 0x11111111u, t);  // s_lo at nibble bit 0
     const uint32_t a1 = bitop3<kOrAnd>(t << 2, 0x22222222u, t);  // s_hi at nibble bit 1
-    const uint32_t s_lo = times7_halves(a0);                      // over nibble bits 0..2
-    const uint32_t s_hi = times7_halves(a1);                      // over nibble bits 1..3
-    // Each nibble of k holds exactly two set bits, so subtracting 1 per nibble
-    // never borrows across nibbles: hi = higher kept column, k ^ hi = lower.
-    const uint32_t hi = k & (k - 0x11111111u);
-    return (hi & s_hi) | bitop3<kXorAnd>(k, hi, s_lo);
+    return bitop3<kSelect>(k - 0x11111111u, times7_halves(a1), times7_halves(a0));
 }
 
-// X[w][b]: plane b of the chunk's meta word w.
+// X[w][b]: plane b of the chunk's meta word w.  Per plane, with P / N the
+// kept columns holding +1 / -1 and M = sign_mask (M = N on kept columns):
+//   popc((X & P) | (~X & N)) = popc(K & (X ^ M)),
+// one v_bitop3 and one accumulating v_bcnt.  The popc(N) term (weight 1, like
+// plane 0) is the number of set sign bits: popc of the two values words.
+// The weighted sum of the plane counts is evaluated by Horner's rule from
+// plane 7 (weight -128) down, one shift-and-add per plane.
 __device__ __forceinline__ int chunk_dot(const uint4 K, const uint2 V, const uint32_t (&X)[4][8]) {
     const uint32_t kw[4] = {K.x, K.y, K.z, K.w};
     int cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int cneg = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        const uint32_t neg = neg_mask(kw[w], w < 2 ? V.x : V.y, (w & 1) != 0);
-        // (X & P) | (~X & N) with P = k & ~N, as one 3-input op of (X, k, N)
+        const uint32_t m = sign_mask(kw[w], w < 2 ? V.x : V.y, (w & 1) != 0);
 #pragma unroll
-        for (int b = 0; b < 8; ++b)
-            cnt[b] = bcnt_acc(bitop3<kSelectKeep>(X[w][b], kw[w], neg), cnt[b]);
-        cneg = bcnt_acc(neg, cneg);
+        for (int b = 0; b < 8; ++b) cnt[b] = bcnt_acc(bitop3<kKeptXor>(X[w][b], kw[w], m), cnt[b]);
     }
-    int s = cneg - (cnt[7] << 7);
+    cnt[0] = bcnt_acc(V.x, cnt[0]);
+    cnt[0] = bcnt_acc(V.y, cnt[0]);
+    int s = cnt[6] - 2 * cnt[7];
 #pragma unroll
-    for (int b = 0; b < 7; ++b) s += cnt[b] << b;
+    for (int b = 5; b >= 0; --b) s = (s << 1) + cnt[b];
     return s;
 }
 
@@ -423,6 +432,192 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Si
         step = step_n;
         tile = tile_n;
         row = row_n;
+    }
+}
+
+// ---- streaming kernel for one packed matrix -------------------------------------
+//
+// The same per-chunk arithmetic, laid out for matrices much larger than one
+// pass of the grid.  Thread (ro, c) = (tid / C, tid % C) owns the 128-column
+// chunk c of row s * RS + ro in step s.  The F = rows / RS full steps are
+// split into contiguous ranges [b*F/G, (b+1)*F/G), one per block, so every
+// block streams one contiguous span of the matrix and the blocks differ by at
+// most one step; the last block also takes the rows % RS tail rows.  A
+// block's row sums all live in LDS (integer atomics) and are written once,
+// after the loop.  In the loop a load is a buffer load through a resource
+// whose base is the step's first row (scalar registers) plus the thread's
+// fixed byte offset, with no bounds test (threads beyond RS rows per step
+// read row 0 of the step and drop the sum).  Four register sets rotate, so
+// three steps are in flight while one is reduced.  The loop body holds only
+// loads, bit arithmetic and LDS atomics (no barrier, no global store, no
+// early exit), which keeps the compiler's wait counts exact: each wait
+// covers the step being reduced and never the ones in flight.
+struct StreamLoad {
+    uint4 k;
+    uint2 v;
+};
+
+// Buffer resource word 3 for gfx9-family raw (unformatted, stride 0) loads.
+constexpr int kBufferFlags = 0x00020000;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 as_uint4(u32x4_t v) { return make_uint4(v.x, v.y, v.z, v.w); }
+__device__ __forceinline__ uint2 as_uint2(u32x2_t v) { return make_uint2(v.x, v.y); }
+
+constexpr int kStreamMaxRows = 8192;  // LDS row sums per block (32 KB)
+
+// At most 80 VGPRs: 6 waves per SIMD, three 512-thread blocks per CU.
+template <class Act, class Sink>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6)))
+void gemv_stream_kernel(Weights wt, Act act, Sink sink, int nfull, int row_base) {
+    extern __shared__ uint32_t smem[];
+    const int nwords = wt.cols >> 5;
+    const int C = wt.cols / kChunk;
+    const int RS = kBlock / C;  // rows per step
+    const int rows = wt.rows;
+    // step indices stay 32-bit (scalar compares; rows < 2^31)
+    const int s_begin = static_cast<int>(static_cast<long>(nfull) * blockIdx.x / gridDim.x);
+    const int s_end = static_cast<int>(static_cast<long>(nfull) * (blockIdx.x + 1) / gridDim.x);
+    const bool last = blockIdx.x == gridDim.x - 1;
+    const int tail = last ? rows - nfull * RS : 0;   // rows after the full steps
+    const int span = (s_end - s_begin) * RS + tail;  // rows of this block
+    uint32_t* planes = smem;
+    int* acc = reinterpret_cast<int*>(smem + 8 * nwords);
+    const int acc_slots = (span + RS + 3) & ~3;
+
+    const int tid = threadIdx.x;
+    const int c = tid % C;
+    const int ro = tid / C;
+    const bool active = ro < RS;
+    // per-thread byte offsets from the step's first row (inactive threads: row 0)
+    const int om = active ? (ro * wt.ms + 4 * c) * 4 : 16 * c;
+    const int ov = active ? (ro * wt.vs + 2 * c) * 4 : 8 * c;
+
+    // Buffer extents in bytes from the step's first row to the matrix end,
+    // capped below 2^31 (all scalar 32-bit arithmetic).
+    const int ms4 = wt.ms * 4, vs4 = wt.vs * 4;
+    const int cap_m = 0x7FFFFFFF / ms4, cap_v = 0x7FFFFFFF / vs4;
+    auto load = [&](int s) {
+        const int ub = s * RS;
+        const int left = rows - ub;
+        const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t*>(wt.meta + static_cast<long>(ub) * wt.ms), static_cast<short>(0),
+            (left < cap_m ? left : cap_m) * ms4, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t*>(wt.values + static_cast<long>(ub) * wt.vs),
+            static_cast<short>(0), (left < cap_v ? left : cap_v) * vs4, kBufferFlags);
+        StreamLoad L;
+        L.k = as_uint4(__builtin_amdgcn_raw_buffer_load_b128(rm, om, 0, 0));
+        L.v = as_uint2(__builtin_amdgcn_raw_buffer_load_b64(rv, ov, 0, 0));
+        return L;
+    };
+
+    const int n = s_end - s_begin;
+    const int s_last = n > 0 ? s_end - 1 : 0;
+    auto at = [&](int s) { return s < s_end ? s : s_last; };
+
+    // The activation loads go first (they head the prologue's chain), then
+    // the first three steps' weights, which arrive while the prologue runs.
+    typename Act::Regs regs;
+    act.issue(tid, regs);
+    StreamLoad S0 = load(at(s_begin)), S1 = load(at(s_begin + 1)), S2 = load(at(s_begin + 2)), S3;
+    act.prepare();
+    sink.prepare();
+    act.build(planes, wt.cols, tid,
+              reinterpret_cast<float*>(smem + ((8 * nwords + acc_slots + 3) & ~3)), regs);
+    for (int i = tid; i < acc_slots; i += kBlock) acc[i] = 0;
+    __syncthreads();
+    sink.bind(act);
+    uint32_t X[4][8];
+    load_x(planes + c * 32, X);
+
+    auto reduce = [&](int s, const StreamLoad& L) {
+        const int d = chunk_dot(L.k, L.v, X);
+        if (active) atomicAdd(&acc[(s - s_begin) * RS + ro], d);
+    };
+
+    if (n > 0) {
+        // A counted loop over groups of four steps with its only exit at the
+        // latch (a mid-body exit would join the loop head on a path with fewer
+        // loads in flight, and the compiler's merged wait state would then
+        // drain every load each iteration).  Loads past the last step re-read
+        // the last step.  sched_barrier keeps each load where it is written
+        // (the scheduler otherwise sinks loads into the reduction before them).
+        __builtin_amdgcn_sched_barrier(0);
+        int s = s_begin;
+        for (int q = 0; q < (n >> 2); ++q, s += 4) {
+            S3 = load(at(s + 3));
+            __builtin_amdgcn_sched_barrier(0);
+            reduce(s, S0);
+            S0 = load(at(s + 4));
+            __builtin_amdgcn_sched_barrier(0);
+            reduce(s + 1, S1);
+            S1 = load(at(s + 5));
+            __builtin_amdgcn_sched_barrier(0);
+            reduce(s + 2, S2);
+            S2 = load(at(s + 6));
+            __builtin_amdgcn_sched_barrier(0);
+            reduce(s + 3, S3);
+        }
+        // the n % 4 remaining steps are s, s+1, s+2, held in S0, S1, S2
+        if (n & 3) reduce(s, S0);
+        if ((n & 3) > 1) reduce(s + 1, S1);
+        if ((n & 3) > 2) reduce(s + 2, S2);
+    }
+    if (tail > 0 && active && ro < tail) {  // the last block's partial step
+        const long r = static_cast<long>(nfull) * RS + ro;
+        const uint4 k = *reinterpret_cast<const uint4*>(wt.meta + r * wt.ms + 4 * c);
+        const uint2 v = *reinterpret_cast<const uint2*>(wt.values + r * wt.vs + 2 * c);
+        atomicAdd(&acc[n * RS + ro], chunk_dot(k, v, X));
+    }
+    __syncthreads();
+    const int row0 = s_begin * RS;
+    for (int j = tid; j < span; j += kBlock)
+        sink.store(static_cast<long>(row_base) + row0 + j, acc[j]);
+}
+
+// Grid: the resident capacity (each block a contiguous range of steps).  A
+// matrix whose per-block span would exceed kStreamMaxRows is split into
+// consecutive row ranges, one launch each.  Blocks per CU: the register
+// limit (queried once per instantiation) and the LDS of the launch.
+template <class Act, class Sink>
+void launch_stream(const Weights& wt, Act act, Sink sink, hipStream_t stream) {
+    static int regs_per_cu = 0;
+    if (regs_per_cu <= 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<Act, Sink>, kBlock,
+                                                         0) != hipSuccess ||
+            n <= 0)
+            n = 1;
+        regs_per_cu = n;
+    }
+    const long lds_cu = device_lds_per_cu();
+    const int C = wt.cols / kChunk;
+    const long RS = kBlock / C;
+    const long fixed = static_cast<long>(wt.cols) + static_cast<long>(Act::extra_lds(wt.cols)) + 48;
+    for (long r0 = 0; r0 < wt.rows;) {
+        const long left = wt.rows - r0;
+        long per_cu = regs_per_cu, grid = 1, nfull = 0, n = left;
+        size_t lds = 0;
+        for (;;) {
+            const long resident = per_cu * device_cu_count();
+            // at most kStreamMaxRows rows of sums per block
+            const long max_rows = resident * (kStreamMaxRows / RS - 1) * RS;
+            n = left < max_rows ? left : max_rows;
+            nfull = n / RS;
+            grid = nfull < resident ? nfull : resident;
+            if (grid < 1) grid = 1;
+            const long steps_per_block = (nfull + grid - 1) / grid;
+            lds = static_cast<size_t>(fixed + ((steps_per_block + 2) * RS + 8) * 4);
+            if (per_cu == 1 || per_cu * static_cast<long>(lds) <= lds_cu) break;
+            --per_cu;
+        }
+        Weights part{wt.meta + r0 * wt.ms, wt.values + r0 * wt.vs, static_cast<int>(n), wt.cols,
+                     wt.ms, wt.vs};
+        hipLaunchKernelGGL((gemv_stream_kernel<Act, Sink>), dim3(static_cast<int>(grid)),
+                           dim3(kBlock), lds, stream, part, act, sink, static_cast<int>(nfull),
+                           static_cast<int>(r0));
+        r0 += n;
     }
 }
 

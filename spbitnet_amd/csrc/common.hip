@@ -11,6 +11,7 @@ namespace {
 thread_local char g_err[512] = {0};
 constexpr int kMaxDevices = 64;
 int g_cu_count[kMaxDevices] = {0};
+int g_lds_per_cu[kMaxDevices] = {0};
 }  // namespace
 
 void set_error(const char* fmt, ...) {
@@ -50,6 +51,20 @@ int device_cu_count() {
             n <= 0)
             n = 256;
         g_cu_count[dev] = n;
+    }
+    return n;
+}
+
+int device_lds_per_cu() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 65536;
+    int n = g_lds_per_cu[dev];
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) !=
+                hipSuccess ||
+            n <= 0)
+            n = 65536;
+        g_lds_per_cu[dev] = n;
     }
     return n;
 }

@@ -29,6 +29,9 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// LDS bytes per compute unit of the current device (cached per device).
+int device_lds_per_cu();
+
 // ---- 16-bit float conversions (bit patterns in uint16_t) --------------------
 
 struct F16 {

@@ -8,19 +8,20 @@
 //
 // How it is computed here (bit-plane kernel):
 //   * A meta word is directly a 32-column keep mask K (bit j <=> column
-//     32w+j kept).  The 2-bit sign pairs are expanded in registers into the
-//     mask N of columns holding -1 with nibble-parallel bit tricks:
-//     H = K & (K - 0x1111_1111) isolates the higher kept bit of every group
-//     (no borrow crosses a nibble since each holds two set bits), K ^ H the
-//     lower one; no lookup table.
+//     32w+j kept).  The 2-bit sign pairs are expanded in registers into a
+//     mask M holding each kept column's sign bit, with nibble-parallel bit
+//     tricks and no lookup table: D = K - 0x1111_1111 clears the lower kept
+//     bit of every group and keeps the higher one (no borrow crosses a
+//     nibble since each holds two set bits), so M = D ? s_hi : s_lo.
 //   * The int8 activations are used as 8 bit planes (X_b: bit j = bit b of
 //     column j's two's-complement byte).  For the columns of a meta word,
+//     with P / N the kept columns holding +1 / -1,
 //       sum_{j in P} x_j - sum_{j in N} x_j
 //         = sum_b c_b * popc((X_b & P) | (~X_b & N)) + popc(N),
-//     P = K & ~N, c_b = 2^b (b < 7), c_7 = -128.  The select is one
-//     v_bitop3_b32 of (X_b, K, N) and the count one accumulating
-//     v_bcnt_u32_b32: two VALU ops per plane per 32 columns, additions and
-//     bit operations only, no multiplies on the activations.
+//     c_b = 2^b (b < 7), c_7 = -128, and (X_b & P) | (~X_b & N) = K & (X_b ^ M):
+//     one v_bitop3_b32 and one accumulating v_bcnt_u32_b32 per plane per 32
+//     columns, additions and bit operations only, no multiplies on the
+//     activations.  popc(N) is the number of set sign bits.
 //   * Plane layout (shared by LDS and the global "activation planes" format):
 //     word [w * 8 + b] holds plane b of columns 32w .. 32w+31, so the 8
 //     planes of a 128-column chunk are 128 contiguous bytes.  Planes come
@@ -28,13 +29,13 @@
 //     thread (SWAR 8x8 bit transpose, lane-parallel, one load per thread),
 //     or precomputed in global memory by spb_activation_planes /
 //     spb_absmax_quantize_planes_*.
-//   * Work mapping: a thread owns one 128-column chunk (16 bytes of meta, 8 of
-//     signs, 128/64-bit vector loads) and keeps that chunk's 32 plane words
-//     in registers for every row it visits; consecutive threads take
-//     consecutive chunks of consecutive rows, so each load instruction of a
-//     block reads one contiguous span.  Per-row partial sums meet in LDS
-//     (integer atomics: exact in any order).  Blocks stride over row tiles so
-//     a large matrix is streamed by a grid sized to the resident capacity.
+//   * Work mapping (streaming kernel): a thread owns one 128-column chunk
+//     (16 bytes of meta, 8 of signs, 128/64-bit buffer loads) and keeps that
+//     chunk's 32 plane words in registers for every row it visits;
+//     consecutive threads take consecutive chunks of consecutive rows, so
+//     each load instruction of a block reads one contiguous span.  Each block
+//     streams a contiguous range of rows with three steps of loads in flight;
+//     per-row partial sums meet in LDS (integer atomics: exact in any order).
 // Shapes the bit-plane kernel does not take (cols % 128 != 0, cols > 32768,
 // unaligned rows or activations) go to a general wave-per-row kernel.
 #include "bitplane.hpp"
@@ -140,7 +141,7 @@ int fused_bitlinear(const char* fn, const uint32_t* meta, const uint32_t* values
     const QuantSrc<T> src{x, d_absmax, 0.0f};
     const DequantSink<T> sink{output, d_absmax, gamma, 0.0f};
     if (bitplane_ok(meta, values, cols, ms, vs) && aligned(x, 16))
-        launch_bitplane(wt, BuildPlanes<QuantSrc<T>>{src}, sink, as_stream(stream));
+        launch_stream(wt, BuildPlanes<QuantSrc<T>>{src}, sink, as_stream(stream));
     else
         launch_general(wt, src, sink, as_stream(stream));
     return launch_status(fn);
@@ -158,7 +159,7 @@ int fused_bitlinear_planes(const char* fn, const uint32_t* meta, const uint32_t*
     const Weights wt{meta, values, rows, cols, ms, vs};
     const DequantSink<T> sink{output, d_absmax, gamma, 0.0f};
     if (bitplane_ok(meta, values, cols, ms, vs))
-        launch_bitplane(wt, GlobalPlanes{planes}, sink, as_stream(stream));
+        launch_stream(wt, GlobalPlanes{planes}, sink, as_stream(stream));
     else
         launch_general(wt, PlaneSrc{planes}, sink, as_stream(stream));
     return launch_status(fn);
@@ -215,7 +216,7 @@ extern "C" int spb_sparse_ternary_gemv(const uint32_t* meta, const uint32_t* val
     if (!x || !y) return invalid("%s: null activation or output pointer", fn);
     const Weights wt{meta, values, rows, cols, ms, vs};
     if (bitplane_ok(meta, values, cols, ms, vs) && aligned(x, 16))
-        launch_bitplane(wt, BuildPlanes<Int8Src>{Int8Src{x}}, Int32Sink{y}, as_stream(stream));
+        launch_stream(wt, BuildPlanes<Int8Src>{Int8Src{x}}, Int32Sink{y}, as_stream(stream));
     else
         launch_general(wt, Int8Src{x}, Int32Sink{y}, as_stream(stream));
     return launch_status(fn);
@@ -232,7 +233,7 @@ extern "C" int spb_sparse_ternary_gemv_planes(const uint32_t* meta, const uint32
     if (!aligned(planes, 16)) return invalid("%s: planes must be 16-byte aligned", fn);
     const Weights wt{meta, values, rows, cols, ms, vs};
     if (bitplane_ok(meta, values, cols, ms, vs))
-        launch_bitplane(wt, GlobalPlanes{planes}, Int32Sink{y}, as_stream(stream));
+        launch_stream(wt, GlobalPlanes{planes}, Int32Sink{y}, as_stream(stream));
     else
         launch_general(wt, PlaneSrc{planes}, Int32Sink{y}, as_stream(stream));
     return launch_status(fn);
