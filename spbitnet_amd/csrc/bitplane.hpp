@@ -466,10 +466,8 @@ __device__ __forceinline__ uint2 as_uint2(u32x2_t v) { return make_uint2(v.x, v.
 
 constexpr int kStreamMaxRows = 8192;  // LDS row sums per block (32 KB)
 
-// At most 80 VGPRs: 6 waves per SIMD, three 512-thread blocks per CU.
 template <class Act, class Sink>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6)))
-void gemv_stream_kernel(Weights wt, Act act, Sink sink, int nfull, int row_base) {
+__global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act, Sink sink, int nfull, int row_base) {
     extern __shared__ uint32_t smem[];
     const int nwords = wt.cols >> 5;
     const int C = wt.cols / kChunk;
@@ -576,42 +574,26 @@ void gemv_stream_kernel(Weights wt, Act act, Sink sink, int nfull, int row_base)
         sink.store(static_cast<long>(row_base) + row0 + j, acc[j]);
 }
 
-// Grid: the resident capacity (each block a contiguous range of steps).  A
-// matrix whose per-block span would exceed kStreamMaxRows is split into
-// consecutive row ranges, one launch each.  Blocks per CU: the register
-// limit (queried once per instantiation) and the LDS of the launch.
+// Grid: one block per CU, each a contiguous range of steps.  On MI355X a
+// cold 265 MB pass (80 x 6912x2560) ran in ~51 us with one 512-thread block
+// per CU and ~61 / ~65 us with two / three (the register limit), so more
+// resident waves lose to fewer, longer streams.  A matrix whose per-block
+// span would exceed kStreamMaxRows is split into consecutive row ranges, one
+// launch each.
 template <class Act, class Sink>
 void launch_stream(const Weights& wt, Act act, Sink sink, hipStream_t stream) {
-    static int regs_per_cu = 0;
-    if (regs_per_cu <= 0) {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<Act, Sink>, kBlock,
-                                                         0) != hipSuccess ||
-            n <= 0)
-            n = 1;
-        regs_per_cu = n;
-    }
-    const long lds_cu = device_lds_per_cu();
     const int C = wt.cols / kChunk;
     const long RS = kBlock / C;
+    const long cus = device_cu_count();
     const long fixed = static_cast<long>(wt.cols) + static_cast<long>(Act::extra_lds(wt.cols)) + 48;
+    const long max_rows = cus * (kStreamMaxRows / RS - 1) * RS;  // <= kStreamMaxRows sums per block
     for (long r0 = 0; r0 < wt.rows;) {
-        const long left = wt.rows - r0;
-        long per_cu = regs_per_cu, grid = 1, nfull = 0, n = left;
-        size_t lds = 0;
-        for (;;) {
-            const long resident = per_cu * device_cu_count();
-            // at most kStreamMaxRows rows of sums per block
-            const long max_rows = resident * (kStreamMaxRows / RS - 1) * RS;
-            n = left < max_rows ? left : max_rows;
-            nfull = n / RS;
-            grid = nfull < resident ? nfull : resident;
-            if (grid < 1) grid = 1;
-            const long steps_per_block = (nfull + grid - 1) / grid;
-            lds = static_cast<size_t>(fixed + ((steps_per_block + 2) * RS + 8) * 4);
-            if (per_cu == 1 || per_cu * static_cast<long>(lds) <= lds_cu) break;
-            --per_cu;
-        }
+        const long n = wt.rows - r0 < max_rows ? wt.rows - r0 : max_rows;
+        const long nfull = n / RS;
+        long grid = nfull < cus ? nfull : cus;
+        if (grid < 1) grid = 1;
+        const long steps_per_block = (nfull + grid - 1) / grid;
+        const size_t lds = static_cast<size_t>(fixed + ((steps_per_block + 2) * RS + 8) * 4);
         Weights part{wt.meta + r0 * wt.ms, wt.values + r0 * wt.vs, static_cast<int>(n), wt.cols,
                      wt.ms, wt.vs};
         hipLaunchKernelGGL((gemv_stream_kernel<Act, Sink>), dim3(static_cast<int>(grid)),

@@ -47,6 +47,7 @@ constexpr int kAttnThreads = 256;
 constexpr int kAttnMaxGroup = 8;  // q heads per kv head
 constexpr int kLmBlock = 256;
 constexpr int kLmMaxH = 8192;
+constexpr int kLmMaxRows = 2048;  // LM-head rows per block (grid >= vocab / 2048)
 
 struct EngineState {
     int pos;         // position of the token the next step processes
@@ -778,24 +779,54 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
 // Final RMSNorm (unit order over kLmBlock threads), then
 // logits[r] = sum_c W[r][c] * xn[c] in fp32: lane l of the row's wave takes
 // the 8-element chunks l, l+64, ... (fma in element order), then the
-// wave tree.  Each wave keeps RR rows (NC 16-byte chunks per lane each) in
-// flight.  Argmax = lowest index among the maxima (std::max_element,
+// wave tree.  Block b streams the contiguous rows [b*V/G, (b+1)*V/G); its
+// wave w takes rows b0 + w, b0 + w + 4, ...  A lane keeps its NC chunks of
+// the normalised x in registers as bf16 pairs (the values are bf16-rounded,
+// so the packing is exact), and NB row buffers rotate: NB - 1 rows are in
+// flight while one is reduced (the first rows load before the norm).  The
+// loop has no global store (logits are staged in LDS) and no predicated
+// load (kFull: H % 512 == 0), so its wait counts cover one row only.
+// Argmax = lowest index among the maxima (std::max_element,
 // src/main.cpp:194-200).  The last block to finish reduces the per-block
 // maxima and advances the decode state.  Reference half_gemv_kernel
 // (inference_kernels.cu:488-531) with fp16 -> bf16 weights.
-template <int NC, int RR>
+template <int NC, int NB, bool kFull>
 __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
     const float* __restrict__ wn, float eps, float* __restrict__ logits,
     float* __restrict__ part_v, int* __restrict__ part_i, EngineState* __restrict__ st,
     int* __restrict__ tokens, int V, int H) {
+    static_assert(NB == 2 || NB == 3, "two or three row buffers");
+    constexpr int kWaves = kLmBlock / kWave;
     __shared__ __align__(16) float xs[kLmMaxH];
-    __shared__ float red[kLmBlock / kWave];
-    __shared__ float wv[kLmBlock / kWave];
-    __shared__ int wi[kLmBlock / kWave];
+    __shared__ float lg[kLmMaxRows];  // the block's logits, stored after the loop
+    __shared__ float red[kWaves];
+    __shared__ float wv[kWaves];
+    __shared__ int wi[kWaves];
     __shared__ int last;
     if (st->done) return;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int nch = H >> 3;
+    const long b0 = static_cast<long>(V) * blockIdx.x / gridDim.x;
+    const long b1 = static_cast<long>(V) * (blockIdx.x + 1) / gridDim.x;
+    const long n = (b1 - b0 - wave + kWaves - 1) / kWaves;  // rows of this wave (may be <= 0)
+    const long i_last = n > 0 ? n - 1 : 0;
+    auto row_of = [&](long i) { return b0 + wave + (i <= i_last ? i : i_last) * kWaves; };
+    auto load_row = [&](long i, uint4 (&w)[NC]) {
+        const long r = row_of(i);
+        const uint4* wr = reinterpret_cast<const uint4*>(W + (r < V ? r : V - 1) * H);
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+            const int c = lane + k * kWave;
+            if (kFull)  // every chunk exists: unconditional loads
+                w[k] = wr[c];
+            else
+                w[k] = c < nch ? wr[c] : make_uint4(0, 0, 0, 0);
+        }
+    };
+    uint4 wa[NC], wb[NC], wc[NC];
+    load_row(0, wa);
+    if (NB == 3) load_row(1, wb);
 
     HeldWeights<kLmBlock> hw;
     HeldUnits<kLmBlock> hx;
@@ -805,49 +836,79 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     const float inv = inv_rms(block_sum<kLmBlock>(ss, red), H, eps);
     hw.apply(xs, wn, inv, H >> 3, tid);
     __syncthreads();
-
-    const int nch = H >> 3;
-    const long waves = static_cast<long>(gridDim.x) * (kLmBlock / kWave);
-    float best = -INFINITY;
-    int best_i = 0x7FFFFFFF;
-    for (long r0 = static_cast<long>(blockIdx.x) * (kLmBlock / kWave) + wave; r0 < V;
-         r0 += RR * waves) {
-        uint4 w[RR][NC];
+    uint4 xp[NC];
 #pragma unroll
-        for (int q = 0; q < RR; ++q) {
-            const long r = r0 + q * waves;
-            const uint4* wr = reinterpret_cast<const uint4*>(W + r * H);
+    for (int k = 0; k < NC; ++k) {
+        const int c = lane + k * kWave;
+        if (c < nch) {
+            float f[8];
+            load_f8(xs + 8 * c, f);
+            uint32_t u[4];
 #pragma unroll
-            for (int k = 0; k < NC; ++k) {
-                const int c = lane + k * kWave;
-                w[q][k] = (r < V && c < nch) ? wr[c] : make_uint4(0, 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < RR; ++q) {
-            const long r = r0 + q * waves;
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < NC; ++k) {
-                const int c = lane + k * kWave;
-                if (c < nch) {
-                    float f[8], xv[8];
-                    unpack_bf16x8(w[q][k], f);
-                    load_f8(xs + 8 * c, xv);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(f[e], xv[e], acc);
-                }
-            }
-            acc = wave_sum_tree(acc);
-            if (r < V) {
-                if (lane == 0) logits[r] = acc;
-                if (acc > best) {  // rows ascend within a wave: strict > keeps the first maximum
-                    best = acc;
-                    best_i = static_cast<int>(r);
-                }
-            }
+            for (int q = 0; q < 4; ++q)
+                u[q] = (__builtin_bit_cast(uint32_t, f[2 * q]) >> 16) |
+                       (__builtin_bit_cast(uint32_t, f[2 * q + 1]) & 0xFFFF0000u);
+            xp[k] = make_uint4(u[0], u[1], u[2], u[3]);
+        } else {
+            xp[k] = make_uint4(0, 0, 0, 0);
         }
     }
+
+    float best = -INFINITY;
+    int best_i = 0x7FFFFFFF;
+    auto reduce_row = [&](long i, const uint4 (&w)[NC]) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+            const int c = lane + k * kWave;
+            if (kFull || c < nch) {
+                float f[8], xv[8];
+                unpack_bf16x8(w[k], f);
+                unpack_bf16x8(xp[k], xv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(f[e], xv[e], acc);
+            }
+        }
+        acc = wave_sum_tree(acc);
+        const long r = row_of(i);
+        // LDS, not global: a global store in the loop would make the
+        // compiler drain the loads in flight
+        if (lane == 0) lg[r - b0] = acc;
+        if (acc > best) {  // rows ascend within a wave: strict > keeps the first maximum
+            best = acc;
+            best_i = static_cast<int>(r);
+        }
+    };
+    // Counted loops with their only exit at the latch (exact wait counts, as
+    // in the streaming GEMV); loads past the wave's last row re-read it.
+    long i = 0;
+    if (NB == 3) {
+        for (long p = 0; p < n / 3; ++p, i += 3) {
+            load_row(i + 2, wc);
+            __builtin_amdgcn_sched_barrier(0);
+            reduce_row(i, wa);
+            load_row(i + 3, wa);
+            __builtin_amdgcn_sched_barrier(0);
+            reduce_row(i + 1, wb);
+            load_row(i + 4, wb);
+            __builtin_amdgcn_sched_barrier(0);
+            reduce_row(i + 2, wc);
+        }
+        if (n > 0 && n % 3 > 0) reduce_row(i, wa);
+        if (n > 0 && n % 3 > 1) reduce_row(i + 1, wb);
+    } else {
+        for (long p = 0; p < n / 2; ++p, i += 2) {
+            load_row(i + 1, wb);
+            __builtin_amdgcn_sched_barrier(0);
+            reduce_row(i, wa);
+            load_row(i + 2, wa);
+            __builtin_amdgcn_sched_barrier(0);
+            reduce_row(i + 1, wb);
+        }
+        if (n > 0 && (n & 1)) reduce_row(i, wa);
+    }
+    __syncthreads();
+    for (long j = tid; j < b1 - b0; j += kLmBlock) logits[b0 + j] = lg[j];
     if (lane == 0) {
         wv[wave] = best;
         wi[wave] = best_i;
@@ -916,28 +977,33 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
 typedef void (*LmKernel)(const uint16_t*, const uint16_t*, const float*, float, float*, float*,
                          int*, EngineState*, int*, int, int);
 
-// Instantiation for H: NC = ceil(H / 512) chunks per lane (H <= 8192).
-LmKernel lm_head_for(int H, int* rows_in_flight) {
-    const int nc = (H / 8 + kWave - 1) / kWave;
-    *rows_in_flight = nc <= 4 ? 4 : (nc <= 8 ? 2 : 1);
+// Instantiation for H: NC = ceil(H / 512) chunks per lane (H <= 8192), two
+// row buffers; kFull when H % 512 == 0.
+template <bool kFull>
+LmKernel lm_head_for_nc(int nc) {
     switch (nc) {
-        case 1: return lm_head_kernel<1, 4>;
-        case 2: return lm_head_kernel<2, 4>;
-        case 3: return lm_head_kernel<3, 4>;
-        case 4: return lm_head_kernel<4, 4>;
-        case 5: return lm_head_kernel<5, 2>;
-        case 6: return lm_head_kernel<6, 2>;
-        case 7: return lm_head_kernel<7, 2>;
-        case 8: return lm_head_kernel<8, 2>;
-        case 9: return lm_head_kernel<9, 1>;
-        case 10: return lm_head_kernel<10, 1>;
-        case 11: return lm_head_kernel<11, 1>;
-        case 12: return lm_head_kernel<12, 1>;
-        case 13: return lm_head_kernel<13, 1>;
-        case 14: return lm_head_kernel<14, 1>;
-        case 15: return lm_head_kernel<15, 1>;
-        default: return lm_head_kernel<16, 1>;
+        case 1: return lm_head_kernel<1, 2, kFull>;
+        case 2: return lm_head_kernel<2, 2, kFull>;
+        case 3: return lm_head_kernel<3, 2, kFull>;
+        case 4: return lm_head_kernel<4, 2, kFull>;
+        case 5: return lm_head_kernel<5, 2, kFull>;
+        case 6: return lm_head_kernel<6, 2, kFull>;
+        case 7: return lm_head_kernel<7, 2, kFull>;
+        case 8: return lm_head_kernel<8, 2, kFull>;
+        case 9: return lm_head_kernel<9, 2, kFull>;
+        case 10: return lm_head_kernel<10, 2, kFull>;
+        case 11: return lm_head_kernel<11, 2, kFull>;
+        case 12: return lm_head_kernel<12, 2, kFull>;
+        case 13: return lm_head_kernel<13, 2, kFull>;
+        case 14: return lm_head_kernel<14, 2, kFull>;
+        case 15: return lm_head_kernel<15, 2, kFull>;
+        default: return lm_head_kernel<16, 2, kFull>;
     }
+}
+
+LmKernel lm_head_for(int H) {
+    const int nc = (H / 8 + kWave - 1) / kWave;
+    return (H % 512 == 0) ? lm_head_for_nc<true>(nc) : lm_head_for_nc<false>(nc);
 }
 
 // ---- random-init weights (model generation on the device) ------------------------
@@ -1236,16 +1302,16 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
     e->final_norm = final_norm;
     e->max_seq = max_seq;
     e->S = (max_seq + kAttnSplit - 1) / kAttnSplit;
-    int rr = 1;
-    e->lm_kernel = lm_head_for(H, &rr);
-    int resident = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, e->lm_kernel, kLmBlock, 0) !=
-            hipSuccess ||
-        resident <= 0)
-        resident = 1;
+    e->lm_kernel = lm_head_for(H);
+    // One block per CU: every block streams a contiguous range of rows.  On
+    // MI355X a cold 657 MB pass ran fastest with one 4-wave block per CU
+    // (~123 us) and slower with 2 or 3 (~133 / ~144 us).  At least V / 2048
+    // blocks (the logits of a block are staged in LDS).
     const long lm_need = (static_cast<long>(V) + kLmBlock / kWave - 1) / (kLmBlock / kWave);
-    const long lm_res = static_cast<long>(resident) * device_cu_count();
-    e->lm_grid = static_cast<int>(lm_need < lm_res ? lm_need : lm_res);
+    const long lm_min = (static_cast<long>(V) + kLmMaxRows - 1) / kLmMaxRows;
+    long lm_grid = device_cu_count();
+    if (lm_grid > lm_need) lm_grid = lm_need;
+    e->lm_grid = static_cast<int>(lm_grid > lm_min ? lm_grid : lm_min);
 
     auto& own = e->owned;
     const size_t kv = static_cast<size_t>(nkv) * max_seq * hd;
