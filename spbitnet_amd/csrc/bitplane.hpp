@@ -683,11 +683,18 @@ void launch_bitplane(const W& wt, Act act, Sink sink, hipStream_t stream, int to
     const long steps_max = 8;
     const size_t plane_lds = static_cast<size_t>(wt.cols) + Act::extra_lds(wt.cols);
     const size_t lds_max = plane_lds + 2 * RS * steps_max * 4 + 12;
-    long resident =
-        static_cast<long>(bitplane_blocks_per_cu<W, Act, Sink>(lds_max)) * device_cu_count();
-    resident = (resident + tokens - 1) / tokens;  // tokens share the resident capacity
-    // Enough tiles for every resident block; longer tiles once the matrix
-    // is several times the resident capacity.
+    // One token (the GEMV and the decode engine): at most one block per CU.
+    // With more tiles than CUs, the CUs that run two blocks finish last and
+    // set the kernel time (measured: 277 blocks on 256 CUs took ~2x the
+    // median block), so longer tiles on fewer blocks win.  Batched use:
+    // the resident capacity, shared by the tokens.
+    long resident = device_cu_count();
+    if (tokens > 1) {
+        resident *= bitplane_blocks_per_cu<W, Act, Sink>(lds_max);
+        resident = (resident + tokens - 1) / tokens;
+    }
+    // Enough tiles for every block; longer tiles once the matrix is several
+    // times that.
     long steps = (static_cast<long>(wt.rows) + RS * resident - 1) / (RS * resident);
     steps = steps < 1 ? 1 : (steps > steps_max ? steps_max : steps);
     const long tile_rows = RS * steps;
