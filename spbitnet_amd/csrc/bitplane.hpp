@@ -263,6 +263,7 @@ struct Int32Sink {
     long token_stride = 0;  // batched use: token t writes y + t * token_stride
     __device__ void offset(long t) { y += t * token_stride; }
     __device__ void prepare() {}
+    __device__ void prefetch(long, int, int) {}
     template <class A>
     __device__ void bind(const A&) {}
     __device__ void store(long r, int acc) const { y[r] = acc; }
@@ -276,6 +277,7 @@ struct DequantSink {
     float dq;
     __device__ void offset(long) {}
     __device__ void prepare() { dq = dequant_scale(gamma, *d_absmax); }
+    __device__ void prefetch(long, int, int) {}
     template <class A>
     __device__ void bind(const A&) {}
     __device__ void store(long r, int acc) const {
@@ -362,8 +364,22 @@ __device__ __forceinline__ void load_x(const uint32_t* src, uint32_t (&X)[4][8])
 //   block), act.prepare(), act.build(planes, cols, tid, scratch, regs)
 //   -- scratch: the
 //   Act::extra_lds(cols) bytes of LDS after the row sums;
-//   sink.prepare() before the prologue, sink.bind(act) after it (a sink may
-//   take a scale the prologue computed), sink.store(row, acc).
+//   sink.prepare() before the prologue, sink.prefetch(row0, n, tid) with the
+//   block's first tile (loads the epilogue will need), sink.bind(act) after
+//   the prologue (a sink may take a scale the prologue computed), and
+//   sink.store(row, acc) per row -- or, for a sink with SinkPairs<S>::value,
+//   sink.store_pair(row, acc_row, acc_row_plus_1) per even row (tiles then
+//   hold an even number of rows).
+template <class S>
+struct SinkPairs {
+    static constexpr bool value = false;
+};
+
+template <class Sink>
+__host__ __device__ constexpr int rows_per_step(int C) {
+    return SinkPairs<Sink>::value ? (kBlock / C) & ~1 : kBlock / C;
+}
+
 template <class W, class Act, class Sink>
 __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Sink sink,
                                                                int tile_steps, long ntiles) {
@@ -371,7 +387,7 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Si
     if (act.skip()) return;
     const int nwords = wt.cols >> 5;
     const int C = wt.cols / kChunk;
-    const int RS = kBlock / C;
+    const int RS = rows_per_step<Sink>(C);
     const int tile_rows = RS * tile_steps;
     uint32_t* planes = smem;  // word [w * 8 + b]
     int* acc0 = reinterpret_cast<int*>(smem + 8 * nwords);
@@ -396,6 +412,7 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Si
     ChunkLoad cur = wt.load(row, c, active);
     act.prepare();
     sink.prepare();
+    sink.prefetch(tile * tile_rows, tile_rows, tid);
     uint32_t X[4][8];
     // prologue scratch after the row sums, 16-byte aligned
     act.build(planes, wt.cols, tid,
@@ -421,9 +438,17 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Si
         if (step == tile_steps - 1) {
             __syncthreads();  // uniform: (tile, step) are the same in every thread
             const long row0 = tile * tile_rows;
-            for (int j = tid; j < tile_rows; j += kBlock) {
-                if (row0 + j < wt.rows) sink.store(row0 + j, acc[j]);
-                acc[j] = 0;
+            if constexpr (SinkPairs<Sink>::value) {
+                for (int j = 2 * tid; j < tile_rows; j += 2 * kBlock) {
+                    if (row0 + j < wt.rows) sink.store_pair(row0 + j, acc[j], acc[j + 1]);
+                    acc[j] = 0;
+                    acc[j + 1] = 0;
+                }
+            } else {
+                for (int j = tid; j < tile_rows; j += kBlock) {
+                    if (row0 + j < wt.rows) sink.store(row0 + j, acc[j]);
+                    acc[j] = 0;
+                }
             }
             parity ^= 1;
         }
@@ -679,7 +704,7 @@ int bitplane_blocks_per_cu(size_t lds) {
 template <class W, class Act, class Sink>
 void launch_bitplane(const W& wt, Act act, Sink sink, hipStream_t stream, int tokens = 1) {
     const int C = wt.cols / kChunk;
-    const long RS = kBlock / C;
+    const long RS = rows_per_step<Sink>(C);
     const long steps_max = 8;
     const size_t plane_lds = static_cast<size_t>(wt.cols) + Act::extra_lds(wt.cols);
     const size_t lds_max = plane_lds + 2 * RS * steps_max * 4 + 12;

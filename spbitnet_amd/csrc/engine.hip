@@ -33,6 +33,7 @@
 // Every floating-point reduction has a fixed order (listed at each helper), so
 // the CPU oracle in oracle/ reproduces the logits bit for bit.
 #include <cmath>
+#include <cstddef>
 #include <new>
 #include <vector>
 
@@ -59,6 +60,25 @@ struct EngineState {
     unsigned ticket;  // LM-head blocks finished in the current step
     int generated;
 };
+static_assert(offsetof(EngineState, pos) == 0 && offsetof(EngineState, prompt_len) == 4 &&
+                  offsetof(EngineState, limit) == 8 && offsetof(EngineState, done) == 12,
+              "state_head reads the first four fields as one 16-byte load");
+
+// The decode state's {pos, prompt_len, limit, done} through one vector
+// (buffer) load.  A plain load of a uniform field compiles to a scalar load,
+// whose wait counter is shared with LDS: the first LDS wait of a prologue
+// would then also wait for it.  A vector load completes in order with the
+// kernel's other vector loads and is waited for only where it is used.
+struct StateHead {
+    int pos, prompt_len, limit, done;
+};
+__device__ __forceinline__ StateHead state_head(const EngineState* st) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<EngineState*>(st), static_cast<short>(0), 16, kBufferFlags);
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, 0, 0, 0);
+    return StateHead{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z),
+                     static_cast<int>(v.w)};
+}
 
 // ---- fixed-order arithmetic shared with the oracle ------------------------------
 
@@ -392,11 +412,13 @@ struct AttnCombine {
     const float* pl;    // [nh][S]
     const float* pacc;  // [nh][S][hd]
     int hd, S, chunk;
-    struct Regs {};
-    __device__ void issue(int, const EngineState*, Regs&) const {}
-    __device__ float fill(float* vec, float*, int n, int tid, float*, const EngineState* st,
-                          Regs&) const {
-        int ns = st->pos / chunk + 1;  // splits holding positions 0..pos
+    struct Regs {
+        int pos;
+    };
+    __device__ void issue(int, const EngineState* st, Regs& r) const { r.pos = state_head(st).pos; }
+    __device__ float fill(float* vec, float*, int n, int tid, float*, const EngineState*,
+                          Regs& r) const {
+        int ns = r.pos / chunk + 1;  // splits holding positions 0..pos
         ns = ns < S ? ns : S;
         const int units = n >> 3;
         float mx = 0.0f;
@@ -617,6 +639,7 @@ struct SegBf16Sink {
     float dq0, dq1, dq2;
     __device__ void offset(long) {}
     __device__ void prepare() {}
+    __device__ void prefetch(long, int, int) {}
     template <class A>
     __device__ void bind(const A& a) {
         const float m = a.absmax();
@@ -632,114 +655,201 @@ struct SegBf16Sink {
 
 // down projection: x_out[r] = bf16(bf16(acc * dq) + res[r])
 // (inference.cu:256-262; residual_add_kernel, inference_kernels.cu:471-479).
+// The residual row a thread stores in the block's first tile is loaded at
+// kernel start (prefetch), off the epilogue's critical path.
 struct ResidualSink {
     uint16_t* x_out;
     const uint16_t* res;
     float gamma;
     float dq;
+    long pre_row;
+    uint16_t pre_res;
     __device__ void offset(long) {}
     __device__ void prepare() {}
+    __device__ void prefetch(long row0, int n, int tid) {
+        pre_row = tid < n ? row0 + tid : -1;
+        pre_res = tid < n ? res[row0 + tid] : 0;
+    }
     template <class A>
     __device__ void bind(const A& a) {
         dq = dequant_scale(gamma, a.absmax());
     }
     __device__ void store(long r, int acc) const {
         const float d = bf16r(static_cast<float>(acc) * dq);
-        x_out[r] = BF16::from_float(d + BF16::to_float(res[r]));
+        const uint16_t rv = r == pre_row ? static_cast<uint16_t>(opaque(static_cast<uint32_t>(pre_res)))
+                                         : res[r];
+        x_out[r] = BF16::from_float(d + BF16::to_float(rv));
     }
+};
+
+// q/k/v outputs of the stacked projection (q rows [0, end0), k rows
+// [end0, end1), v rows [end1, ...)): each row dequantised with its own
+// projection's gamma and rounded to bf16, out = bf16(acc * ((gamma*absmax)/127));
+// then every (2i, 2i+1) pair of a q or k head rotated by RoPE at the decode
+// position (rope_kernel, inference_kernels.cu:185-206),
+//   (x0, x1) -> (bf16(x0*cos - x1*sin), bf16(x0*sin + x1*cos)),
+// and k and v written to this layer's KV cache at pos (scatter_kv,
+// inference_kernels.cu:215-227; the cache is [kv head][max_seq][head_dim])
+// unless the decode state is done.  The RoPE row of the decode position is
+// cur_rope (written by the previous step's LM head, or by the host when the
+// state is set), so no load waits for pos until the cache writes.
+struct QkvRopeSink {
+    uint16_t* out;
+    uint16_t* kc;
+    uint16_t* vc;
+    const float2* cur_rope;  // [hd/2] (cos, sin) at the decode position
+    const EngineState* st;
+    float g0, g1, g2;
+    int end0, end1;
+    int hd, max_seq;
+    int hd_log2;  // hd is 64 or 128
+    float dq0, dq1, dq2;
+    int pos, live;
+    long pre_row;
+    float2 pre_cs;
+    __device__ void offset(long) {}
+    __device__ void prepare() {}
+    __device__ int rope_pair(long r) const {  // pair index of q/k row r within its head
+        const int rr = static_cast<int>(r < end0 ? r : r - end0);
+        return (rr & (hd - 1)) >> 1;
+    }
+    // element offset of row r of a k or v segment (r relative to the segment)
+    // in the cache [kv head][max_seq][hd] at pos
+    __device__ long cache_at(int r) const {
+        return ((static_cast<long>(r >> hd_log2) * max_seq + pos) << hd_log2) + (r & (hd - 1));
+    }
+    __device__ void prefetch(long row0, int n, int tid) {
+        const StateHead h = state_head(st);  // needed only by the cache writes
+        pos = h.pos;
+        live = !h.done;
+        pre_row = 2 * tid < n ? row0 + 2 * tid : -1;
+        pre_cs = make_float2(0.0f, 0.0f);
+        if (pre_row >= 0 && pre_row < end1) pre_cs = cur_rope[rope_pair(pre_row)];
+    }
+    template <class A>
+    __device__ void bind(const A& a) {
+        const float m = a.absmax();
+        dq0 = dequant_scale(g0, m);
+        dq1 = dequant_scale(g1, m);
+        dq2 = dequant_scale(g2, m);
+    }
+    __device__ void store_pair(long r, int a0, int a1) const {
+        const bool is_q = r < end0, is_v = r >= end1;
+        const float dq = is_q ? opaque(dq0) : (is_v ? opaque(dq2) : opaque(dq1));
+        const float x0 = bf16r(static_cast<float>(a0) * dq);
+        const float x1 = bf16r(static_cast<float>(a1) * dq);
+        // a pair is one 32-bit store (r is even; the buffers are 4-byte aligned)
+        if (is_v) {
+            const uint32_t y = static_cast<uint32_t>(BF16::from_float(x0)) |
+                               (static_cast<uint32_t>(BF16::from_float(x1)) << 16);
+            *reinterpret_cast<uint32_t*>(out + r) = y;
+            if (live)
+                *reinterpret_cast<uint32_t*>(vc + cache_at(static_cast<int>(r - end1))) = y;
+            return;
+        }
+        // opaque: a select between a member and a load would otherwise become a
+        // load from a selected address, which moves the sink to scratch memory
+        float2 cs;
+        if (r == pre_row)
+            cs = make_float2(opaque(pre_cs.x), opaque(pre_cs.y));
+        else
+            cs = cur_rope[rope_pair(r)];
+        const uint32_t y = static_cast<uint32_t>(BF16::from_float(x0 * cs.x - x1 * cs.y)) |
+                           (static_cast<uint32_t>(BF16::from_float(x0 * cs.y + x1 * cs.x)) << 16);
+        *reinterpret_cast<uint32_t*>(out + r) = y;
+        if (!is_q && live)
+            *reinterpret_cast<uint32_t*>(kc + cache_at(static_cast<int>(r - end0))) = y;
+    }
+};
+
+template <>
+struct SinkPairs<QkvRopeSink> {
+    static constexpr bool value = true;
 };
 
 // ---- attention -----------------------------------------------------------------------
 
-// One block per (64-position split s, kv head): RoPE of the group's q heads
-// and (in the split holding pos) of k, KV-cache write of k and v at pos,
-// scores, the split's softmax numerator and unnormalised weighted sum of V.
+// One block per (64-position split s, kv head): scores of the group's q
+// heads against the split's cached keys, the split's softmax numerator and
+// unnormalised weighted sum of V.  q arrives rotated and the cache already
+// holds k and v at pos (both written by the qkv projection's epilogue), so
+// every load is issued at kernel start: q of the group and the split's V rows
+// into LDS, each lane's K row (lane = position) into registers; rows past pos
+// are loaded too (the cache is allocated to max_seq) and masked.
 //   score_j = (sum over d ascending of fma(q[d], k_j[d], .)) * scale
 //   per head: m = max_j score_j, e_j = exp(score_j - m),
 //   l = tree sum of e over the 64 lanes (lane = position in the split),
 //   acc[d] = sum_j e_j v_j[d] (j ascending, fma).
-// rope: [max_seq][hd/2] (cos, sin) of angle pos * theta^(-2i/hd).
-// Reference: rope_kernel, scatter_kv, attention_scores, softmax,
-// attention_output (inference_kernels.cu:185-371), GQA kv = h * nkv / nh.
+// Reference: attention_scores, softmax, attention_output
+// (inference_kernels.cu:241-371), GQA kv = h * nkv / nh.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
-    const uint16_t* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-    const float2* __restrict__ rope, float* __restrict__ pm, float* __restrict__ pl,
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, float* __restrict__ pm, float* __restrict__ pl,
     float* __restrict__ pacc, const EngineState* __restrict__ st, int nh, int nkv, int max_seq,
     int S, float scale) {
-    constexpr int kHalf = HD / 2, kU = HD / 8;
-    __shared__ float qs[kAttnMaxGroup][HD];
-    __shared__ float kn[HD];
+    constexpr int kU = HD / 8;
+    __shared__ __align__(16) float qs[kAttnMaxGroup][HD];
     __shared__ __align__(16) float vs[kAttnSplit][HD];
     __shared__ float sc[kAttnMaxGroup][kAttnSplit];
     __shared__ float hmax[kAttnMaxGroup], hsum[kAttnMaxGroup];
-    if (st->done) return;
-    const int pos = st->pos;
     const int s = blockIdx.x, kvh = blockIdx.y;
     const int j0 = s * kAttnSplit;
-    if (j0 > pos) return;
-    const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
-    const bool has_pos = j0 + jn - 1 == pos;
     const int G = nh / nkv;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const float2* rp = rope + static_cast<long>(pos) * kHalf;
-    const uint16_t* vh = qkv + (nh + nkv) * HD + kvh * HD;
     const long cache0 = static_cast<long>(kvh) * max_seq * HD;
-
-    for (int idx = tid; idx < G * kHalf; idx += kAttnThreads) {
-        const int g = idx / kHalf, i = idx - g * kHalf;
-        const uint16_t* qh = qkv + (kvh * G + g) * HD;
-        const float x0 = BF16::to_float(qh[2 * i]), x1 = BF16::to_float(qh[2 * i + 1]);
-        const float2 cs = rp[i];
-        qs[g][2 * i] = bf16r(x0 * cs.x - x1 * cs.y);
-        qs[g][2 * i + 1] = bf16r(x0 * cs.y + x1 * cs.x);
+    const int jmax = max_seq - 1;
+    // speculative loads (positions clamped to the cache)
+    const int jl = j0 + lane <= jmax ? j0 + lane : jmax;
+    uint4 kraw[kU];
+    {
+        const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(jl) * HD);
+#pragma unroll
+        for (int c = 0; c < kU; ++c) kraw[c] = kr[c];
     }
-    if (has_pos) {
-        const uint16_t* kh = qkv + nh * HD + kvh * HD;
-        const long at = cache0 + static_cast<long>(pos) * HD;
-        for (int i = tid; i < kHalf; i += kAttnThreads) {
-            const float x0 = BF16::to_float(kh[2 * i]), x1 = BF16::to_float(kh[2 * i + 1]);
-            const float2 cs = rp[i];
-            const uint16_t k0 = BF16::from_float(x0 * cs.x - x1 * cs.y);
-            const uint16_t k1 = BF16::from_float(x0 * cs.y + x1 * cs.x);
-            kn[2 * i] = BF16::to_float(k0);
-            kn[2 * i + 1] = BF16::to_float(k1);
-            kc[at + 2 * i] = k0;
-            kc[at + 2 * i + 1] = k1;
-        }
-        for (int d = tid; d < HD; d += kAttnThreads) vc[at + d] = vh[d];
-    }
-    // V rows of the split -> LDS (the row at pos straight from this step's v)
-    for (int idx = tid; idx < jn * kU; idx += kAttnThreads) {
+    // V rows of the split: kVPer 16-byte units per thread, all loads issued
+    // before the first LDS store (one memory latency, not kVPer)
+    constexpr int kVPer = kAttnSplit * kU / kAttnThreads;
+    static_assert(kVPer * kAttnThreads == kAttnSplit * kU, "V units per thread");
+    uint4 vraw[kVPer];
+#pragma unroll
+    for (int t = 0; t < kVPer; ++t) {
+        const int idx = tid + t * kAttnThreads;
         const int jj = idx / kU, c = idx - jj * kU;
-        const int j = j0 + jj;
-        const uint4 r = j == pos ? reinterpret_cast<const uint4*>(vh)[c]
-                                 : reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
+        const int j = j0 + jj <= jmax ? j0 + jj : jmax;
+        vraw[t] = reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
+    }
+    uint4 qraw = make_uint4(0, 0, 0, 0);
+    const bool has_q = tid < G * kU;
+    if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + (kvh * G) * HD)[tid];
+    const StateHead sh = state_head(st);
+    const int done = sh.done, pos = sh.pos;
+#pragma unroll
+    for (int t = 0; t < kVPer; ++t) {
+        const int idx = tid + t * kAttnThreads;
+        const int jj = idx / kU, c = idx - jj * kU;
         float f[8];
-        unpack_bf16x8(r, f);
+        unpack_bf16x8(vraw[t], f);
         store_f8(&vs[jj][8 * c], f);
     }
+    if (has_q) {
+        float f[8];
+        unpack_bf16x8(qraw, f);
+        store_f8(&qs[tid / kU][8 * (tid % kU)], f);
+    }
+    if (done || j0 > pos) return;  // uniform
+    const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
     __syncthreads();
 
     // scores: lane = position, wave w takes heads w, w + 4
     if (lane < jn) {
-        const int j = j0 + lane;
         float k[HD];
-        if (j == pos) {
 #pragma unroll
-            for (int d = 0; d < HD; ++d) k[d] = kn[d];
-        } else {
-            const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD);
-            uint4 raw[kU];
+        for (int c = 0; c < kU; ++c) {
+            float f[8];
+            unpack_bf16x8(kraw[c], f);
 #pragma unroll
-            for (int c = 0; c < kU; ++c) raw[c] = kr[c];
-#pragma unroll
-            for (int c = 0; c < kU; ++c) {
-                float f[8];
-                unpack_bf16x8(raw[c], f);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) k[8 * c + e] = f[e];
-            }
+            for (int e = 0; e < 8; ++e) k[8 * c + e] = f[e];
         }
         for (int g = wave; g < G; g += kAttnThreads / kWave) {
             float acc = 0.0f;
@@ -795,7 +905,8 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
     const float* __restrict__ wn, float eps, float* __restrict__ logits,
     float* __restrict__ part_v, int* __restrict__ part_i, EngineState* __restrict__ st,
-    int* __restrict__ tokens, int V, int H) {
+    int* __restrict__ tokens, int V, int H, const float2* __restrict__ rope,
+    float2* __restrict__ cur_rope, int half_hd, int max_seq) {
     static_assert(NB == 2 || NB == 3, "two or three row buffers");
     constexpr int kWaves = kLmBlock / kWave;
     __shared__ __align__(16) float xs[kLmMaxH];
@@ -804,7 +915,6 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     __shared__ float wv[kWaves];
     __shared__ int wi[kWaves];
     __shared__ int last;
-    if (st->done) return;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int nch = H >> 3;
     const long b0 = static_cast<long>(V) * blockIdx.x / gridDim.x;
@@ -827,6 +937,7 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     uint4 wa[NC], wb[NC], wc[NC];
     load_row(0, wa);
     if (NB == 3) load_row(1, wb);
+    if (st->done) return;  // after the first row loads (they are in bounds either way)
 
     HeldWeights<kLmBlock> hw;
     HeldUnits<kLmBlock> hx;
@@ -931,6 +1042,7 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     __syncthreads();
     if (!last) return;
     __threadfence();
+    const int pos_old = st->pos;  // read before thread 0 advances it (barrier below)
     float b = -INFINITY;
     int bi = 0x7FFFFFFF;
     for (int k = tid; k < static_cast<int>(gridDim.x); k += kLmBlock) {
@@ -972,10 +1084,15 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
         if (nxt >= st->limit) st->done = 1;
         st->ticket = 0u;
     }
+    // RoPE row of the next position for the next step's q/k projection
+    {
+        const int p = pos_old + 1 < max_seq ? pos_old + 1 : max_seq - 1;
+        for (int i = tid; i < half_hd; i += kLmBlock) cur_rope[i] = rope[static_cast<long>(p) * half_hd + i];
+    }
 }
 
 typedef void (*LmKernel)(const uint16_t*, const uint16_t*, const float*, float, float*, float*,
-                         int*, EngineState*, int*, int, int);
+                         int*, EngineState*, int*, int, int, const float2*, float2*, int, int);
 
 // Instantiation for H: NC = ceil(H / 512) chunks per lane (H <= 8192), two
 // row buffers; kFull when H % 512 == 0.
@@ -1153,6 +1270,7 @@ struct spb_engine {
     int* part_i = nullptr;
     int* tokens = nullptr;
     float2* rope = nullptr;
+    float2* cur_rope = nullptr;  // RoPE row of the decode position
     EngineState* st = nullptr;
     hipStream_t stream = nullptr;      // where graphs are launched (null = legacy stream)
     hipStream_t cap_stream = nullptr;  // capture stream
@@ -1178,18 +1296,30 @@ struct spb_engine {
             {
                 InputNorm p{xa, l == 0 ? embed : nullptr, tokens, xa, L.input_layernorm, eps,
                             cfg.hidden_size};
-                SegBf16Sink sink{qkv, L.q_proj.gamma, L.k_proj.gamma, L.v_proj.gamma,
-                                 L.q_proj.rows, L.q_proj.rows + L.k_proj.rows, 0.f, 0.f, 0.f};
+                QkvRopeSink sink{};
+                sink.out = qkv;
+                sink.kc = kcache[l];
+                sink.vc = vcache[l];
+                sink.cur_rope = cur_rope;
+                sink.st = st;
+                sink.g0 = L.q_proj.gamma;
+                sink.g1 = L.k_proj.gamma;
+                sink.g2 = L.v_proj.gamma;
+                sink.end0 = L.q_proj.rows;
+                sink.end1 = L.q_proj.rows + L.k_proj.rows;
+                sink.hd = hd;
+                sink.hd_log2 = hd == 64 ? 6 : 7;
+                sink.max_seq = max_seq;
                 launch_bitplane(seg_weights(&L.q_proj, &L.k_proj, &L.v_proj),
                                 ProducerPlanes<InputNorm>{p, st, 0.f}, sink, s);
             }
             if (hd == 64)
                 hipLaunchKernelGGL(attention_kernel<64>, dim3(S, nkv), dim3(kAttnThreads), 0, s,
-                                   qkv, kcache[l], vcache[l], rope, pm, pl, pacc, st, nh, nkv,
+                                   qkv, kcache[l], vcache[l], pm, pl, pacc, st, nh, nkv,
                                    max_seq, S, scale);
             else
                 hipLaunchKernelGGL(attention_kernel<128>, dim3(S, nkv), dim3(kAttnThreads), 0, s,
-                                   qkv, kcache[l], vcache[l], rope, pm, pl, pacc, st, nh, nkv,
+                                   qkv, kcache[l], vcache[l], pm, pl, pacc, st, nh, nkv,
                                    max_seq, S, scale);
             {
                 AttnCombine p{pm, pl, pacc, hd, S, kAttnSplit};
@@ -1217,7 +1347,7 @@ struct spb_engine {
         }
         hipLaunchKernelGGL(lm_kernel, dim3(lm_grid), dim3(kLmBlock), 0, s, lm_head, xa,
                            final_norm, eps, logits, part_v, part_i, st, tokens,
-                           cfg.vocab_size, cfg.hidden_size);
+                           cfg.vocab_size, cfg.hidden_size, rope, cur_rope, hd / 2, max_seq);
     }
 };
 
@@ -1246,7 +1376,11 @@ int set_state(spb_engine* e, int pos, int prompt_len, int stop_eos) {
     h.ticket = 0u;
     h.generated = 0;
     // Synchronous with respect to the host: h lives on this stack frame.
+    const int half = e->cfg.head_dim / 2;
+    const int rp = pos < e->max_seq ? pos : e->max_seq - 1;
     if (hipMemcpyAsync(e->st, &h, sizeof(h), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
+        hipMemcpyAsync(e->cur_rope, e->rope + static_cast<long>(rp) * half,
+                       sizeof(float2) * half, hipMemcpyDeviceToDevice, e->stream) != hipSuccess ||
         hipStreamSynchronize(e->stream) != hipSuccess)
         return launch_status("spb_engine: state upload");
     return 0;
@@ -1332,6 +1466,7 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
          (e->part_i = dev_alloc<int>(e->lm_grid, own)) &&
          (e->tokens = dev_alloc<int>(max_seq + 1, own)) &&
          (e->rope = dev_alloc<float2>(static_cast<size_t>(max_seq) * (hd / 2), own)) &&
+         (e->cur_rope = dev_alloc<float2>(hd / 2, own)) &&
          (e->st = dev_alloc<EngineState>(1, own));
     if (!ok) {
         delete e;
