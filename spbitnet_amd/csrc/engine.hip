@@ -773,9 +773,14 @@ struct SinkPairs<QkvRopeSink> {
 // heads against the split's cached keys, the split's softmax numerator and
 // unnormalised weighted sum of V.  q arrives rotated and the cache already
 // holds k and v at pos (both written by the qkv projection's epilogue), so
-// every load is issued at kernel start: q of the group and the split's V rows
-// into LDS, each lane's K row (lane = position) into registers; rows past pos
-// are loaded too (the cache is allocated to max_seq) and masked.
+// every load is issued at kernel start; rows past pos are loaded too (the
+// cache is allocated to max_seq) and masked.
+//   * scores: thread t takes the (position, head) pairs t, t + 256, ... with
+//     position = pair / G and head = pair % G, so the G lanes of one position
+//     share one K-row load and a wave reads 64 / G rows; q of the group is in
+//     LDS (float), the K row in registers.
+//   * V rows of the split stay bf16 in LDS; a PV thread owns dims (d, d+1)
+//     of one head and reads both with one 32-bit LDS load.
 //   score_j = (sum over d ascending of fma(q[d], k_j[d], .)) * scale
 //   per head: m = max_j score_j, e_j = exp(score_j - m),
 //   l = tree sum of e over the 64 lanes (lane = position in the split),
@@ -789,8 +794,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     float* __restrict__ pacc, const EngineState* __restrict__ st, int nh, int nkv, int max_seq,
     int S, float scale) {
     constexpr int kU = HD / 8;
+    constexpr int kVRow = HD / 2 + 1;  // 32-bit words per bf16 V row in LDS (+1: no bank conflicts)
     __shared__ __align__(16) float qs[kAttnMaxGroup][HD];
-    __shared__ __align__(16) float vs[kAttnSplit][HD];
+    __shared__ uint32_t vs[kAttnSplit][kVRow];
     __shared__ float sc[kAttnMaxGroup][kAttnSplit];
     __shared__ float hmax[kAttnMaxGroup], hsum[kAttnMaxGroup];
     const int s = blockIdx.x, kvh = blockIdx.y;
@@ -799,16 +805,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const long cache0 = static_cast<long>(kvh) * max_seq * HD;
     const int jmax = max_seq - 1;
-    // speculative loads (positions clamped to the cache)
-    const int jl = j0 + lane <= jmax ? j0 + lane : jmax;
+    const int npairs = kAttnSplit * G;
+    // K rows of this thread's first pair (positions clamped to the cache)
+    const int p0 = tid / G;
     uint4 kraw[kU];
     {
-        const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(jl) * HD);
+        const int j = j0 + p0 <= jmax ? j0 + p0 : jmax;
+        const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD);
 #pragma unroll
-        for (int c = 0; c < kU; ++c) kraw[c] = kr[c];
+        for (int c = 0; c < kU; ++c) kraw[c] = tid < npairs ? kr[c] : make_uint4(0, 0, 0, 0);
     }
     // V rows of the split: kVPer 16-byte units per thread, all loads issued
-    // before the first LDS store (one memory latency, not kVPer)
+    // before the first LDS store
     constexpr int kVPer = kAttnSplit * kU / kAttnThreads;
     static_assert(kVPer * kAttnThreads == kAttnSplit * kU, "V units per thread");
     uint4 vraw[kVPer];
@@ -828,9 +836,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     for (int t = 0; t < kVPer; ++t) {
         const int idx = tid + t * kAttnThreads;
         const int jj = idx / kU, c = idx - jj * kU;
-        float f[8];
-        unpack_bf16x8(vraw[t], f);
-        store_f8(&vs[jj][8 * c], f);
+        uint32_t* row = &vs[jj][4 * c];
+        row[0] = vraw[t].x;
+        row[1] = vraw[t].y;
+        row[2] = vraw[t].z;
+        row[3] = vraw[t].w;
     }
     if (has_q) {
         float f[8];
@@ -841,21 +851,25 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
     __syncthreads();
 
-    // scores: lane = position, wave w takes heads w, w + 4
-    if (lane < jn) {
-        float k[HD];
+    // scores
+    for (int pr = tid, first = 1; pr < npairs; pr += kAttnThreads, first = 0) {
+        const int p = pr / G, g = pr - p * G;
+        if (!first) {  // G > 4: a later pass loads its own rows
+            const int j = j0 + p <= jmax ? j0 + p : jmax;
+            const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD);
 #pragma unroll
-        for (int c = 0; c < kU; ++c) {
-            float f[8];
-            unpack_bf16x8(kraw[c], f);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) k[8 * c + e] = f[e];
+            for (int c = 0; c < kU; ++c) kraw[c] = kr[c];
         }
-        for (int g = wave; g < G; g += kAttnThreads / kWave) {
+        if (p < jn) {
             float acc = 0.0f;
 #pragma unroll
-            for (int d = 0; d < HD; ++d) acc = __builtin_fmaf(qs[g][d], k[d], acc);
-            sc[g][lane] = acc * scale;
+            for (int c = 0; c < kU; ++c) {
+                float f[8];
+                unpack_bf16x8(kraw[c], f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qs[g][8 * c + e], f[e], acc);
+            }
+            sc[g][p] = acc * scale;
         }
     }
     __syncthreads();
@@ -871,13 +885,19 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
         }
     }
     __syncthreads();
-    for (int o = tid; o < G * HD; o += kAttnThreads) {
-        const int g = o / HD, d = o - g * HD;
-        float acc = 0.0f;
-        for (int jj = 0; jj < jn; ++jj) acc = __builtin_fmaf(sc[g][jj], vs[jj][d], acc);
+    for (int o = tid; o < G * (HD / 2); o += kAttnThreads) {
+        const int g = o / (HD / 2), dp = o - g * (HD / 2);
+        float a0 = 0.0f, a1 = 0.0f;
+        for (int jj = 0; jj < jn; ++jj) {
+            const uint32_t w = vs[jj][dp];
+            const float e = sc[g][jj];
+            a0 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w & 0xFFFFu)), a0);
+            a1 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w >> 16)), a1);
+        }
         const int h = kvh * G + g;
-        pacc[(static_cast<long>(h) * S + s) * HD + d] = acc;
-        if (d == 0) {
+        float* out = pacc + (static_cast<long>(h) * S + s) * HD + 2 * dp;
+        *reinterpret_cast<float2*>(out) = make_float2(a0, a1);
+        if (dp == 0) {
             pm[h * S + s] = hmax[g];
             pl[h * S + s] = hsum[g];
         }
