@@ -58,6 +58,11 @@ struct Weights {
     __device__ ChunkLoad load(long r, int c, bool active) const {
         return chunk_at(meta, values, r, ms, vs, c, active && r < rows);
     }
+    // unconditional load of a row known to be in range
+    __device__ ChunkLoad load_in(long r, int c) const {
+        return ChunkLoad{*reinterpret_cast<const uint4*>(meta + r * ms + 4 * c),
+                         *reinterpret_cast<const uint2*>(values + r * vs + 2 * c), true};
+    }
 };
 
 // Up to three packed matrices with the same cols, stacked by rows: the
@@ -81,6 +86,17 @@ struct SegWeights {
         const int sv = vs + (s1 ? dvs1 : 0) + (s2 ? dvs2 : 0);
         const long lr = r - (s1 ? end0 : 0) - (s2 ? end1 - end0 : 0);
         return chunk_at(meta + om, values + ov, lr, sm, sv, c, active && r < rows);
+    }
+    // unconditional load of a row known to be in range
+    __device__ ChunkLoad load_in(long r, int c) const {
+        const bool s1 = r >= end0, s2 = r >= end1;
+        const long om = (s1 ? dm1 : 0) + (s2 ? dm2 : 0);
+        const long ov = (s1 ? dv1 : 0) + (s2 ? dv2 : 0);
+        const int sm = ms + (s1 ? dms1 : 0) + (s2 ? dms2 : 0);
+        const int sv = vs + (s1 ? dvs1 : 0) + (s2 ? dvs2 : 0);
+        const long lr = r - (s1 ? end0 : 0) - (s2 ? end1 - end0 : 0);
+        return ChunkLoad{*reinterpret_cast<const uint4*>(meta + om + lr * sm + 4 * c),
+                         *reinterpret_cast<const uint2*>(values + ov + lr * sv + 2 * c), true};
     }
 };
 
@@ -460,6 +476,78 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Si
     }
 }
 
+// ---- latency-bound kernel: one row span per block -------------------------------
+//
+// For matrices of a few steps per CU (the decode engine's projections, where
+// one launch reads a few MB and its time is a chain of latencies): block b of
+// G owns the rows [b*R/G, (b+1)*R/G) (R counted in row pairs for a pair
+// sink), thread (ro, c) the chunk c of rows start + i*RS + ro for i < MS.
+// Every chunk load of the thread is issued right after the activation loads
+// and before the prologue (rows past the span read the span's last row and
+// drop it), so the weight latency overlaps the prologue's instead of
+// following it.  Same per-chunk arithmetic and LDS row sums as
+// gemv_bitplane_kernel, so the results are identical.
+template <class W, class Act, class Sink, int MS>
+__global__ __launch_bounds__(kBlock) void gemv_span_kernel(W wt, Act act, Sink sink) {
+    extern __shared__ uint32_t smem[];
+    if (act.skip()) return;
+    constexpr bool kPairs = SinkPairs<Sink>::value;
+    const int nwords = wt.cols >> 5;
+    const int C = wt.cols / kChunk;
+    const int RS = rows_per_step<Sink>(C);
+    uint32_t* planes = smem;  // word [w * 8 + b]
+    int* acc = reinterpret_cast<int*>(smem + 8 * nwords);
+    const int tid = threadIdx.x;
+    const int c = tid % C;
+    const int ro = tid / C;
+    const long G = gridDim.x, b = blockIdx.x;
+    long start, end;
+    if constexpr (kPairs) {
+        const long pairs = wt.rows >> 1;
+        start = 2 * (b * pairs / G);
+        end = 2 * ((b + 1) * pairs / G);
+    } else {
+        start = b * wt.rows / G;
+        end = (b + 1) * wt.rows / G;
+    }
+    const int n = static_cast<int>(end - start);
+
+    act.offset(blockIdx.y);
+    sink.offset(blockIdx.y);
+    typename Act::Regs regs;
+    act.issue(tid, regs);  // activation loads first: they head the critical path
+    ChunkLoad L[MS];
+#pragma unroll
+    for (int i = 0; i < MS; ++i) {
+        const long r = start + i * RS + ro;
+        L[i] = wt.load_in(r < end ? r : end - 1, c);
+    }
+    act.prepare();
+    sink.prepare();
+    sink.prefetch(start, n, tid);
+    uint32_t X[4][8];
+    // prologue scratch after the row sums, 16-byte aligned
+    act.build(planes, wt.cols, tid,
+              reinterpret_cast<float*>(smem + ((8 * nwords + MS * RS + 3) & ~3)), regs);
+    for (int i = tid; i < MS * RS; i += kBlock) acc[i] = 0;
+    __syncthreads();
+    sink.bind(act);
+    if (ro < RS) {
+        load_x(planes + c * 32, X);
+#pragma unroll
+        for (int i = 0; i < MS; ++i) {
+            const int j = i * RS + ro;
+            if (j < n) atomicAdd(&acc[j], chunk_dot(L[i].k, L[i].v, X));
+        }
+    }
+    __syncthreads();
+    if constexpr (kPairs) {
+        for (int j = 2 * tid; j < n; j += 2 * kBlock) sink.store_pair(start + j, acc[j], acc[j + 1]);
+    } else {
+        for (int j = tid; j < n; j += kBlock) sink.store(start + j, acc[j]);
+    }
+}
+
 // ---- streaming kernel for one packed matrix -------------------------------------
 //
 // The same per-chunk arithmetic, laid out for matrices much larger than one
@@ -728,6 +816,34 @@ void launch_bitplane(const W& wt, Act act, Sink sink, hipStream_t stream, int to
     const size_t lds = plane_lds + 2 * static_cast<size_t>(tile_rows) * 4 + 12;
     hipLaunchKernelGGL((gemv_bitplane_kernel<W, Act, Sink>), dim3(grid, tokens), dim3(kBlock),
                        lds, stream, wt, act, sink, static_cast<int>(steps), tiles);
+}
+
+// Span launch over every CU (at most one block per CU) when each block's
+// span fits kSpanMaxSteps steps; returns false (nothing launched) otherwise.
+constexpr int kSpanMaxSteps = 4;
+
+template <class W, class Act, class Sink>
+bool launch_span(const W& wt, Act act, Sink sink, hipStream_t stream) {
+    const int C = wt.cols / kChunk;
+    const long RS = rows_per_step<Sink>(C);
+    const long unit = SinkPairs<Sink>::value ? 2 : 1;
+    const long units = wt.rows / unit;
+    if (units * unit != wt.rows || units == 0) return false;
+    long G = device_cu_count();
+    G = G < units ? G : units;
+    const long per = (units + G - 1) / G * unit;  // most rows of one block
+    const long ms = (per + RS - 1) / RS;
+    if (ms > kSpanMaxSteps) return false;
+    const size_t lds = static_cast<size_t>(wt.cols) + Act::extra_lds(wt.cols) +
+                       static_cast<size_t>(ms * RS) * 4 + 16;
+    const dim3 grid(static_cast<unsigned>(G)), block(kBlock);
+    switch (ms) {
+    case 1: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 1>), grid, block, lds, stream, wt, act, sink); break;
+    case 2: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 2>), grid, block, lds, stream, wt, act, sink); break;
+    case 3: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 3>), grid, block, lds, stream, wt, act, sink); break;
+    default: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 4>), grid, block, lds, stream, wt, act, sink); break;
+    }
+    return true;
 }
 
 template <class Src, class Sink>

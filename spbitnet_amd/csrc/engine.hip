@@ -1273,6 +1273,14 @@ Weights single_weights(const spb_sparse_linear& l) {
 
 using namespace spb;
 
+// A projection of the decode step: the span kernel (every weight load issued
+// before the prologue) when each CU's share fits its few steps, else the
+// tiled kernel.
+template <class W, class Act, class Sink>
+void launch_projection(const W& wt, Act act, Sink sink, hipStream_t s) {
+    if (!launch_span(wt, act, sink, s)) launch_bitplane(wt, act, sink, s);
+}
+
 struct spb_engine {
     spb_model_config cfg{};
     std::vector<spb_transformer_layer> layers;
@@ -1330,7 +1338,7 @@ struct spb_engine {
                 sink.hd = hd;
                 sink.hd_log2 = hd == 64 ? 6 : 7;
                 sink.max_seq = max_seq;
-                launch_bitplane(seg_weights(&L.q_proj, &L.k_proj, &L.v_proj),
+                launch_projection(seg_weights(&L.q_proj, &L.k_proj, &L.v_proj),
                                 ProducerPlanes<InputNorm>{p, st, 0.f}, sink, s);
             }
             if (hd == 64)
@@ -1345,7 +1353,7 @@ struct spb_engine {
                 AttnCombine p{pm, pl, pacc, hd, S, kAttnSplit};
                 SegBf16Sink sink{obuf, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma,
                                  L.o_proj.rows, L.o_proj.rows, 0.f, 0.f, 0.f};
-                launch_bitplane(single_weights(L.o_proj), ProducerPlanes<AttnCombine>{p, st, 0.f},
+                launch_projection(single_weights(L.o_proj), ProducerPlanes<AttnCombine>{p, st, 0.f},
                                 sink, s);
             }
             {
@@ -1354,14 +1362,14 @@ struct spb_engine {
                 SegBf16Sink sink{gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
                                  L.gate_proj.rows, L.gate_proj.rows + L.up_proj.rows, 0.f, 0.f,
                                  0.f};
-                launch_bitplane(seg_weights(&L.gate_proj, &L.up_proj, nullptr),
+                launch_projection(seg_weights(&L.gate_proj, &L.up_proj, nullptr),
                                 ProducerPlanes<SubNormResidualNorm>{p, st, 0.f}, sink, s);
             }
             {
                 const int I = cfg.intermediate_size;
                 Relu2Norm p{gu, gu + I, L.ffn_sub_norm, eps, I};
                 ResidualSink sink{xa, xb, L.down_proj.gamma, 0.f};
-                launch_bitplane(single_weights(L.down_proj), ProducerPlanes<Relu2Norm>{p, st, 0.f},
+                launch_projection(single_weights(L.down_proj), ProducerPlanes<Relu2Norm>{p, st, 0.f},
                                 sink, s);
             }
         }
