@@ -515,16 +515,24 @@ __global__ __launch_bounds__(kBlock) void gemv_span_kernel(W wt, Act act, Sink s
     act.offset(blockIdx.y);
     sink.offset(blockIdx.y);
     typename Act::Regs regs;
-    act.issue(tid, regs);  // activation loads first: they head the critical path
+    // Loads in three groups, kept in this order (the scheduler barriers stop
+    // the compiler from interleaving them): the activations, which head the
+    // critical path, then the weights, then the epilogue's.  The wait counter
+    // retires loads in issue order, so the prologue's waits then cover the
+    // activations alone.
+    act.issue(tid, regs);
+    __builtin_amdgcn_sched_barrier(0);
     ChunkLoad L[MS];
 #pragma unroll
     for (int i = 0; i < MS; ++i) {
         const long r = start + i * RS + ro;
         L[i] = wt.load_in(r < end ? r : end - 1, c);
     }
+    __builtin_amdgcn_sched_barrier(0);
     act.prepare();
     sink.prepare();
     sink.prefetch(start, n, tid);
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t X[4][8];
     // prologue scratch after the row sums, 16-byte aligned
     act.build(planes, wt.cols, tid,

@@ -60,25 +60,23 @@ struct EngineState {
     unsigned ticket;  // LM-head blocks finished in the current step
     int generated;
 };
-static_assert(offsetof(EngineState, pos) == 0 && offsetof(EngineState, prompt_len) == 4 &&
-                  offsetof(EngineState, limit) == 8 && offsetof(EngineState, done) == 12,
-              "state_head reads the first four fields as one 16-byte load");
+static_assert(offsetof(EngineState, pos) == 0 && offsetof(EngineState, done) == 12,
+              "state_pos and state_done read these offsets");
 
-// The decode state's {pos, prompt_len, limit, done} through one vector
-// (buffer) load.  A plain load of a uniform field compiles to a scalar load,
-// whose wait counter is shared with LDS: the first LDS wait of a prologue
-// would then also wait for it.  A vector load completes in order with the
-// kernel's other vector loads and is waited for only where it is used.
-struct StateHead {
-    int pos, prompt_len, limit, done;
-};
-__device__ __forceinline__ StateHead state_head(const EngineState* st) {
+// A field of the decode state through a one-dword vector (buffer) load.  A
+// plain load of a uniform field compiles to a scalar load, whose wait counter
+// is shared with LDS: the first LDS wait of a prologue would then also wait
+// for it.  A vector load completes in order with the kernel's other vector
+// loads and is waited for only where it is used.  One dword per field: a
+// wider load with dead fields lets the register allocator reuse their
+// registers, and writing such a register waits for the whole load.
+__device__ __forceinline__ int state_load(const EngineState* st, int offset) {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<EngineState*>(st), static_cast<short>(0), 16, kBufferFlags);
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, 0, 0, 0);
-    return StateHead{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z),
-                     static_cast<int>(v.w)};
+    return static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
 }
+__device__ __forceinline__ int state_pos(const EngineState* st) { return state_load(st, 0); }
+__device__ __forceinline__ int state_done(const EngineState* st) { return state_load(st, 12); }
 
 // ---- fixed-order arithmetic shared with the oracle ------------------------------
 
@@ -179,6 +177,11 @@ __device__ __forceinline__ float inv_rms(float ss, int n, float eps) {
 // kUnits units before using any of them.  Sums of squares accumulate per
 // thread in unit order (element order inside a unit) with fma, then
 // block_sum: this "unit order" is what the oracle restates.
+// A vector of at most kUnits * T units (every vector of the 2B model) is one
+// pass, loaded whole by issue() ahead of the GEMV's weight loads; the one-pass
+// code (kOne) then issues no global load at all.  A load issued after the
+// weights would make the prologue wait for them too: the memory wait counter
+// retires loads in issue order.
 
 constexpr int kUnits = 2;  // units per thread per pass
 
@@ -239,16 +242,20 @@ __device__ __forceinline__ float scale_by_weight(float* vec, const float* w, flo
 template <int T>
 struct HeldWeights {
     float f[kUnits][8];
+    // unconditional loads, units past the vector clamped to its last (their
+    // values are never used), so the wait counts of the prologue stay exact
     __device__ void load(const float* w, int units, int tid) {
-        if (units > kUnits * T) return;
 #pragma unroll
         for (int k = 0; k < kUnits; ++k) {
             const int u = tid + k * T;
-            if (u < units) load_f8(w + 8 * u, f[k]);
+            load_f8(w + 8 * (u < units ? u : units - 1), f[k]);
         }
     }
+    template <bool kOne>
     __device__ float apply(float* vec, const float* w, float inv, int units, int tid) const {
-        if (units > kUnits * T) return scale_by_weight<T>(vec, w, inv, units, tid);
+        if constexpr (!kOne) {
+            if (units > kUnits * T) return scale_by_weight<T>(vec, w, inv, units, tid);
+        }
         float m = 0.0f;
 #pragma unroll
         for (int k = 0; k < kUnits; ++k) {
@@ -275,9 +282,9 @@ struct HeldUnits {
     __device__ void load(const uint16_t* src, int units, int tid) {
         const uint4* s4 = reinterpret_cast<const uint4*>(src);
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {
+        for (int k = 0; k < kUnits; ++k) {  // unconditional, as HeldWeights::load
             const int u = tid + k * T;
-            if (u < units) r[k] = s4[u];
+            r[k] = s4[u < units ? u : units - 1];
         }
     }
 };
@@ -285,20 +292,20 @@ struct HeldUnits {
 // bf16 vector src -> vec (as float), returning this thread's sum of squares;
 // copy (nullable) receives the raw bf16 units.  first: the first pass,
 // already loaded.
-template <int T>
+template <int T, bool kOne>
 __device__ __forceinline__ float load_bf16_sumsq(const uint16_t* src, float* vec, int units,
                                                  int tid, uint16_t* copy,
                                                  const HeldUnits<T>& first) {
     const uint4* s4 = reinterpret_cast<const uint4*>(src);
     float ss = 0.0f;
-    for (int base = 0; base < units; base += kUnits * T) {
+    for (int base = 0; base < (kOne ? 1 : units); base += kUnits * T) {
         uint4 r[kUnits];
 #pragma unroll
         for (int k = 0; k < kUnits; ++k) {
             const int u = base + tid + k * T;
             if (base == 0)
                 r[k] = first.r[k];
-            else if (u < units)
+            else if (!kOne && u < units)
                 r[k] = s4[u];
         }
 #pragma unroll
@@ -343,7 +350,7 @@ constexpr int kRedSlot = 16;  // floats per reduction slot (>= kBlock / 64)
 // values.  The GEMVs run even after the decode state is done (their reads
 // stay in bounds and their outputs are scratch), so no kernel waits on the
 // state before its first loads.
-template <class P>
+template <class P, bool kOne>
 struct ProducerPlanes {
     P p;
     const EngineState* st;
@@ -360,7 +367,7 @@ struct ProducerPlanes {
         float* vec = scratch;
         float* aux = scratch + cols;
         float* red = scratch + cols * (1 + P::kAux);
-        const float m = p.fill(vec, aux, cols, tid, red, st, r);
+        const float m = p.template fill<kOne>(vec, aux, cols, tid, red, st, r);
         amax = block_max<kBlock>(m, red + 2 * kRedSlot);  // its barrier also orders vec
         BuildPlanes<LdsQuantSrc>{LdsQuantSrc{vec, quant_scale(amax)}}.build(planes, cols, tid,
                                                                             nullptr);
@@ -391,12 +398,18 @@ struct InputNorm {
         r.hx.load(r.src, n >> 3, tid);
         r.hw.load(w, n >> 3, tid);
     }
+    template <bool kOne>
+    __device__ float fill_pass(float* vec, int tid, float* red, Regs& r) const {
+        const float ss = load_bf16_sumsq<kBlock, kOne>(
+            r.src, vec, n >> 3, tid, embed && blockIdx.x == 0 ? x_out : nullptr, r.hx);
+        const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
+        return r.hw.template apply<kOne>(vec, w, inv, n >> 3, tid);
+    }
+    bool one_pass() const { return (n >> 3) <= kUnits * kBlock; }
+    template <bool kOne>
     __device__ float fill(float* vec, float*, int, int tid, float* red, const EngineState*,
                           Regs& r) const {
-        const float ss = load_bf16_sumsq<kBlock>(r.src, vec, n >> 3, tid,
-                                                 embed && blockIdx.x == 0 ? x_out : nullptr, r.hx);
-        const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
-        return r.hw.apply(vec, w, inv, n >> 3, tid);
+        return fill_pass<kOne>(vec, tid, red, r);
     }
 };
 
@@ -412,56 +425,89 @@ struct AttnCombine {
     const float* pl;    // [nh][S]
     const float* pacc;  // [nh][S][hd]
     int hd, S, chunk;
+    int n;  // nh * hd
+    bool one_pass() const { return (n >> 3) <= kBlock; }  // a thread per unit
+    struct Batch {
+        float pv[kBatch][8], lv[kBatch], mv[kBatch];
+    };
+    // batch 0 of the thread's first unit is loaded before pos is known (ahead
+    // of the GEMV's weights)
     struct Regs {
         int pos;
+        Batch b0;
     };
-    __device__ void issue(int, const EngineState* st, Regs& r) const { r.pos = state_head(st).pos; }
-    __device__ float fill(float* vec, float*, int n, int tid, float*, const EngineState*,
-                          Regs& r) const {
-        int ns = r.pos / chunk + 1;  // splits holding positions 0..pos
-        ns = ns < S ? ns : S;
-        const int units = n >> 3;
-        float mx = 0.0f;
-        for (int u = tid; u < units; u += kBlock) {
-            const int h = (8 * u) / hd, d0 = 8 * u - h * hd;
-            const float* m = pm + h * S;
-            float M = -INFINITY;
-            for (int s0 = 0; s0 < ns; s0 += kBatch) {
-                float mv[kBatch];
+    // splits s0 .. s0 + kBatch - 1 of unit (h, d0); unconditional, splits
+    // clamped to S - 1 (those past pos's are dropped)
+    __device__ void load_batch(int h, int d0, int s0, Batch& b) const {
 #pragma unroll
-                for (int b = 0; b < kBatch; ++b) mv[b] = s0 + b < ns ? m[s0 + b] : -INFINITY;
-#pragma unroll
-                for (int b = 0; b < kBatch; ++b) M = __builtin_fmaxf(M, mv[b]);
-            }
-            float l = 0.0f, a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            for (int s0 = 0; s0 < ns; s0 += kBatch) {
-                float pv[kBatch][8], lv[kBatch], mv[kBatch];
-#pragma unroll
-                for (int b = 0; b < kBatch; ++b) {
-                    const int s = s0 + b;
-                    if (s < ns) {
-                        load_f8(pacc + (static_cast<long>(h) * S + s) * hd + d0, pv[b]);
-                        lv[b] = pl[h * S + s];
-                        mv[b] = m[s];
-                    }
-                }
-#pragma unroll
-                for (int b = 0; b < kBatch; ++b) {
-                    if (s0 + b < ns) {
-                        const float w = exp_neg(mv[b] - M);
-                        l = __builtin_fmaf(w, lv[b], l);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) a[e] = __builtin_fmaf(w, pv[b][e], a[e]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                a[e] = bf16r(a[e] / l);
-                mx = __builtin_fmaxf(mx, __builtin_fabsf(a[e]));
-            }
-            store_f8(vec + 8 * u, a);
+        for (int k = 0; k < kBatch; ++k) {
+            const int s = s0 + k < S ? s0 + k : S - 1;
+            load_f8(pacc + (static_cast<long>(h) * S + s) * hd + d0, b.pv[k]);
+            b.lv[k] = pl[h * S + s];
+            b.mv[k] = pm[h * S + s];
         }
+    }
+    __device__ void issue(int tid, const EngineState* st, Regs& r) const {
+        r.pos = state_pos(st);
+        const int u = tid < (n >> 3) ? tid : (n >> 3) - 1;
+        const int h = (8 * u) / hd;
+        load_batch(h, 8 * u - h * hd, 0, r.b0);
+    }
+    // unit u over splits 0 .. ns-1, batch 0 from held when non-null
+    __device__ float combine(float* vec, int u, int ns, const Batch* held) const {
+        const int h = (8 * u) / hd, d0 = 8 * u - h * hd;
+        Batch b0;
+        if (held)
+            b0 = *held;
+        else
+            load_batch(h, d0, 0, b0);
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) M = __builtin_fmaxf(M, k < ns ? b0.mv[k] : -INFINITY);
+        for (int s0 = kBatch; s0 < ns; s0 += kBatch) {
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k)
+                M = __builtin_fmaxf(M, s0 + k < ns ? pm[h * S + s0 + k] : -INFINITY);
+        }
+        float l = 0.0f, a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        auto accumulate = [&](const Batch& b, int s0) {
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                if (s0 + k < ns) {
+                    const float w = exp_neg(b.mv[k] - M);
+                    l = __builtin_fmaf(w, b.lv[k], l);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) a[e] = __builtin_fmaf(w, b.pv[k][e], a[e]);
+                }
+            }
+        };
+        accumulate(b0, 0);
+        for (int s0 = kBatch; s0 < ns; s0 += kBatch) {
+            Batch b;
+            load_batch(h, d0, s0, b);
+            accumulate(b, s0);
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            a[e] = bf16r(a[e] / l);
+            mx = __builtin_fmaxf(mx, __builtin_fabsf(a[e]));
+        }
+        store_f8(vec + 8 * u, a);
+        return mx;
+    }
+    template <bool kOne>
+    __device__ float fill(float* vec, float*, int, int tid, float*, const EngineState*,
+                          Regs& r) const {
+        // opaque: pos stays a vector register until here (a scalar copy of a
+        // uniform load is otherwise placed right after the load, and waits
+        // for it ahead of the GEMV's weight loads)
+        int ns = opaque(r.pos) / chunk + 1;  // splits holding positions 0..pos
+        ns = ns < S ? ns : S;
+        if constexpr (kOne) return tid < (n >> 3) ? combine(vec, tid, ns, &r.b0) : 0.0f;
+        float mx = combine(vec, tid, ns, &r.b0);  // more units than threads
+        for (int u = tid + kBlock; u < (n >> 3); u += kBlock)
+            mx = __builtin_fmaxf(mx, combine(vec, u, ns, nullptr));
         return mx;
     }
 };
@@ -486,16 +532,21 @@ struct SubNormResidualNorm {
         const int units = n >> 3;
         r.ho.load(o, units, tid);
         r.hr.load(res, units, tid);
-        if (w_sub) r.hs.load(w_sub, units, tid);
+        r.hs.load(w_sub ? w_sub : w_post, units, tid);  // unconditional (dropped when absent)
         r.hp.load(w_post, units, tid);
     }
+    bool one_pass() const { return (n >> 3) <= kUnits * kBlock; }
+    template <bool kOne>
     __device__ float fill(float* vec, float* aux, int, int tid, float* red, const EngineState*,
                           Regs& r) const {
+        return fill_pass<kOne>(vec, aux, tid, red, r);
+    }
+    template <bool kOne>
+    __device__ float fill_pass(float* vec, float* aux, int tid, float* red, Regs& r) const {
         const int units = n >> 3;
-        const bool held = units <= kUnits * kBlock;
         // o -> vec (sum of squares), residual -> aux
         float ss = 0.0f;
-        for (int base = 0; base < units; base += kUnits * kBlock) {
+        for (int base = 0; base < (kOne ? 1 : units); base += kUnits * kBlock) {
             uint4 ro[kUnits], rr[kUnits];
 #pragma unroll
             for (int k = 0; k < kUnits; ++k) {
@@ -503,7 +554,7 @@ struct SubNormResidualNorm {
                 if (base == 0) {
                     ro[k] = r.ho.r[k];
                     rr[k] = r.hr.r[k];
-                } else if (u < units) {
+                } else if (!kOne && u < units) {
                     ro[k] = reinterpret_cast<const uint4*>(o)[u];
                     rr[k] = reinterpret_cast<const uint4*>(res)[u];
                 }
@@ -525,7 +576,7 @@ struct SubNormResidualNorm {
         const float inv = w_sub ? inv_rms(block_sum<kBlock>(ss, red), n, eps) : 1.0f;
         // o = bf16((o * inv) * w_sub) (when present); x = bf16(o + r)
         float ss2 = 0.0f;
-        for (int base = 0; base < units; base += kUnits * kBlock) {
+        for (int base = 0; base < (kOne ? 1 : units); base += kUnits * kBlock) {
 #pragma unroll
             for (int k = 0; k < kUnits; ++k) {
                 const int u = base + tid + k * kBlock;
@@ -534,7 +585,7 @@ struct SubNormResidualNorm {
                 load_f8(vec + 8 * u, f);
                 load_f8(aux + 8 * u, g);
                 if (w_sub) {
-                    if (held) {
+                    if (kOne) {
 #pragma unroll
                         for (int e = 0; e < 8; ++e) ws[e] = r.hs.f[k][e];
                     } else {
@@ -560,7 +611,7 @@ struct SubNormResidualNorm {
             }
         }
         const float inv2 = inv_rms(block_sum<kBlock>(ss2, red + kRedSlot), n, eps);
-        return r.hp.apply(vec, w_post, inv2, units, tid);
+        return r.hp.template apply<kOne>(vec, w_post, inv2, units, tid);
     }
 };
 
@@ -572,6 +623,7 @@ struct Relu2Norm {
     const uint16_t* g;
     const uint16_t* u;
     const float* w;
+    const float* w_load;  // w, or any buffer of at least n floats when w is absent
     float eps;
     int n;
     struct Regs {
@@ -582,13 +634,19 @@ struct Relu2Norm {
         const int units = n >> 3;
         r.hg.load(g, units, tid);
         r.hu.load(u, units, tid);
-        if (w) r.hw.load(w, units, tid);
+        r.hw.load(w_load, units, tid);  // unconditional (dropped when w is absent)
     }
+    bool one_pass() const { return (n >> 3) <= kUnits * kBlock; }
+    template <bool kOne>
     __device__ float fill(float* vec, float*, int, int tid, float* red, const EngineState*,
                           Regs& r) const {
+        return fill_pass<kOne>(vec, tid, red, r);
+    }
+    template <bool kOne>
+    __device__ float fill_pass(float* vec, int tid, float* red, Regs& r) const {
         const int units = n >> 3;
         float ss = 0.0f, mx = 0.0f;
-        for (int base = 0; base < units; base += kUnits * kBlock) {
+        for (int base = 0; base < (kOne ? 1 : units); base += kUnits * kBlock) {
             uint4 rg[kUnits], ru[kUnits];
 #pragma unroll
             for (int k = 0; k < kUnits; ++k) {
@@ -596,7 +654,7 @@ struct Relu2Norm {
                 if (base == 0) {
                     rg[k] = r.hg.r[k];
                     ru[k] = r.hu.r[k];
-                } else if (q < units) {
+                } else if (!kOne && q < units) {
                     rg[k] = reinterpret_cast<const uint4*>(g)[q];
                     ru[k] = reinterpret_cast<const uint4*>(u)[q];
                 }
@@ -624,7 +682,7 @@ struct Relu2Norm {
         }
         if (!w) return mx;
         const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
-        return r.hw.apply(vec, w, inv, units, tid);
+        return r.hw.template apply<kOne>(vec, w, inv, units, tid);
     }
 };
 
@@ -668,7 +726,7 @@ struct ResidualSink {
     __device__ void prepare() {}
     __device__ void prefetch(long row0, int n, int tid) {
         pre_row = tid < n ? row0 + tid : -1;
-        pre_res = tid < n ? res[row0 + tid] : 0;
+        pre_res = res[row0 + (tid < n ? tid : 0)];  // unconditional
     }
     template <class A>
     __device__ void bind(const A& a) {
@@ -719,12 +777,11 @@ struct QkvRopeSink {
         return ((static_cast<long>(r >> hd_log2) * max_seq + pos) << hd_log2) + (r & (hd - 1));
     }
     __device__ void prefetch(long row0, int n, int tid) {
-        const StateHead h = state_head(st);  // needed only by the cache writes
-        pos = h.pos;
-        live = !h.done;
+        pos = state_pos(st);  // pos and done are needed only by the cache writes
+        live = !state_done(st);
         pre_row = 2 * tid < n ? row0 + 2 * tid : -1;
-        pre_cs = make_float2(0.0f, 0.0f);
-        if (pre_row >= 0 && pre_row < end1) pre_cs = cur_rope[rope_pair(pre_row)];
+        // unconditional (row 0's pair when the thread has no q/k row)
+        pre_cs = cur_rope[rope_pair(pre_row >= 0 && pre_row < end1 ? pre_row : 0)];
     }
     template <class A>
     __device__ void bind(const A& a) {
@@ -830,8 +887,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     uint4 qraw = make_uint4(0, 0, 0, 0);
     const bool has_q = tid < G * kU;
     if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + (kvh * G) * HD)[tid];
-    const StateHead sh = state_head(st);
-    const int done = sh.done, pos = sh.pos;
+    const int done = state_done(st), pos = state_pos(st);
 #pragma unroll
     for (int t = 0; t < kVPer; ++t) {
         const int idx = tid + t * kAttnThreads;
@@ -954,18 +1010,21 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
                 w[k] = c < nch ? wr[c] : make_uint4(0, 0, 0, 0);
         }
     };
+    // x and the norm weights first (the prologue waits for them alone), then
+    // the first rows; H <= NC * 64 elements are one pass of kLmBlock threads
+    constexpr bool kOne = NC * kWave <= kUnits * kLmBlock;
+    HeldWeights<kLmBlock> hw;
+    HeldUnits<kLmBlock> hx;
+    hx.load(x, H >> 3, tid);
+    hw.load(wn, H >> 3, tid);
     uint4 wa[NC], wb[NC], wc[NC];
     load_row(0, wa);
     if (NB == 3) load_row(1, wb);
     if (st->done) return;  // after the first row loads (they are in bounds either way)
 
-    HeldWeights<kLmBlock> hw;
-    HeldUnits<kLmBlock> hx;
-    hx.load(x, H >> 3, tid);
-    hw.load(wn, H >> 3, tid);
-    const float ss = load_bf16_sumsq<kLmBlock>(x, xs, H >> 3, tid, nullptr, hx);
+    const float ss = load_bf16_sumsq<kLmBlock, kOne>(x, xs, H >> 3, tid, nullptr, hx);
     const float inv = inv_rms(block_sum<kLmBlock>(ss, red), H, eps);
-    hw.apply(xs, wn, inv, H >> 3, tid);
+    hw.template apply<kOne>(xs, wn, inv, H >> 3, tid);
     __syncthreads();
     uint4 xp[NC];
 #pragma unroll
@@ -1277,8 +1336,16 @@ using namespace spb;
 // before the prologue) when each CU's share fits its few steps, else the
 // tiled kernel.
 template <class W, class Act, class Sink>
-void launch_projection(const W& wt, Act act, Sink sink, hipStream_t s) {
+void launch_gemv(const W& wt, Act act, Sink sink, hipStream_t s) {
     if (!launch_span(wt, act, sink, s)) launch_bitplane(wt, act, sink, s);
+}
+// The prologue in its one-pass form when the vector fits one pass.
+template <class W, class P, class Sink>
+void launch_projection(const W& wt, const P& p, const EngineState* st, Sink sink, hipStream_t s) {
+    if (p.one_pass())
+        launch_gemv(wt, ProducerPlanes<P, true>{p, st, 0.f}, sink, s);
+    else
+        launch_gemv(wt, ProducerPlanes<P, false>{p, st, 0.f}, sink, s);
 }
 
 struct spb_engine {
@@ -1339,7 +1406,7 @@ struct spb_engine {
                 sink.hd_log2 = hd == 64 ? 6 : 7;
                 sink.max_seq = max_seq;
                 launch_projection(seg_weights(&L.q_proj, &L.k_proj, &L.v_proj),
-                                ProducerPlanes<InputNorm>{p, st, 0.f}, sink, s);
+                                p, st, sink, s);
             }
             if (hd == 64)
                 hipLaunchKernelGGL(attention_kernel<64>, dim3(S, nkv), dim3(kAttnThreads), 0, s,
@@ -1350,11 +1417,10 @@ struct spb_engine {
                                    qkv, kcache[l], vcache[l], pm, pl, pacc, st, nh, nkv,
                                    max_seq, S, scale);
             {
-                AttnCombine p{pm, pl, pacc, hd, S, kAttnSplit};
+                AttnCombine p{pm, pl, pacc, hd, S, kAttnSplit, nh * hd};
                 SegBf16Sink sink{obuf, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma,
                                  L.o_proj.rows, L.o_proj.rows, 0.f, 0.f, 0.f};
-                launch_projection(single_weights(L.o_proj), ProducerPlanes<AttnCombine>{p, st, 0.f},
-                                sink, s);
+                launch_projection(single_weights(L.o_proj), p, st, sink, s);
             }
             {
                 SubNormResidualNorm p{obuf, xa, xb, L.attn_sub_norm, L.post_attention_layernorm,
@@ -1363,14 +1429,16 @@ struct spb_engine {
                                  L.gate_proj.rows, L.gate_proj.rows + L.up_proj.rows, 0.f, 0.f,
                                  0.f};
                 launch_projection(seg_weights(&L.gate_proj, &L.up_proj, nullptr),
-                                ProducerPlanes<SubNormResidualNorm>{p, st, 0.f}, sink, s);
+                                p, st, sink, s);
             }
             {
                 const int I = cfg.intermediate_size;
-                Relu2Norm p{gu, gu + I, L.ffn_sub_norm, eps, I};
+                // without the sub-norm, the held-weight loads read gu (2I bf16 = I floats)
+                Relu2Norm p{gu, gu + I, L.ffn_sub_norm,
+                            L.ffn_sub_norm ? L.ffn_sub_norm : reinterpret_cast<const float*>(gu),
+                            eps, I};
                 ResidualSink sink{xa, xb, L.down_proj.gamma, 0.f};
-                launch_projection(single_weights(L.down_proj), ProducerPlanes<Relu2Norm>{p, st, 0.f},
-                                sink, s);
+                launch_projection(single_weights(L.down_proj), p, st, sink, s);
             }
         }
         hipLaunchKernelGGL(lm_kernel, dim3(lm_grid), dim3(kLmBlock), 0, s, lm_head, xa,
