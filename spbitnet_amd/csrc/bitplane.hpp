@@ -214,9 +214,10 @@ struct BuildPlanes {
     Src src;
     __device__ void offset(long t) { src.offset(t); }
     __device__ void prepare() { src.prepare(); }
-    // Transposes the activations, 8 columns per thread, into LDS planes
-    // (bytes of word [w*8+b]).  The loads of up to two units are issued
-    // before either is transposed.
+    // Transposes the activations, 8 columns per thread, into the LDS planes
+    // (plane-major: word (b, w) at b * nw + w, nw = cols / 32; a unit is one
+    // byte of each plane).  The loads of up to two units are issued before
+    // either is transposed.
     struct Regs {};
     static size_t extra_lds(int) { return 0; }
     __device__ bool skip() const { return false; }
@@ -226,6 +227,7 @@ struct BuildPlanes {
     }
     __device__ void build(uint32_t* planes, int cols, int tid, float*) const {
         const int units = cols >> 3;
+        const int nw = cols >> 5;
         uint8_t* pb = reinterpret_cast<uint8_t*>(planes);
         for (int u0 = tid; u0 < units; u0 += 2 * kBlock) {
             const int u1 = u0 + kBlock;
@@ -236,16 +238,16 @@ struct BuildPlanes {
             const int w0 = u0 >> 2, q0 = u0 & 3;
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                pb[(w0 * 8 + b) * 4 + q0] = static_cast<uint8_t>(lo0 >> (8 * b));
-                pb[(w0 * 8 + b + 4) * 4 + q0] = static_cast<uint8_t>(hi0 >> (8 * b));
+                pb[(b * nw + w0) * 4 + q0] = static_cast<uint8_t>(lo0 >> (8 * b));
+                pb[((b + 4) * nw + w0) * 4 + q0] = static_cast<uint8_t>(hi0 >> (8 * b));
             }
             if (u1 < units) {
                 transpose8x8(lo1, hi1);
                 const int w1 = u1 >> 2, q1 = u1 & 3;
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
-                    pb[(w1 * 8 + b) * 4 + q1] = static_cast<uint8_t>(lo1 >> (8 * b));
-                    pb[(w1 * 8 + b + 4) * 4 + q1] = static_cast<uint8_t>(hi1 >> (8 * b));
+                    pb[(b * nw + w1) * 4 + q1] = static_cast<uint8_t>(lo1 >> (8 * b));
+                    pb[((b + 4) * nw + w1) * 4 + q1] = static_cast<uint8_t>(hi1 >> (8 * b));
                 }
             }
         }
@@ -253,10 +255,10 @@ struct BuildPlanes {
 };
 
 // Planes precomputed in global memory (spb_activation_planes or
-// spb_absmax_quantize_planes_*): the block copies the cols bytes into LDS with
-// 16-byte loads (every thread of the block then reads its chunk from LDS; a
-// direct global read per thread would request 128 B x 512 threads per block
-// from L2 for cols bytes of data).
+// spb_absmax_quantize_planes_*, word [w*8+b]): the block copies the cols bytes
+// into the plane-major LDS layout with 16-byte loads (every thread of the
+// block then reads its chunk from LDS; a direct global read per thread would
+// request 128 B x 512 threads per block from L2 for cols bytes of data).
 struct GlobalPlanes {
     const uint32_t* p;
     __device__ void offset(long) {}
@@ -267,8 +269,15 @@ struct GlobalPlanes {
     __device__ void issue(int, Regs&) {}
     __device__ void build(uint32_t* planes, int cols, int tid, float*, Regs&) const {
         const uint4* src = reinterpret_cast<const uint4*>(p);
-        uint4* dst = reinterpret_cast<uint4*>(planes);
-        for (int i = tid; i < (cols >> 4); i += kBlock) dst[i] = src[i];
+        const int nw = cols >> 5;
+        for (int i = tid; i < (cols >> 4); i += kBlock) {
+            const uint4 v = src[i];  // words w*8 + b .. +3 with w = i / 2, b = 4 * (i % 2)
+            uint32_t* d = planes + (4 * (i & 1)) * nw + (i >> 1);
+            d[0] = v.x;
+            d[nw] = v.y;
+            d[2 * nw] = v.z;
+            d[3 * nw] = v.w;
+        }
     }
 };
 
@@ -350,19 +359,17 @@ __device__ __forceinline__ int chunk_dot(const uint4 K, const uint2 V, const uin
 }
 
 // The 32 plane words of one 128-column chunk (128 contiguous bytes).
-__device__ __forceinline__ void load_x(const uint32_t* src, uint32_t (&X)[4][8]) {
-    const uint4* p = reinterpret_cast<const uint4*>(src);
+// The 4 x 8 plane words of chunk c (columns 128c .. 128c+127) from the
+// plane-major LDS layout: one 16-byte read per plane, at 16c bytes into the
+// plane, so the chunks of neighbouring threads sit in neighbouring banks.
+__device__ __forceinline__ void load_x(const uint32_t* planes, int c, int nw, uint32_t (&X)[4][8]) {
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const uint4 a = p[2 * w], b = p[2 * w + 1];
-        X[w][0] = a.x;
-        X[w][1] = a.y;
-        X[w][2] = a.z;
-        X[w][3] = a.w;
-        X[w][4] = b.x;
-        X[w][5] = b.y;
-        X[w][6] = b.z;
-        X[w][7] = b.w;
+    for (int b = 0; b < 8; ++b) {
+        const uint4 v = *reinterpret_cast<const uint4*>(planes + b * nw + 4 * c);
+        X[0][b] = v.x;
+        X[1][b] = v.y;
+        X[2][b] = v.z;
+        X[3][b] = v.w;
     }
 }
 
@@ -405,7 +412,7 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Si
     const int C = wt.cols / kChunk;
     const int RS = rows_per_step<Sink>(C);
     const int tile_rows = RS * tile_steps;
-    uint32_t* planes = smem;  // word [w * 8 + b]
+    uint32_t* planes = smem;  // plane-major: word (b, w) at b * nwords + w
     int* acc0 = reinterpret_cast<int*>(smem + 8 * nwords);
     int* acc1 = acc0 + tile_rows;
 
@@ -436,7 +443,7 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Si
     for (int i = tid; i < 2 * tile_rows; i += kBlock) acc0[i] = 0;
     __syncthreads();
     sink.bind(act);
-    if (active) load_x(planes + c * 32, X);
+    if (active) load_x(planes, c, nwords, X);
 
     for (;;) {
         int step_n = step + 1;
@@ -495,7 +502,7 @@ __global__ __launch_bounds__(kBlock) void gemv_span_kernel(W wt, Act act, Sink s
     const int nwords = wt.cols >> 5;
     const int C = wt.cols / kChunk;
     const int RS = rows_per_step<Sink>(C);
-    uint32_t* planes = smem;  // word [w * 8 + b]
+    uint32_t* planes = smem;  // plane-major: word (b, w) at b * nwords + w
     int* acc = reinterpret_cast<int*>(smem + 8 * nwords);
     const int tid = threadIdx.x;
     const int c = tid % C;
@@ -541,7 +548,7 @@ __global__ __launch_bounds__(kBlock) void gemv_span_kernel(W wt, Act act, Sink s
     __syncthreads();
     sink.bind(act);
     if (ro < RS) {
-        load_x(planes + c * 32, X);
+        load_x(planes, c, nwords, X);
 #pragma unroll
         for (int i = 0; i < MS; ++i) {
             const int j = i * RS + ro;
@@ -600,7 +607,7 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
     const bool last = blockIdx.x == gridDim.x - 1;
     const int tail = last ? rows - nfull * RS : 0;   // rows after the full steps
     const int span = (s_end - s_begin) * RS + tail;  // rows of this block
-    uint32_t* planes = smem;
+    uint32_t* planes = smem;  // plane-major: word (b, w) at b * nwords + w
     int* acc = reinterpret_cast<int*>(smem + 8 * nwords);
     const int acc_slots = (span + RS + 3) & ~3;
 
@@ -648,7 +655,7 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
     __syncthreads();
     sink.bind(act);
     uint32_t X[4][8];
-    load_x(planes + c * 32, X);
+    load_x(planes, c, nwords, X);
 
     auto reduce = [&](int s, const StreamLoad& L) {
         const int d = chunk_dot(L.k, L.v, X);

@@ -22,13 +22,17 @@
 //     one v_bitop3_b32 and one accumulating v_bcnt_u32_b32 per plane per 32
 //     columns, additions and bit operations only, no multiplies on the
 //     activations.  popc(N) is the number of set sign bits.
-//   * Plane layout (shared by LDS and the global "activation planes" format):
-//     word [w * 8 + b] holds plane b of columns 32w .. 32w+31, so the 8
-//     planes of a 128-column chunk are 128 contiguous bytes.  Planes come
-//     either from a prologue that transposes the activations 8 columns per
-//     thread (SWAR 8x8 bit transpose, lane-parallel, one load per thread),
-//     or precomputed in global memory by spb_activation_planes /
-//     spb_absmax_quantize_planes_*.
+//   * Plane layouts.  Global "activation planes" format: word [w * 8 + b]
+//     holds plane b of columns 32w .. 32w+31 (the 8 planes of a 128-column
+//     chunk are 128 contiguous bytes).  In LDS the planes are plane-major,
+//     word (b, w) at b * (cols / 32) + w, so a thread reads its chunk with one
+//     16-byte read per plane and neighbouring chunks fall in neighbouring
+//     banks (the global layout would put every chunk of a wave in the same
+//     banks).  Planes come either from a prologue that transposes the
+//     activations 8 columns per thread (SWAR 8x8 bit transpose,
+//     lane-parallel, one load per thread), or precomputed in global memory by
+//     spb_activation_planes / spb_absmax_quantize_planes_* and rearranged on
+//     the copy into LDS.
 //   * Work mapping (streaming kernel): a thread owns one 128-column chunk
 //     (16 bytes of meta, 8 of signs, 128/64-bit buffer loads) and keeps that
 //     chunk's 32 plane words in registers for every row it visits;
