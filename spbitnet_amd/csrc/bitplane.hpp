@@ -151,6 +151,54 @@ __device__ __forceinline__ void transpose8x8(uint32_t& lo, uint32_t& hi) {
     hi ^= t >> 4;
 }
 
+// ---- one unit of activations from registers into the LDS planes ---------------------
+//
+// q = clamp(rint_ne(v * scale), -128, 127), the reference's rule
+// (src/kernels/sparse_ternary.cu:199, 216-217), as v * scale (rounded) plus
+// 1.5 * 2^23: the sum's ulp is 1, so the addition rounds to the nearest
+// integer, ties to even, while |v * scale| < 2^22, and one med3 clamps the
+// biased value (anything beyond 2^22 clamps to the same end).  The low byte
+// of the biased float is q's two's-complement byte.  (NaN inputs are not
+// defined here: activations are finite.)
+__device__ __forceinline__ uint32_t q8_biased(float v, float scale) {
+    constexpr float kBias = 12582912.0f;
+    return __builtin_bit_cast(
+        uint32_t, __builtin_amdgcn_fmed3f(v * scale + kBias, kBias - 128.0f, kBias + 127.0f));
+}
+
+// Unit u (columns 8u .. 8u+7) of the activations, 8 floats in registers,
+// quantised and stored into the plane-major LDS planes.  The 4 units of a
+// plane word sit in the 4 lanes of a quad (u % 4 == lane % 4 for
+// u = tid + k * kBlock); after the 8x8 bit transpose each lane holds one byte
+// of every plane, and a byte transpose across the quad (two DPP exchanges,
+// lane ^ 1 then lane ^ 2) gives lane q the whole words of planes q and q + 4:
+// two dword stores instead of eight byte stores.  All 4 lanes of a quad run
+// this together.
+__device__ __forceinline__ void store_unit_planes(uint32_t* planes, int nw, int u,
+                                                  const float (&v)[8], float scale) {
+    uint32_t t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = q8_biased(v[e], scale);
+    // byte e of (lo, hi) = column 8u + e
+    uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], 0x0C0C0400u) | __builtin_amdgcn_perm(t[3], t[2], 0x04000C0Cu);
+    uint32_t hi = __builtin_amdgcn_perm(t[5], t[4], 0x0C0C0400u) | __builtin_amdgcn_perm(t[7], t[6], 0x04000C0Cu);
+    transpose8x8(lo, hi);  // byte b of lo / hi: plane b / b + 4 of the unit's 8 columns
+    const int q = u & 3;
+    // stage 1 (partner lane ^ 1): even lanes [own0, p0, own2, p2], odd [p1, own1, p3, own3];
+    // stage 2 (partner lane ^ 2): lanes 0, 1 [own0, own1, p0, p1], lanes 2, 3 [p2, p3, own2, own3]
+    const uint32_t sel1 = (q & 1) ? 0x03070105u : 0x06020400u;
+    const uint32_t sel2 = (q & 2) ? 0x03020706u : 0x05040100u;
+    auto quad_t = [&](uint32_t x) {
+        const uint32_t p1 = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xF, 0xF, true));
+        x = __builtin_amdgcn_perm(p1, x, sel1);
+        const uint32_t p2 = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x4E, 0xF, 0xF, true));
+        return __builtin_amdgcn_perm(p2, x, sel2);
+    };
+    const int w = u >> 2;
+    planes[q * nw + w] = quad_t(lo);
+    planes[(q + 4) * nw + w] = quad_t(hi);
+}
+
 // ---- activation sources ----------------------------------------------------------
 
 // int8 activations.
@@ -358,7 +406,6 @@ __device__ __forceinline__ int chunk_dot(const uint4 K, const uint2 V, const uin
     return s;
 }
 
-// The 32 plane words of one 128-column chunk (128 contiguous bytes).
 // The 4 x 8 plane words of chunk c (columns 128c .. 128c+127) from the
 // plane-major LDS layout: one 16-byte read per plane, at 16c bytes into the
 // plane, so the chunks of neighbouring threads sit in neighbouring banks.
@@ -594,7 +641,9 @@ __device__ __forceinline__ uint2 as_uint2(u32x2_t v) { return make_uint2(v.x, v.
 
 constexpr int kStreamMaxRows = 8192;  // LDS row sums per block (32 KB)
 
-template <class Act, class Sink>
+constexpr int kStreamDepth = 4;  // register sets: kStreamDepth - 1 steps in flight
+
+template <class Act, class Sink, int D>
 __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act, Sink sink, int nfull, int row_base) {
     extern __shared__ uint32_t smem[];
     const int nwords = wt.cols >> 5;
@@ -643,10 +692,12 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
     auto at = [&](int s) { return s < s_end ? s : s_last; };
 
     // The activation loads go first (they head the prologue's chain), then
-    // the first three steps' weights, which arrive while the prologue runs.
+    // the first D - 1 steps' weights, which arrive while the prologue runs.
     typename Act::Regs regs;
     act.issue(tid, regs);
-    StreamLoad S0 = load(at(s_begin)), S1 = load(at(s_begin + 1)), S2 = load(at(s_begin + 2)), S3;
+    StreamLoad S[D];
+#pragma unroll
+    for (int i = 0; i < D - 1; ++i) S[i] = load(at(s_begin + i));
     act.prepare();
     sink.prepare();
     act.build(planes, wt.cols, tid,
@@ -663,32 +714,28 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
     };
 
     if (n > 0) {
-        // A counted loop over groups of four steps with its only exit at the
+        // A counted loop over groups of D steps with its only exit at the
         // latch (a mid-body exit would join the loop head on a path with fewer
         // loads in flight, and the compiler's merged wait state would then
-        // drain every load each iteration).  Loads past the last step re-read
-        // the last step.  sched_barrier keeps each load where it is written
-        // (the scheduler otherwise sinks loads into the reduction before them).
+        // drain every load each iteration).  In a group, step s + i is reduced
+        // from set i after the load of step s + i + D - 1 into the set freed
+        // last.  Loads past the last step re-read the last step.
+        // sched_barrier keeps each load where it is written (the scheduler
+        // otherwise sinks loads into the reduction before them).
         __builtin_amdgcn_sched_barrier(0);
         int s = s_begin;
-        for (int q = 0; q < (n >> 2); ++q, s += 4) {
-            S3 = load(at(s + 3));
-            __builtin_amdgcn_sched_barrier(0);
-            reduce(s, S0);
-            S0 = load(at(s + 4));
-            __builtin_amdgcn_sched_barrier(0);
-            reduce(s + 1, S1);
-            S1 = load(at(s + 5));
-            __builtin_amdgcn_sched_barrier(0);
-            reduce(s + 2, S2);
-            S2 = load(at(s + 6));
-            __builtin_amdgcn_sched_barrier(0);
-            reduce(s + 3, S3);
+        for (int q = 0; q < n / D; ++q, s += D) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                S[(i + D - 1) % D] = load(at(s + i + D - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                reduce(s + i, S[i]);
+            }
         }
-        // the n % 4 remaining steps are s, s+1, s+2, held in S0, S1, S2
-        if (n & 3) reduce(s, S0);
-        if ((n & 3) > 1) reduce(s + 1, S1);
-        if ((n & 3) > 2) reduce(s + 2, S2);
+        // the n % D remaining steps s, s+1, ... are held in S[0], S[1], ...
+#pragma unroll
+        for (int i = 0; i < D - 1; ++i)
+            if (i < n % D) reduce(s + i, S[i]);
     }
     if (tail > 0 && active && ro < tail) {  // the last block's partial step
         const long r = static_cast<long>(nfull) * RS + ro;
@@ -724,7 +771,7 @@ void launch_stream(const Weights& wt, Act act, Sink sink, hipStream_t stream) {
         const size_t lds = static_cast<size_t>(fixed + ((steps_per_block + 2) * RS + 8) * 4);
         Weights part{wt.meta + r0 * wt.ms, wt.values + r0 * wt.vs, static_cast<int>(n), wt.cols,
                      wt.ms, wt.vs};
-        hipLaunchKernelGGL((gemv_stream_kernel<Act, Sink>), dim3(static_cast<int>(grid)),
+        hipLaunchKernelGGL((gemv_stream_kernel<Act, Sink, kStreamDepth>), dim3(static_cast<int>(grid)),
                            dim3(kBlock), lds, stream, part, act, sink, static_cast<int>(nfull),
                            static_cast<int>(r0));
         r0 += n;

@@ -251,6 +251,21 @@ struct HeldWeights {
             load_f8(w + 8 * (u < units ? u : units - 1), f[k]);
         }
     }
+    // the same on a vector held in registers (unit tid + k * T in v[k])
+    __device__ float scale_regs(float (&v)[kUnits][8], float inv, int units, int tid) const {
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            if (tid + k * T < units) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    v[k][e] = bf16r((v[k][e] * inv) * f[k][e]);
+                    m = __builtin_fmaxf(m, __builtin_fabsf(v[k][e]));
+                }
+            }
+        }
+        return m;
+    }
     template <bool kOne>
     __device__ float apply(float* vec, const float* w, float inv, int units, int tid) const {
         if constexpr (!kOne) {
@@ -367,10 +382,25 @@ struct ProducerPlanes {
         float* vec = scratch;
         float* aux = scratch + cols;
         float* red = scratch + cols * (1 + P::kAux);
-        const float m = p.template fill<kOne>(vec, aux, cols, tid, red, st, r);
-        amax = block_max<kBlock>(m, red + 2 * kRedSlot);  // its barrier also orders vec
-        BuildPlanes<LdsQuantSrc>{LdsQuantSrc{vec, quant_scale(amax)}}.build(planes, cols, tid,
-                                                                            nullptr);
+        if constexpr (kOne) {
+            // one pass: the vector stays in registers (unit tid + k * kBlock in
+            // v[k]) and each thread stores its own units' planes
+            float v[kUnits][8];
+            const float m = p.fill_one(v, tid, red, st, r);
+            amax = block_max<kBlock>(m, red + 2 * kRedSlot);
+            const float scale = quant_scale(amax);
+            const int units = cols >> 3, nw = cols >> 5;
+#pragma unroll
+            for (int k = 0; k < kUnits; ++k) {
+                const int u = tid + k * kBlock;
+                if (u < units) store_unit_planes(planes, nw, u, v[k], scale);  // whole quads
+            }
+        } else {
+            const float m = p.template fill<false>(vec, aux, cols, tid, red, st, r);
+            amax = block_max<kBlock>(m, red + 2 * kRedSlot);  // its barrier also orders vec
+            BuildPlanes<LdsQuantSrc>{LdsQuantSrc{vec, quant_scale(amax)}}.build(planes, cols, tid,
+                                                                                nullptr);
+        }
     }
     __device__ float absmax() const { return amax; }
 };
@@ -404,6 +434,25 @@ struct InputNorm {
             r.src, vec, n >> 3, tid, embed && blockIdx.x == 0 ? x_out : nullptr, r.hx);
         const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
         return r.hw.template apply<kOne>(vec, w, inv, n >> 3, tid);
+    }
+    // one pass, in registers (the order of fill_pass)
+    __device__ float fill_one(float (&v)[kUnits][8], int tid, float* red, const EngineState*,
+                              Regs& r) const {
+        const int units = n >> 3;
+        uint16_t* copy = embed && blockIdx.x == 0 ? x_out : nullptr;
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = tid + k * kBlock;
+            if (u < units) {
+                unpack_bf16x8(r.hx.r[k], v[k]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[k][e], v[k][e], ss);
+                if (copy) reinterpret_cast<uint4*>(copy)[u] = r.hx.r[k];
+            }
+        }
+        const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
+        return r.hw.scale_regs(v, inv, units, tid);
     }
     bool one_pass() const { return (n >> 3) <= kUnits * kBlock; }
     template <bool kOne>
@@ -453,8 +502,9 @@ struct AttnCombine {
         const int h = (8 * u) / hd;
         load_batch(h, 8 * u - h * hd, 0, r.b0);
     }
-    // unit u over splits 0 .. ns-1, batch 0 from held when non-null
-    __device__ float combine(float* vec, int u, int ns, const Batch* held) const {
+    // unit u over splits 0 .. ns-1 (batch 0 from held when non-null) into a;
+    // returns max |a|
+    __device__ float combine(float (&a)[8], int u, int ns, const Batch* held) const {
         const int h = (8 * u) / hd, d0 = 8 * u - h * hd;
         Batch b0;
         if (held)
@@ -469,7 +519,9 @@ struct AttnCombine {
             for (int k = 0; k < kBatch; ++k)
                 M = __builtin_fmaxf(M, s0 + k < ns ? pm[h * S + s0 + k] : -INFINITY);
         }
-        float l = 0.0f, a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float l = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = 0.0f;
         auto accumulate = [&](const Batch& b, int s0) {
 #pragma unroll
             for (int k = 0; k < kBatch; ++k) {
@@ -493,8 +545,20 @@ struct AttnCombine {
             a[e] = bf16r(a[e] / l);
             mx = __builtin_fmaxf(mx, __builtin_fabsf(a[e]));
         }
+        return mx;
+    }
+    __device__ float combine_to(float* vec, int u, int ns, const Batch* held) const {
+        float a[8];
+        const float mx = combine(a, u, ns, held);
         store_f8(vec + 8 * u, a);
         return mx;
+    }
+    // one pass (a unit per thread), in registers
+    __device__ float fill_one(float (&v)[kUnits][8], int tid, float*, const EngineState*,
+                              Regs& r) const {
+        int ns = opaque(r.pos) / chunk + 1;  // opaque: as in fill
+        ns = ns < S ? ns : S;
+        return tid < (n >> 3) ? combine(v[0], tid, ns, &r.b0) : 0.0f;
     }
     template <bool kOne>
     __device__ float fill(float* vec, float*, int, int tid, float*, const EngineState*,
@@ -504,10 +568,10 @@ struct AttnCombine {
         // for it ahead of the GEMV's weight loads)
         int ns = opaque(r.pos) / chunk + 1;  // splits holding positions 0..pos
         ns = ns < S ? ns : S;
-        if constexpr (kOne) return tid < (n >> 3) ? combine(vec, tid, ns, &r.b0) : 0.0f;
-        float mx = combine(vec, tid, ns, &r.b0);  // more units than threads
+        if constexpr (kOne) return tid < (n >> 3) ? combine_to(vec, tid, ns, &r.b0) : 0.0f;
+        float mx = combine_to(vec, tid, ns, &r.b0);  // more units than threads
         for (int u = tid + kBlock; u < (n >> 3); u += kBlock)
-            mx = __builtin_fmaxf(mx, combine(vec, u, ns, nullptr));
+            mx = __builtin_fmaxf(mx, combine_to(vec, u, ns, nullptr));
         return mx;
     }
 };
@@ -534,6 +598,48 @@ struct SubNormResidualNorm {
         r.hr.load(res, units, tid);
         r.hs.load(w_sub ? w_sub : w_post, units, tid);  // unconditional (dropped when absent)
         r.hp.load(w_post, units, tid);
+    }
+    // one pass, in registers (the order of fill_pass)
+    __device__ float fill_one(float (&v)[kUnits][8], int tid, float* red, const EngineState*,
+                              Regs& r) const {
+        const int units = n >> 3;
+        float g[kUnits][8];
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            if (tid + k * kBlock < units) {
+                unpack_bf16x8(r.ho.r[k], v[k]);
+                unpack_bf16x8(r.hr.r[k], g[k]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[k][e], v[k][e], ss);
+            }
+        }
+        const float inv = w_sub ? inv_rms(block_sum<kBlock>(ss, red), n, eps) : 1.0f;
+        float ss2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            const int u = tid + k * kBlock;
+            if (u < units) {
+                uint32_t packed[4];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float f = v[k][e];
+                    if (w_sub) f = bf16r((f * inv) * r.hs.f[k][e]);
+                    f = bf16r(f + g[k][e]);
+                    ss2 = __builtin_fmaf(f, f, ss2);
+                    v[k][e] = f;
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    packed[q] = static_cast<uint32_t>(BF16::from_float(v[k][2 * q])) |
+                                (static_cast<uint32_t>(BF16::from_float(v[k][2 * q + 1])) << 16);
+                if (blockIdx.x == 0)
+                    reinterpret_cast<uint4*>(x_out)[u] =
+                        make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            }
+        }
+        const float inv2 = inv_rms(block_sum<kBlock>(ss2, red + kRedSlot), n, eps);
+        return r.hp.scale_regs(v, inv2, units, tid);
     }
     bool one_pass() const { return (n >> 3) <= kUnits * kBlock; }
     template <bool kOne>
@@ -635,6 +741,34 @@ struct Relu2Norm {
         r.hg.load(g, units, tid);
         r.hu.load(u, units, tid);
         r.hw.load(w_load, units, tid);  // unconditional (dropped when w is absent)
+    }
+    // one pass, in registers (the order of fill_pass)
+    __device__ float fill_one(float (&v)[kUnits][8], int tid, float* red, const EngineState*,
+                              Regs& r) const {
+        const int units = n >> 3;
+        float ss = 0.0f, mx = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k) {
+            if (tid + k * kBlock < units) {
+                float fg[8], fu[8];
+                unpack_bf16x8(r.hg.r[k], fg);
+                unpack_bf16x8(r.hu.r[k], fu);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float rl = __builtin_fmaxf(0.0f, fg[e]);
+                    float m = (rl * rl) * fu[e];
+                    ss = __builtin_fmaf(m, m, ss);
+                    if (!w) {  // no sub-norm: plain rounding
+                        m = bf16r(m);
+                        mx = __builtin_fmaxf(mx, __builtin_fabsf(m));
+                    }
+                    v[k][e] = m;
+                }
+            }
+        }
+        if (!w) return mx;
+        const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
+        return r.hw.scale_regs(v, inv, units, tid);
     }
     bool one_pass() const { return (n >> 3) <= kUnits * kBlock; }
     template <bool kOne>
