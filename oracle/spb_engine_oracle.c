@@ -16,8 +16,10 @@
  *     t, t+T, ... (fma(v, v, acc) for sums of squares, element order inside
  *     a unit), then per 64-thread wave the pairwise tree over adjacent
  *     lanes, then the wave totals in wave order;
- *   attention scores: fma over d ascending; softmax sums: the 64-lane tree
- *     over the positions of a split;
+ *   attention scores: four fma chains, one per quarter of the head dim
+ *     (d ascending inside a quarter), combined as (a0 + a1) + (a2 + a3), then
+ *     times the scale; softmax sums: the 64-lane tree over the positions of a
+ *     split;
  *   LM head: lane l accumulates the 8-element chunks l, l+64, ... with fma in
  *     element order, then the 64-lane tree;
  *   1/sqrt with correctly rounded divide and sqrt (reference: rsqrtf);
@@ -291,9 +293,12 @@ static void attention(spbo_engine* e, int l) {
             for (int jj = 0; jj < jn; ++jj) {
                 const uint16_t* kj = kc + (size_t)(j0 + jj) * hd;
                 for (int g = 0; g < G; ++g) {
-                    float a = 0.0f;
-                    for (int d = 0; d < hd; ++d) a = fmaf(qs[g][d], bf2f(kj[d]), a);
-                    sc[g][jj] = a * scale;
+                    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int d = 0; d < hd; ++d) {
+                        const int k = d / (hd / 4);
+                        a[k] = fmaf(qs[g][d], bf2f(kj[d]), a[k]);
+                    }
+                    sc[g][jj] = ((a[0] + a[1]) + (a[2] + a[3])) * scale;
                 }
             }
             for (int g = 0; g < G; ++g) {

@@ -966,45 +966,53 @@ struct SinkPairs<QkvRopeSink> {
 // holds k and v at pos (both written by the qkv projection's epilogue), so
 // every load is issued at kernel start; rows past pos are loaded too (the
 // cache is allocated to max_seq) and masked.
-//   * scores: thread t takes the (position, head) pairs t, t + 256, ... with
-//     position = pair / G and head = pair % G, so the G lanes of one position
-//     share one K-row load and a wave reads 64 / G rows; q of the group is in
-//     LDS (float), the K row in registers.
+//   * scores: thread t takes quarter qq = t % 4 of the head dim of q head
+//     g = (t / 4) / (64 / G) and the G positions ((t / 4) % (64 / G)) * G + i,
+//     so it reads one quarter of one q head from LDS (LDS return bandwidth is
+//     what bounds a full head per thread) and G quarter K rows from global;
+//     the 4 quarter sums of a (head, position) meet in the 4 lanes of a quad
+//     (two DPP adds).
 //   * V rows of the split stay bf16 in LDS; a PV thread owns dims (d, d+1)
-//     of one head and reads both with one 32-bit LDS load.
-//   score_j = (sum over d ascending of fma(q[d], k_j[d], .)) * scale
+//     of one head and reads both with one 32-bit LDS load, and 4 positions'
+//     weights with one 16-byte load.
+//   score_j = ((a0 + a1) + (a2 + a3)) * scale, a_k = fma over the d of
+//     quarter k (ascending) of q[d] * k_j[d]
 //   per head: m = max_j score_j, e_j = exp(score_j - m),
 //   l = tree sum of e over the 64 lanes (lane = position in the split),
 //   acc[d] = sum_j e_j v_j[d] (j ascending, fma).
 // Reference: attention_scores, softmax, attention_output
 // (inference_kernels.cu:241-371), GQA kv = h * nkv / nh.
-template <int HD>
+template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, float* __restrict__ pm, float* __restrict__ pl,
-    float* __restrict__ pacc, const EngineState* __restrict__ st, int nh, int nkv, int max_seq,
-    int S, float scale) {
-    constexpr int kU = HD / 8;
+    float* __restrict__ pacc, const EngineState* __restrict__ st, int max_seq, int S,
+    float scale) {
+    constexpr int kU = HD / 8;       // 16-byte units per row
+    constexpr int kQU = kU / 4;      // units per quarter row
+    constexpr int kPG = kAttnSplit / G;  // position groups per head
     constexpr int kVRow = HD / 2 + 1;  // 32-bit words per bf16 V row in LDS (+1: no bank conflicts)
-    __shared__ __align__(16) float qs[kAttnMaxGroup][HD];
+    static_assert(kAttnThreads == 4 * kAttnSplit && kAttnSplit % G == 0, "4 quarters x 64 slots");
+    __shared__ __align__(16) float qs[G][HD];
     __shared__ uint32_t vs[kAttnSplit][kVRow];
-    __shared__ float sc[kAttnMaxGroup][kAttnSplit];
-    __shared__ float hmax[kAttnMaxGroup], hsum[kAttnMaxGroup];
+    __shared__ __align__(16) float sc[G][kAttnSplit];
+    __shared__ float hmax[G], hsum[G];
     const int s = blockIdx.x, kvh = blockIdx.y;
     const int j0 = s * kAttnSplit;
-    const int G = nh / nkv;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const long cache0 = static_cast<long>(kvh) * max_seq * HD;
     const int jmax = max_seq - 1;
-    const int npairs = kAttnSplit * G;
-    // K rows of this thread's first pair (positions clamped to the cache)
-    const int p0 = tid / G;
-    uint4 kraw[kU];
-    {
-        const int j = j0 + p0 <= jmax ? j0 + p0 : jmax;
-        const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD);
+    // the thread's quarter K rows (positions clamped to the cache)
+    const int qq = tid & 3, slot = tid >> 2;
+    const int sg = slot / kPG, pb = (slot - sg * kPG) * G;
+    uint4 kq[G][kQU];
 #pragma unroll
-        for (int c = 0; c < kU; ++c) kraw[c] = tid < npairs ? kr[c] : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < G; ++i) {
+        const int j = j0 + pb + i <= jmax ? j0 + pb + i : jmax;
+        const uint4* kr =
+            reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) + qq * kQU;
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) kq[i][u] = kr[u];
     }
     // V rows of the split: kVPer 16-byte units per thread, all loads issued
     // before the first LDS store
@@ -1041,25 +1049,31 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
     __syncthreads();
 
-    // scores
-    for (int pr = tid, first = 1; pr < npairs; pr += kAttnThreads, first = 0) {
-        const int p = pr / G, g = pr - p * G;
-        if (!first) {  // G > 4: a later pass loads its own rows
-            const int j = j0 + p <= jmax ? j0 + p : jmax;
-            const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD);
+    // scores (every lane active: the quads combine through DPP)
+    {
+        float qv[HD / 4];
 #pragma unroll
-            for (int c = 0; c < kU; ++c) kraw[c] = kr[c];
+        for (int u = 0; u < HD / 16; ++u) {
+            const float4 t = *reinterpret_cast<const float4*>(&qs[sg][qq * (HD / 4) + 4 * u]);
+            qv[4 * u] = t.x;
+            qv[4 * u + 1] = t.y;
+            qv[4 * u + 2] = t.z;
+            qv[4 * u + 3] = t.w;
         }
-        if (p < jn) {
-            float acc = 0.0f;
 #pragma unroll
-            for (int c = 0; c < kU; ++c) {
+        for (int i = 0; i < G; ++i) {
+            float a = 0.0f;
+#pragma unroll
+            for (int u = 0; u < kQU; ++u) {
                 float f[8];
-                unpack_bf16x8(kraw[c], f);
+                unpack_bf16x8(kq[i][u], f);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qs[g][8 * c + e], f[e], acc);
+                for (int e = 0; e < 8; ++e) a = __builtin_fmaf(qv[8 * u + e], f[e], a);
             }
-            sc[g][p] = acc * scale;
+            a += dpp_f<0xB1>(a);  // quad_perm [1,0,3,2]: a0 + a1, a2 + a3
+            a += dpp_f<0x4E>(a);  // quad_perm [2,3,0,1]: (a0 + a1) + (a2 + a3)
+            const int p = pb + i;
+            if (qq == 0 && p < jn) sc[sg][p] = a * scale;
         }
     }
     __syncthreads();
@@ -1078,12 +1092,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     for (int o = tid; o < G * (HD / 2); o += kAttnThreads) {
         const int g = o / (HD / 2), dp = o - g * (HD / 2);
         float a0 = 0.0f, a1 = 0.0f;
-        for (int jj = 0; jj < jn; ++jj) {
+        auto step = [&](int jj, float e) {
             const uint32_t w = vs[jj][dp];
-            const float e = sc[g][jj];
             a0 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w & 0xFFFFu)), a0);
             a1 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w >> 16)), a1);
+        };
+        const int n4 = jn >> 2;
+        for (int q = 0; q < n4; ++q) {
+            const float4 e = *reinterpret_cast<const float4*>(&sc[g][4 * q]);
+            step(4 * q, e.x);
+            step(4 * q + 1, e.y);
+            step(4 * q + 2, e.z);
+            step(4 * q + 3, e.w);
         }
+        for (int jj = 4 * n4; jj < jn; ++jj) step(jj, sc[g][jj]);
         const int h = kvh * G + g;
         float* out = pacc + (static_cast<long>(h) * S + s) * HD + 2 * dp;
         *reinterpret_cast<float2*>(out) = make_float2(a0, a1);
@@ -1466,6 +1488,29 @@ Weights single_weights(const spb_sparse_linear& l) {
 
 using namespace spb;
 
+// attention_kernel<HD, G> for head_dim 64 / 128 and GQA groups 1, 2, 4, 8
+// (checked at engine creation).
+template <int HD>
+void launch_attention_hd(int G, dim3 grid, hipStream_t s, const uint16_t* qkv,
+                         const uint16_t* kc, const uint16_t* vc, float* pm, float* pl,
+                         float* pacc, const EngineState* st, int max_seq, int S, float scale) {
+    const dim3 block(kAttnThreads);
+    switch (G) {
+    case 1: hipLaunchKernelGGL((attention_kernel<HD, 1>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
+    case 2: hipLaunchKernelGGL((attention_kernel<HD, 2>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
+    case 4: hipLaunchKernelGGL((attention_kernel<HD, 4>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
+    default: hipLaunchKernelGGL((attention_kernel<HD, 8>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
+    }
+}
+void launch_attention(int hd, int G, int S, int nkv, hipStream_t s, const uint16_t* qkv,
+                      const uint16_t* kc, const uint16_t* vc, float* pm, float* pl, float* pacc,
+                      const EngineState* st, int max_seq, float scale) {
+    if (hd == 64)
+        launch_attention_hd<64>(G, dim3(S, nkv), s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
+    else
+        launch_attention_hd<128>(G, dim3(S, nkv), s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
+}
+
 // A projection of the decode step: the span kernel (every weight load issued
 // before the prologue) when each CU's share fits its few steps, else the
 // tiled kernel.
@@ -1542,14 +1587,8 @@ struct spb_engine {
                 launch_projection(seg_weights(&L.q_proj, &L.k_proj, &L.v_proj),
                                 p, st, sink, s);
             }
-            if (hd == 64)
-                hipLaunchKernelGGL(attention_kernel<64>, dim3(S, nkv), dim3(kAttnThreads), 0, s,
-                                   qkv, kcache[l], vcache[l], pm, pl, pacc, st, nh, nkv,
-                                   max_seq, S, scale);
-            else
-                hipLaunchKernelGGL(attention_kernel<128>, dim3(S, nkv), dim3(kAttnThreads), 0, s,
-                                   qkv, kcache[l], vcache[l], pm, pl, pacc, st, nh, nkv,
-                                   max_seq, S, scale);
+            launch_attention(hd, nh / nkv, S, nkv, s, qkv, kcache[l], vcache[l], pm, pl, pacc, st,
+                             max_seq, scale);
             {
                 AttnCombine p{pm, pl, pacc, hd, S, kAttnSplit, nh * hd};
                 SegBf16Sink sink{obuf, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma,
@@ -1632,8 +1671,8 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
         V <= 0)
         return invalid("%s: non-positive model dimension", fn);
     if (nh * hd != H) return invalid("%s: num_attention_heads * head_dim != hidden_size", fn);
-    if (nh % nkv || nh / nkv > kAttnMaxGroup)
-        return invalid("%s: heads per kv head must divide evenly and be <= %d", fn,
+    if (nh % nkv || (nh / nkv) & (nh / nkv - 1) || nh / nkv > kAttnMaxGroup)
+        return invalid("%s: heads per kv head must divide evenly and be 1, 2, 4 or %d", fn,
                        kAttnMaxGroup);
     if (hd != 64 && hd != 128) return invalid("%s: head_dim must be 64 or 128", fn);
     if (H > kLmMaxH || H % 8) return invalid("%s: hidden_size must be a multiple of 8, <= %d", fn,
