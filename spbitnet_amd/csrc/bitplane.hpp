@@ -541,29 +541,34 @@ __global__ __launch_bounds__(kBlock) void gemv_bitplane_kernel(W wt, Act act, Si
 // drop it), so the weight latency overlaps the prologue's instead of
 // following it.  Same per-chunk arithmetic and LDS row sums as
 // gemv_bitplane_kernel, so the results are identical.
+// The row split of a span launch, computed on the host: block b owns
+// base + (b < rem) units (rows, or row pairs for a pair sink) from
+// b * base + min(b, rem), so the kernel divides nothing (a 64-bit division
+// by the grid size is a chain of ~100 dependent scalar instructions ahead of
+// the first load).
+struct SpanSplit {
+    int base, rem;  // units per block, blocks with one more
+    int RS;         // rows per step
+};
+
 template <class W, class Act, class Sink, int MS>
-__global__ __launch_bounds__(kBlock) void gemv_span_kernel(W wt, Act act, Sink sink) {
+__global__ __launch_bounds__(kBlock) void gemv_span_kernel(W wt, Act act, Sink sink, SpanSplit sp) {
     extern __shared__ uint32_t smem[];
     if (act.skip()) return;
     constexpr bool kPairs = SinkPairs<Sink>::value;
     const int nwords = wt.cols >> 5;
-    const int C = wt.cols / kChunk;
-    const int RS = rows_per_step<Sink>(C);
+    const int C = wt.cols >> 7;  // 128-column chunks
+    const int RS = sp.RS;
     uint32_t* planes = smem;  // plane-major: word (b, w) at b * nwords + w
     int* acc = reinterpret_cast<int*>(smem + 8 * nwords);
     const int tid = threadIdx.x;
-    const int c = tid % C;
-    const int ro = tid / C;
-    const long G = gridDim.x, b = blockIdx.x;
-    long start, end;
-    if constexpr (kPairs) {
-        const long pairs = wt.rows >> 1;
-        start = 2 * (b * pairs / G);
-        end = 2 * ((b + 1) * pairs / G);
-    } else {
-        start = b * wt.rows / G;
-        end = (b + 1) * wt.rows / G;
-    }
+    const int ro = static_cast<int>(static_cast<unsigned>(tid) / static_cast<unsigned>(C));
+    const int c = tid - ro * C;
+    const int b = blockIdx.x;
+    const int u0 = b * sp.base + (b < sp.rem ? b : sp.rem);
+    const int nu = sp.base + (b < sp.rem ? 1 : 0);
+    const long start = kPairs ? 2L * u0 : static_cast<long>(u0);
+    const long end = start + (kPairs ? 2L * nu : static_cast<long>(nu));
     const int n = static_cast<int>(end - start);
 
     act.offset(blockIdx.y);
@@ -898,12 +903,13 @@ bool launch_span(const W& wt, Act act, Sink sink, hipStream_t stream) {
     if (ms > kSpanMaxSteps) return false;
     const size_t lds = static_cast<size_t>(wt.cols) + Act::extra_lds(wt.cols) +
                        static_cast<size_t>(ms * RS) * 4 + 16;
+    const SpanSplit sp{static_cast<int>(units / G), static_cast<int>(units % G), static_cast<int>(RS)};
     const dim3 grid(static_cast<unsigned>(G)), block(kBlock);
     switch (ms) {
-    case 1: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 1>), grid, block, lds, stream, wt, act, sink); break;
-    case 2: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 2>), grid, block, lds, stream, wt, act, sink); break;
-    case 3: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 3>), grid, block, lds, stream, wt, act, sink); break;
-    default: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 4>), grid, block, lds, stream, wt, act, sink); break;
+    case 1: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 1>), grid, block, lds, stream, wt, act, sink, sp); break;
+    case 2: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 2>), grid, block, lds, stream, wt, act, sink, sp); break;
+    case 3: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 3>), grid, block, lds, stream, wt, act, sink, sp); break;
+    default: hipLaunchKernelGGL((gemv_span_kernel<W, Act, Sink, 4>), grid, block, lds, stream, wt, act, sink, sp); break;
     }
     return true;
 }

@@ -473,8 +473,9 @@ struct AttnCombine {
     const float* pm;    // [nh][S]
     const float* pl;    // [nh][S]
     const float* pacc;  // [nh][S][hd]
-    int hd, S, chunk;
-    int n;  // nh * hd
+    int hd, S;
+    int n;        // nh * hd
+    int hd_log2;  // head_dim is 64 or 128
     bool one_pass() const { return (n >> 3) <= kBlock; }  // a thread per unit
     struct Batch {
         float pv[kBatch][8], lv[kBatch], mv[kBatch];
@@ -499,13 +500,13 @@ struct AttnCombine {
     __device__ void issue(int tid, const EngineState* st, Regs& r) const {
         r.pos = state_pos(st);
         const int u = tid < (n >> 3) ? tid : (n >> 3) - 1;
-        const int h = (8 * u) / hd;
-        load_batch(h, 8 * u - h * hd, 0, r.b0);
+        const int h = (8 * u) >> hd_log2;
+        load_batch(h, 8 * u - (h << hd_log2), 0, r.b0);
     }
     // unit u over splits 0 .. ns-1 (batch 0 from held when non-null) into a;
     // returns max |a|
     __device__ float combine(float (&a)[8], int u, int ns, const Batch* held) const {
-        const int h = (8 * u) / hd, d0 = 8 * u - h * hd;
+        const int h = (8 * u) >> hd_log2, d0 = 8 * u - (h << hd_log2);
         Batch b0;
         if (held)
             b0 = *held;
@@ -556,7 +557,7 @@ struct AttnCombine {
     // one pass (a unit per thread), in registers
     __device__ float fill_one(float (&v)[kUnits][8], int tid, float*, const EngineState*,
                               Regs& r) const {
-        int ns = opaque(r.pos) / chunk + 1;  // opaque: as in fill
+        int ns = (opaque(r.pos) >> 6) + 1;  // opaque: as in fill
         ns = ns < S ? ns : S;
         return tid < (n >> 3) ? combine(v[0], tid, ns, &r.b0) : 0.0f;
     }
@@ -566,7 +567,7 @@ struct AttnCombine {
         // opaque: pos stays a vector register until here (a scalar copy of a
         // uniform load is otherwise placed right after the load, and waits
         // for it ahead of the GEMV's weight loads)
-        int ns = opaque(r.pos) / chunk + 1;  // splits holding positions 0..pos
+        int ns = (opaque(r.pos) >> 6) + 1;  // splits holding positions 0..pos
         ns = ns < S ? ns : S;
         if constexpr (kOne) return tid < (n >> 3) ? combine_to(vec, tid, ns, &r.b0) : 0.0f;
         float mx = combine_to(vec, tid, ns, &r.b0);  // more units than threads
@@ -1590,7 +1591,8 @@ struct spb_engine {
             launch_attention(hd, nh / nkv, S, nkv, s, qkv, kcache[l], vcache[l], pm, pl, pacc, st,
                              max_seq, scale);
             {
-                AttnCombine p{pm, pl, pacc, hd, S, kAttnSplit, nh * hd};
+                static_assert(kAttnSplit == 64, "the combine's split index is pos >> 6");
+                AttnCombine p{pm, pl, pacc, hd, S, nh * hd, hd == 64 ? 6 : 7};
                 SegBf16Sink sink{obuf, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma,
                                  L.o_proj.rows, L.o_proj.rows, 0.f, 0.f, 0.f};
                 launch_projection(single_weights(L.o_proj), p, st, sink, s);
