@@ -648,16 +648,28 @@ constexpr int kStreamMaxRows = 8192;  // LDS row sums per block (32 KB)
 
 constexpr int kStreamDepth = 4;  // register sets: kStreamDepth - 1 steps in flight
 
+// Host-computed launch constants of the streaming kernel (no division in the
+// kernel: a 64-bit division is a chain of ~100 dependent scalar instructions).
+struct StreamSplit {
+    int nfull;         // full steps of RS rows
+    int base, rem;     // steps per block: base, plus one for blocks b < rem
+    int RS;            // rows per step
+    int cap_m, cap_v;  // 0x7FFFFFFF / (row stride in bytes) of meta and signs
+    int row_base;      // first row of this launch in the output
+};
+
 template <class Act, class Sink, int D>
-__global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act, Sink sink, int nfull, int row_base) {
+__global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act, Sink sink, StreamSplit sp) {
     extern __shared__ uint32_t smem[];
     const int nwords = wt.cols >> 5;
-    const int C = wt.cols / kChunk;
-    const int RS = kBlock / C;  // rows per step
+    const int C = wt.cols >> 7;  // 128-column chunks
+    const int RS = sp.RS;
     const int rows = wt.rows;
+    const int nfull = sp.nfull, row_base = sp.row_base;
     // step indices stay 32-bit (scalar compares; rows < 2^31)
-    const int s_begin = static_cast<int>(static_cast<long>(nfull) * blockIdx.x / gridDim.x);
-    const int s_end = static_cast<int>(static_cast<long>(nfull) * (blockIdx.x + 1) / gridDim.x);
+    const int bi = blockIdx.x;
+    const int s_begin = bi * sp.base + (bi < sp.rem ? bi : sp.rem);
+    const int s_end = s_begin + sp.base + (bi < sp.rem ? 1 : 0);
     const bool last = blockIdx.x == gridDim.x - 1;
     const int tail = last ? rows - nfull * RS : 0;   // rows after the full steps
     const int span = (s_end - s_begin) * RS + tail;  // rows of this block
@@ -666,8 +678,8 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
     const int acc_slots = (span + RS + 3) & ~3;
 
     const int tid = threadIdx.x;
-    const int c = tid % C;
-    const int ro = tid / C;
+    const int ro = static_cast<int>(static_cast<unsigned>(tid) / static_cast<unsigned>(C));
+    const int c = tid - ro * C;
     const bool active = ro < RS;
     // per-thread byte offsets from the step's first row (inactive threads: row 0)
     const int om = active ? (ro * wt.ms + 4 * c) * 4 : 16 * c;
@@ -676,7 +688,7 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
     // Buffer extents in bytes from the step's first row to the matrix end,
     // capped below 2^31 (all scalar 32-bit arithmetic).
     const int ms4 = wt.ms * 4, vs4 = wt.vs * 4;
-    const int cap_m = 0x7FFFFFFF / ms4, cap_v = 0x7FFFFFFF / vs4;
+    const int cap_m = sp.cap_m, cap_v = sp.cap_v;
     auto load = [&](int s) {
         const int ub = s * RS;
         const int left = rows - ub;
@@ -776,9 +788,11 @@ void launch_stream(const Weights& wt, Act act, Sink sink, hipStream_t stream) {
         const size_t lds = static_cast<size_t>(fixed + ((steps_per_block + 2) * RS + 8) * 4);
         Weights part{wt.meta + r0 * wt.ms, wt.values + r0 * wt.vs, static_cast<int>(n), wt.cols,
                      wt.ms, wt.vs};
+        const StreamSplit sp{static_cast<int>(nfull), static_cast<int>(nfull / grid),
+                             static_cast<int>(nfull % grid), static_cast<int>(RS),
+                             0x7FFFFFFF / (wt.ms * 4), 0x7FFFFFFF / (wt.vs * 4), static_cast<int>(r0)};
         hipLaunchKernelGGL((gemv_stream_kernel<Act, Sink, kStreamDepth>), dim3(static_cast<int>(grid)),
-                           dim3(kBlock), lds, stream, part, act, sink, static_cast<int>(nfull),
-                           static_cast<int>(r0));
+                           dim3(kBlock), lds, stream, part, act, sink, sp);
         r0 += n;
     }
 }

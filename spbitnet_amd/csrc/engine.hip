@@ -1139,7 +1139,7 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     const float* __restrict__ wn, float eps, float* __restrict__ logits,
     float* __restrict__ part_v, int* __restrict__ part_i, EngineState* __restrict__ st,
     int* __restrict__ tokens, int V, int H, const float2* __restrict__ rope,
-    float2* __restrict__ cur_rope, int half_hd, int max_seq) {
+    float2* __restrict__ cur_rope, int half_hd, int max_seq, int rbase, int rrem) {
     static_assert(NB == 2 || NB == 3, "two or three row buffers");
     constexpr int kWaves = kLmBlock / kWave;
     __shared__ __align__(16) float xs[kLmMaxH];
@@ -1150,8 +1150,11 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
     __shared__ int last;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int nch = H >> 3;
-    const long b0 = static_cast<long>(V) * blockIdx.x / gridDim.x;
-    const long b1 = static_cast<long>(V) * (blockIdx.x + 1) / gridDim.x;
+    // rows [b0, b1): rbase each, one more for blocks below rrem (host-computed
+    // V / grid and V % grid: no division here)
+    const int blk = blockIdx.x;
+    const long b0 = static_cast<long>(blk) * rbase + (blk < rrem ? blk : rrem);
+    const long b1 = b0 + rbase + (blk < rrem ? 1 : 0);
     const long n = (b1 - b0 - wave + kWaves - 1) / kWaves;  // rows of this wave (may be <= 0)
     const long i_last = n > 0 ? n - 1 : 0;
     auto row_of = [&](long i) { return b0 + wave + (i <= i_last ? i : i_last) * kWaves; };
@@ -1328,7 +1331,8 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
 }
 
 typedef void (*LmKernel)(const uint16_t*, const uint16_t*, const float*, float, float*, float*,
-                         int*, EngineState*, int*, int, int, const float2*, float2*, int, int);
+                         int*, EngineState*, int*, int, int, const float2*, float2*, int, int,
+                         int, int);
 
 // Instantiation for H: NC = ceil(H / 512) chunks per lane (H <= 8192), two
 // row buffers; kFull when H % 512 == 0.
@@ -1618,7 +1622,8 @@ struct spb_engine {
         }
         hipLaunchKernelGGL(lm_kernel, dim3(lm_grid), dim3(kLmBlock), 0, s, lm_head, xa,
                            final_norm, eps, logits, part_v, part_i, st, tokens,
-                           cfg.vocab_size, cfg.hidden_size, rope, cur_rope, hd / 2, max_seq);
+                           cfg.vocab_size, cfg.hidden_size, rope, cur_rope, hd / 2, max_seq,
+                           cfg.vocab_size / lm_grid, cfg.vocab_size % lm_grid);
     }
 };
 
