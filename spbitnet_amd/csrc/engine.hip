@@ -177,11 +177,13 @@ __device__ __forceinline__ float inv_rms(float ss, int n, float eps) {
 // kUnits units before using any of them.  Sums of squares accumulate per
 // thread in unit order (element order inside a unit) with fma, then
 // block_sum: this "unit order" is what the oracle restates.
-// A vector of at most kUnits * T units (every vector of the 2B model) is one
-// pass, loaded whole by issue() ahead of the GEMV's weight loads; the one-pass
-// code (kOne) then issues no global load at all.  A load issued after the
-// weights would make the prologue wait for them too: the memory wait counter
-// retires loads in issue order.
+// A vector of at most KU * T units, KU = 1 or 2 chosen at compile time (every
+// vector of the 2B model), is one pass: issue() loads it whole ahead of the
+// GEMV's weight loads, KU units per thread (no duplicate loads of a unit
+// beyond the vector's end for the threads a second unit would not reach),
+// and the one-pass code then issues no global load at all.  A load issued
+// after the weights would make the prologue wait for them too: the memory
+// wait counter retires loads in issue order.
 
 constexpr int kUnits = 2;  // units per thread per pass
 
@@ -244,18 +246,20 @@ struct HeldWeights {
     float f[kUnits][8];
     // unconditional loads, units past the vector clamped to its last (their
     // values are never used), so the wait counts of the prologue stay exact
+    template <int KU = kUnits>
     __device__ void load(const float* w, int units, int tid) {
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {
+        for (int k = 0; k < KU; ++k) {
             const int u = tid + k * T;
             load_f8(w + 8 * (u < units ? u : units - 1), f[k]);
         }
     }
     // the same on a vector held in registers (unit tid + k * T in v[k])
+    template <int KU>
     __device__ float scale_regs(float (&v)[kUnits][8], float inv, int units, int tid) const {
         float m = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {
+        for (int k = 0; k < KU; ++k) {
             if (tid + k * T < units) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -294,10 +298,11 @@ struct HeldWeights {
 template <int T>
 struct HeldUnits {
     uint4 r[kUnits];
+    template <int KU = kUnits>
     __device__ void load(const uint16_t* src, int units, int tid) {
         const uint4* s4 = reinterpret_cast<const uint4*>(src);
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {  // unconditional, as HeldWeights::load
+        for (int k = 0; k < KU; ++k) {  // unconditional, as HeldWeights::load
             const int u = tid + k * T;
             r[k] = s4[u < units ? u : units - 1];
         }
@@ -365,7 +370,7 @@ constexpr int kRedSlot = 16;  // floats per reduction slot (>= kBlock / 64)
 // values.  The GEMVs run even after the decode state is done (their reads
 // stay in bounds and their outputs are scratch), so no kernel waits on the
 // state before its first loads.
-template <class P, bool kOne>
+template <class P, int KU>
 struct ProducerPlanes {
     P p;
     const EngineState* st;
@@ -375,23 +380,23 @@ struct ProducerPlanes {
     }
     using Regs = typename P::Regs;
     __device__ bool skip() const { return false; }
-    __device__ void issue(int tid, Regs& r) const { p.issue(tid, st, r); }
+    __device__ void issue(int tid, Regs& r) const { p.template issue<KU ? KU : kUnits>(tid, st, r); }
     __device__ void offset(long) {}
     __device__ void prepare() {}
     __device__ void build(uint32_t* planes, int cols, int tid, float* scratch, Regs& r) {
         float* vec = scratch;
         float* aux = scratch + cols;
         float* red = scratch + cols * (1 + P::kAux);
-        if constexpr (kOne) {
+        if constexpr (KU > 0) {
             // one pass: the vector stays in registers (unit tid + k * kBlock in
-            // v[k]) and each thread stores its own units' planes
+            // v[k], k < KU) and each thread stores its own units' planes
             float v[kUnits][8];
-            const float m = p.fill_one(v, tid, red, st, r);
+            const float m = p.template fill_one<KU>(v, tid, red, st, r);
             amax = block_max<kBlock>(m, red + 2 * kRedSlot);
             const float scale = quant_scale(amax);
             const int units = cols >> 3, nw = cols >> 5;
 #pragma unroll
-            for (int k = 0; k < kUnits; ++k) {
+            for (int k = 0; k < KU; ++k) {
                 const int u = tid + k * kBlock;
                 if (u < units) store_unit_planes(planes, nw, u, v[k], scale);  // whole quads
             }
@@ -423,10 +428,11 @@ struct InputNorm {
         HeldUnits<kBlock> hx;
         HeldWeights<kBlock> hw;
     };
+    template <int KU>
     __device__ void issue(int tid, const EngineState* st, Regs& r) const {
         r.src = embed ? embed + static_cast<long>(tokens[st->pos]) * n : x;
-        r.hx.load(r.src, n >> 3, tid);
-        r.hw.load(w, n >> 3, tid);
+        r.hx.template load<KU>(r.src, n >> 3, tid);
+        r.hw.template load<KU>(w, n >> 3, tid);
     }
     template <bool kOne>
     __device__ float fill_pass(float* vec, int tid, float* red, Regs& r) const {
@@ -435,14 +441,15 @@ struct InputNorm {
         const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
         return r.hw.template apply<kOne>(vec, w, inv, n >> 3, tid);
     }
-    // one pass, in registers (the order of fill_pass)
+    // one pass, in registers (the order of fill_pass); KU units per thread
+    template <int KU>
     __device__ float fill_one(float (&v)[kUnits][8], int tid, float* red, const EngineState*,
                               Regs& r) const {
         const int units = n >> 3;
         uint16_t* copy = embed && blockIdx.x == 0 ? x_out : nullptr;
         float ss = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {
+        for (int k = 0; k < KU; ++k) {
             const int u = tid + k * kBlock;
             if (u < units) {
                 unpack_bf16x8(r.hx.r[k], v[k]);
@@ -452,9 +459,13 @@ struct InputNorm {
             }
         }
         const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
-        return r.hw.scale_regs(v, inv, units, tid);
+        return r.hw.template scale_regs<KU>(v, inv, units, tid);
     }
-    bool one_pass() const { return (n >> 3) <= kUnits * kBlock; }
+    // units per thread of the one-pass form (1 or 2), 0 for the general form
+    int units_per_thread() const {
+        const int u = n >> 3;
+        return u <= kBlock ? 1 : (u <= kUnits * kBlock ? 2 : 0);
+    }
     template <bool kOne>
     __device__ float fill(float* vec, float*, int, int tid, float* red, const EngineState*,
                           Regs& r) const {
@@ -476,7 +487,7 @@ struct AttnCombine {
     int hd, S;
     int n;        // nh * hd
     int hd_log2;  // head_dim is 64 or 128
-    bool one_pass() const { return (n >> 3) <= kBlock; }  // a thread per unit
+    int units_per_thread() const { return (n >> 3) <= kBlock ? 1 : 0; }  // a thread per unit
     struct Batch {
         float pv[kBatch][8], lv[kBatch], mv[kBatch];
     };
@@ -497,6 +508,7 @@ struct AttnCombine {
             b.mv[k] = pm[h * S + s];
         }
     }
+    template <int KU>
     __device__ void issue(int tid, const EngineState* st, Regs& r) const {
         r.pos = state_pos(st);
         const int u = tid < (n >> 3) ? tid : (n >> 3) - 1;
@@ -555,6 +567,7 @@ struct AttnCombine {
         return mx;
     }
     // one pass (a unit per thread), in registers
+    template <int KU>
     __device__ float fill_one(float (&v)[kUnits][8], int tid, float*, const EngineState*,
                               Regs& r) const {
         int ns = (opaque(r.pos) >> 6) + 1;  // opaque: as in fill
@@ -593,21 +606,23 @@ struct SubNormResidualNorm {
         HeldUnits<kBlock> ho, hr;
         HeldWeights<kBlock> hs, hp;
     };
+    template <int KU>
     __device__ void issue(int tid, const EngineState*, Regs& r) const {
         const int units = n >> 3;
-        r.ho.load(o, units, tid);
-        r.hr.load(res, units, tid);
-        r.hs.load(w_sub ? w_sub : w_post, units, tid);  // unconditional (dropped when absent)
-        r.hp.load(w_post, units, tid);
+        r.ho.template load<KU>(o, units, tid);
+        r.hr.template load<KU>(res, units, tid);
+        r.hs.template load<KU>(w_sub ? w_sub : w_post, units, tid);  // unconditional (dropped when absent)
+        r.hp.template load<KU>(w_post, units, tid);
     }
-    // one pass, in registers (the order of fill_pass)
+    // one pass, in registers (the order of fill_pass); KU units per thread
+    template <int KU>
     __device__ float fill_one(float (&v)[kUnits][8], int tid, float* red, const EngineState*,
                               Regs& r) const {
         const int units = n >> 3;
         float g[kUnits][8];
         float ss = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {
+        for (int k = 0; k < KU; ++k) {
             if (tid + k * kBlock < units) {
                 unpack_bf16x8(r.ho.r[k], v[k]);
                 unpack_bf16x8(r.hr.r[k], g[k]);
@@ -618,7 +633,7 @@ struct SubNormResidualNorm {
         const float inv = w_sub ? inv_rms(block_sum<kBlock>(ss, red), n, eps) : 1.0f;
         float ss2 = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {
+        for (int k = 0; k < KU; ++k) {
             const int u = tid + k * kBlock;
             if (u < units) {
                 uint32_t packed[4];
@@ -640,9 +655,13 @@ struct SubNormResidualNorm {
             }
         }
         const float inv2 = inv_rms(block_sum<kBlock>(ss2, red + kRedSlot), n, eps);
-        return r.hp.scale_regs(v, inv2, units, tid);
+        return r.hp.template scale_regs<KU>(v, inv2, units, tid);
     }
-    bool one_pass() const { return (n >> 3) <= kUnits * kBlock; }
+    // units per thread of the one-pass form (1 or 2), 0 for the general form
+    int units_per_thread() const {
+        const int u = n >> 3;
+        return u <= kBlock ? 1 : (u <= kUnits * kBlock ? 2 : 0);
+    }
     template <bool kOne>
     __device__ float fill(float* vec, float* aux, int, int tid, float* red, const EngineState*,
                           Regs& r) const {
@@ -737,19 +756,21 @@ struct Relu2Norm {
         HeldUnits<kBlock> hg, hu;
         HeldWeights<kBlock> hw;
     };
+    template <int KU>
     __device__ void issue(int tid, const EngineState*, Regs& r) const {
         const int units = n >> 3;
-        r.hg.load(g, units, tid);
-        r.hu.load(u, units, tid);
-        r.hw.load(w_load, units, tid);  // unconditional (dropped when w is absent)
+        r.hg.template load<KU>(g, units, tid);
+        r.hu.template load<KU>(u, units, tid);
+        r.hw.template load<KU>(w_load, units, tid);  // unconditional (dropped when w is absent)
     }
-    // one pass, in registers (the order of fill_pass)
+    // one pass, in registers (the order of fill_pass); KU units per thread
+    template <int KU>
     __device__ float fill_one(float (&v)[kUnits][8], int tid, float* red, const EngineState*,
                               Regs& r) const {
         const int units = n >> 3;
         float ss = 0.0f, mx = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kUnits; ++k) {
+        for (int k = 0; k < KU; ++k) {
             if (tid + k * kBlock < units) {
                 float fg[8], fu[8];
                 unpack_bf16x8(r.hg.r[k], fg);
@@ -769,9 +790,13 @@ struct Relu2Norm {
         }
         if (!w) return mx;
         const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
-        return r.hw.scale_regs(v, inv, units, tid);
+        return r.hw.template scale_regs<KU>(v, inv, units, tid);
     }
-    bool one_pass() const { return (n >> 3) <= kUnits * kBlock; }
+    // units per thread of the one-pass form (1 or 2), 0 for the general form
+    int units_per_thread() const {
+        const int u = n >> 3;
+        return u <= kBlock ? 1 : (u <= kUnits * kBlock ? 2 : 0);
+    }
     template <bool kOne>
     __device__ float fill(float* vec, float*, int, int tid, float* red, const EngineState*,
                           Regs& r) const {
@@ -1523,13 +1548,15 @@ template <class W, class Act, class Sink>
 void launch_gemv(const W& wt, Act act, Sink sink, hipStream_t s) {
     if (!launch_span(wt, act, sink, s)) launch_bitplane(wt, act, sink, s);
 }
-// The prologue in its one-pass form when the vector fits one pass.
+// The prologue in its one-pass form (one or two units per thread) when the
+// vector fits one pass.
 template <class W, class P, class Sink>
 void launch_projection(const W& wt, const P& p, const EngineState* st, Sink sink, hipStream_t s) {
-    if (p.one_pass())
-        launch_gemv(wt, ProducerPlanes<P, true>{p, st, 0.f}, sink, s);
-    else
-        launch_gemv(wt, ProducerPlanes<P, false>{p, st, 0.f}, sink, s);
+    switch (p.units_per_thread()) {
+    case 1: launch_gemv(wt, ProducerPlanes<P, 1>{p, st, 0.f}, sink, s); break;
+    case 2: launch_gemv(wt, ProducerPlanes<P, 2>{p, st, 0.f}, sink, s); break;
+    default: launch_gemv(wt, ProducerPlanes<P, 0>{p, st, 0.f}, sink, s); break;
+    }
 }
 
 struct spb_engine {
