@@ -72,22 +72,21 @@ def decode_bytes_per_token(cfg) -> int:
     return cfg.num_hidden_layers * per_layer + cfg.vocab_size * H * 2
 
 
-def decode_config3(args, log, ev, stream):
-    """Config 3: bs=1 greedy decode of the BitNet-b1.58-2B-4T shape with
-    random-init weights (generated on the device), prompt = BOS + 32 seeded
-    token ids, then args.decode_tokens greedy steps, all as graph replays of
-    the engine's token step; tokens/s over the decode steps only (the
-    reference's convention, src/main.cpp:175-215)."""
+def _decode_run(log, ev, stream, max_seq, prompt_len, n, seed=2025):
+    """Greedy decode of the BitNet-b1.58-2B-4T shape with random-init weights
+    (generated on the device): reset + prefill of a BOS + (prompt_len - 1)
+    seeded-token prompt, then n greedy steps, all as graph replays of the
+    engine's token step; tokens/s over the decode steps only (the reference's
+    convention, src/main.cpp:175-215)."""
     import numpy as np
     import torch
     from spbitnet_amd.model import InferenceEngine, Model, ModelConfig
     cfg = ModelConfig.bitnet_b158_2b4t()
-    log("decode: generating the random 2.4B-parameter model")
-    model = Model.random(cfg, seed=2025)
-    eng = InferenceEngine(model, max_seq=256)
+    log(f"decode: generating the random 2.4B-parameter model (max_seq {max_seq})")
+    model = Model.random(cfg, seed=seed)
+    eng = InferenceEngine(model, max_seq=max_seq)
     prompt = [cfg.bos_token_id] + [int(t) for t in
-                                   np.random.default_rng(2025).integers(0, cfg.vocab_size, 32)]
-    n = args.decode_tokens
+                                   np.random.default_rng(seed).integers(0, cfg.vocab_size, prompt_len - 1)]
     runs = []
     for _ in range(3):
         eng.generate(prompt, 0, stop_at_eos=False)  # reset + prefill
@@ -105,6 +104,7 @@ def decode_config3(args, log, ev, stream):
     out = {
         "model": "BitNet-b1.58-2B-4T shape, random init (30 layers, hidden 2560, 20/5 heads, "
                  "FFN 6912, vocab 128256, bf16 tied embedding / LM head, bf16 KV cache)",
+        "max_seq": max_seq,
         "prompt_tokens": len(prompt),
         "decode_tokens": n,
         "tok_per_s": round(n / (ms * 1e-3), 1),
@@ -117,11 +117,26 @@ def decode_config3(args, log, ev, stream):
         "greedy_repeatable": toks == again,
         "first_tokens": toks[:8],
     }
-    log(f"decode: {out['tok_per_s']} tok/s")
+    log(f"decode (prompt {len(prompt)}): {out['tok_per_s']} tok/s")
     eng.close()
     del model
     torch.cuda.empty_cache()
     return out
+
+
+def decode_config3(args, log, ev, stream):
+    """Config 3: 33-token prompt (BOS + 32 seeded ids), args.decode_tokens
+    greedy steps."""
+    return _decode_run(log, ev, stream, max_seq=256, prompt_len=33, n=args.decode_tokens)
+
+
+def decode_config4_bs1(args, log, ev, stream):
+    """Config 4 at batch 1: a 2048-token prompt into a 4096-position KV
+    cache, then args.decode_tokens greedy steps (attention over ~2050-2180
+    positions, 33-35 splits).  The engine, like the reference's
+    InferenceEngine::forward, decodes one sequence; batch 8 and 32 are not
+    built."""
+    return _decode_run(log, ev, stream, max_seq=4096, prompt_len=2048, n=args.decode_tokens)
 
 
 def main() -> int:
@@ -137,6 +152,8 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the config-3 end-to-end decode measurement")
     ap.add_argument("--decode-tokens", type=int, default=128)
+    ap.add_argument("--no-long-decode", action="store_true",
+                    help="skip the config-4 (2048-token prompt, 4096 KV) batch-1 decode")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB once (known bytes, for scaling rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE) and exit")
@@ -400,6 +417,8 @@ def main() -> int:
 
     if not args.no_decode:
         detail["decode_config3"] = decode_config3(args, log, ev, stream)
+        if not args.no_long_decode:
+            detail["decode_config4_bs1"] = decode_config4_bs1(args, log, ev, stream)
 
     # ---- CPU baseline: the reference's CPU GEMV on this host, single thread
     cpu = None

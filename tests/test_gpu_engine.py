@@ -92,7 +92,8 @@ def test_engine_greedy_128_matches_oracle(gpu):
 
 
 def test_engine_attention_splits(gpu):
-    """Prompt longer than one 256-position attention split."""
+    """Prompt spanning 10 of the 64-position attention splits (more than the
+    combine's first batch of 4)."""
     cfg = _small_config(num_hidden_layers=1)
     model, eng, ora = _engine_pair(cfg, seed=21, max_seq=700)
     prompt = _prompt(600, cfg.vocab_size, 13)
@@ -102,8 +103,20 @@ def test_engine_attention_splits(gpu):
     eng.close()
 
 
+def test_engine_long_context_4096(gpu):
+    """Config-4 geometry on a one-layer model: a 4096-position KV cache, a
+    2048-token prompt, then greedy steps past position 2048 (33 splits)."""
+    cfg = _small_config(num_hidden_layers=1, max_position_embeddings=4096)
+    model, eng, ora = _engine_pair(cfg, seed=23, max_seq=4096)
+    prompt = _prompt(2048, cfg.vocab_size, 17)
+    print("generate 2048 + 24", flush=True)
+    got = eng.generate(prompt, 24, stop_at_eos=False)
+    assert got == ora.generate(prompt, 24)
+    eng.close()
+
+
 def test_engine_without_sub_norms_and_gqa_variants(gpu):
-    for kw, nkv in [(dict(sub_norms=False), 2), ({}, 8), ({}, 1)]:
+    for kw, nkv in [(dict(sub_norms=False), 2), ({}, 8), ({}, 4), ({}, 1)]:
         cfg = _small_config(num_key_value_heads=nkv)
         print(f"variant {kw} nkv={nkv}", flush=True)
         model, eng, ora = _engine_pair(cfg, seed=31 + nkv, max_seq=96, **kw)
