@@ -12,11 +12,11 @@ streams from HBM) reduced by one launch of the drop-in GEMV entry point
 The JSON line reports
   value      algorithmic GB/s of the step (packed weight bytes + x + y per
              launch, divided by the step time; inputs resident in HBM; the
-             step is replayed from a HIP graph)
+             K timed steps are one HIP graph, replayed once)
   roofline   the streaming GEMV kernel: algorithmic bytes per launch / its
-             average launch duration (HIP events on the launch stream around
-             a graph of 10 back-to-back launches per shape), against the
-             8 TB/s HBM peak
+             average launch duration over the timed region (HIP events on
+             the launch stream around the K-step graph, 2K launches),
+             against the 8 TB/s HBM peak
   cpu_baseline  the reference's CPU GEMV (its own unpack_to_int8 + int32 MAC,
              built from the reference sources into oracle/_ref) on the
              6912x2560 matrix, single thread, on this host
@@ -142,8 +142,10 @@ def decode_config4_bs1(args, log, ev, stream):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--prewarm-ms", type=float, default=30.0,
+                    help="run the step this long before the warmup steps (clock ramp)")
     ap.add_argument("--copies", type=int, default=80, help="distinct weight copies per shape")
     ap.add_argument("--layers", type=int, default=30, help="layers of the decode-shaped step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -249,51 +251,52 @@ def main() -> int:
             return 1
     log("streamed outputs exact")
 
-    # The step is replayed from a HIP graph (captured once: one launch per
-    # shape), so the host's per-launch cost stays out of the GPU timeline.
-    g_step = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g_step):
-        step()
-    for _ in range(args.warmup):
-        g_step.replay()
+    # The GPU's clocks settle only after ~2 ms of sustained load following an
+    # idle period (launches of this step measured 55-64 us at first, then
+    # ~47-51 us), so the step first runs for --prewarm-ms from a one-step
+    # graph.  The W warmup steps and the K timed steps are then each one HIP
+    # graph holding W (K) steps, replayed once: consecutive launches run back
+    # to back as in a decode, without the ~8 us a graph replay adds at its
+    # start, and the host's per-launch cost stays out of the GPU timeline.
+    def step_graph(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(n):
+                step()
+        return g
+
+    g_one = step_graph(1)
+    t_pre = time.perf_counter()
+    while time.perf_counter() - t_pre < args.prewarm_ms * 1e-3:
+        for _ in range(8):
+            g_one.replay()
+        torch.cuda.synchronize()
+    del g_one
+    if args.warmup > 0:
+        g_warm = step_graph(args.warmup)
+        g_warm.replay()
+        del g_warm
+    g_timed = step_graph(args.steps)
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps")
     e0, e1 = ev(), ev()
     e0.record(stream)
-    for _ in range(args.steps):
-        g_step.replay()
+    g_timed.replay()
     e1.record(stream)
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
     value_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
-    del g_step
+    del g_timed
 
-    # Average launch duration of the GEMV kernel: HIP events around a graph of
-    # 10 back-to-back launches of one shape on the launch stream (the events
-    # bracket kernels only; consecutive graph kernels start ~1-2 us apart,
-    # which this average includes).
-    per_shape = {}
-    for item in launches:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(10):
-                launch(item)
-        g.replay()
-        torch.cuda.synchronize()
-        a, b = ev(), ev()
-        a.record(stream)
-        for _ in range(3):
-            g.replay()
-        b.record(stream)
-        torch.cuda.synchronize()
-        per_shape[item[0]] = a.elapsed_time(b) * 1e3 / 30
-        del g
-    avg_us = sum(per_shape.values()) / len(per_shape)
+    # Average launch duration of the GEMV kernel over the timed region: the
+    # events bracket the 2K launches of the timed graph (back to back; the
+    # average includes the ~1 us between consecutive graph kernels).
+    avg_us = ms_per_step * 1e3 / len(launches)
     avg_bytes = step_bytes / len(launches)
     kernel_gbs = avg_bytes / (avg_us * 1e-6) / 1e9
     detail = {
-        "streamed_launch_us": {k: round(v, 2) for k, v in per_shape.items()},
         "copies_per_shape": args.copies,
+        "prewarm_ms": args.prewarm_ms,
     }
     del launches
 

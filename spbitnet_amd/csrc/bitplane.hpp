@@ -20,6 +20,21 @@ constexpr int kChunk = 128;           // columns per thread per row (bit-plane k
 constexpr int kMaxPlaneCols = 32768;  // bit-plane kernel column limit (C <= kBlock/2)
 
 // Work item of one thread: the 128-column chunk c of one row.
+// Weight loads with the non-temporal hint (nt): in a decode step every weight
+// byte is read once.  On MI355X, bs=1 decode of the 2.4B model ran 1090 tok/s
+// with the projections' and the LM head's weight loads non-temporal, against
+// 1026 with ordinary loads (1026 / 1041 with only one of the two).
+typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t nt_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 nt_load(const uint4* p) {
+    const nt_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 nt_load(const uint2* p) {
+    const nt_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x2*>(p));
+    return make_uint2(v.x, v.y);
+}
+
 struct ChunkLoad {
     uint4 k;
     uint2 v;
@@ -58,10 +73,10 @@ struct Weights {
     __device__ ChunkLoad load(long r, int c, bool active) const {
         return chunk_at(meta, values, r, ms, vs, c, active && r < rows);
     }
-    // unconditional load of a row known to be in range
+    // unconditional (non-temporal) load of a row known to be in range
     __device__ ChunkLoad load_in(long r, int c) const {
-        return ChunkLoad{*reinterpret_cast<const uint4*>(meta + r * ms + 4 * c),
-                         *reinterpret_cast<const uint2*>(values + r * vs + 2 * c), true};
+        return ChunkLoad{nt_load(reinterpret_cast<const uint4*>(meta + r * ms + 4 * c)),
+                         nt_load(reinterpret_cast<const uint2*>(values + r * vs + 2 * c)), true};
     }
 };
 
@@ -87,7 +102,7 @@ struct SegWeights {
         const long lr = r - (s1 ? end0 : 0) - (s2 ? end1 - end0 : 0);
         return chunk_at(meta + om, values + ov, lr, sm, sv, c, active && r < rows);
     }
-    // unconditional load of a row known to be in range
+    // unconditional (non-temporal) load of a row known to be in range
     __device__ ChunkLoad load_in(long r, int c) const {
         const bool s1 = r >= end0, s2 = r >= end1;
         const long om = (s1 ? dm1 : 0) + (s2 ? dm2 : 0);
@@ -95,8 +110,8 @@ struct SegWeights {
         const int sm = ms + (s1 ? dms1 : 0) + (s2 ? dms2 : 0);
         const int sv = vs + (s1 ? dvs1 : 0) + (s2 ? dvs2 : 0);
         const long lr = r - (s1 ? end0 : 0) - (s2 ? end1 - end0 : 0);
-        return ChunkLoad{*reinterpret_cast<const uint4*>(meta + om + lr * sm + 4 * c),
-                         *reinterpret_cast<const uint2*>(values + ov + lr * sv + 2 * c), true};
+        return ChunkLoad{nt_load(reinterpret_cast<const uint4*>(meta + om + lr * sm + 4 * c)),
+                         nt_load(reinterpret_cast<const uint2*>(values + ov + lr * sv + 2 * c)), true};
     }
 };
 
@@ -626,8 +641,10 @@ __global__ __launch_bounds__(kBlock) void gemv_span_kernel(W wt, Act act, Sink s
 // block's row sums all live in LDS (integer atomics) and are written once,
 // after the loop.  In the loop a load is a buffer load through a resource
 // whose base is the step's first row (scalar registers) plus the thread's
-// fixed byte offset, with no bounds test (threads beyond RS rows per step
-// read row 0 of the step and drop the sum).  Four register sets rotate, so
+// fixed byte offset, with no bounds test (threads beyond RS rows per step and
+// the pipeline's loads past the block's last step are out of the buffer's
+// range: they return zeros without reading memory, and their sums are
+// dropped).  Four register sets rotate, so
 // three steps are in flight while one is reduced.  The loop body holds only
 // loads, bit arithmetic and LDS atomics (no barrier, no global store, no
 // early exit), which keeps the compiler's wait counts exact: each wait
@@ -639,6 +656,15 @@ struct StreamLoad {
 
 // Buffer resource word 3 for gfx9-family raw (unformatted, stride 0) loads.
 constexpr int kBufferFlags = 0x00020000;
+// Cache policy of the streamed weight loads: nt (non-temporal).  Every weight
+// byte is read once; on MI355X the hint took a cold 265 MB launch with three
+// blocks per CU from ~49.5 to ~46.8 us (it made no difference with one).
+constexpr int kStreamLoadPolicy = 2;
+// Buffer extents are capped at kExtentCap bytes, so an offset of kOutOfRange
+// puts every dword of a 16-byte load out of range (the load returns zeros and
+// reads no memory).
+constexpr int kExtentCap = 0x7FFF0000;
+constexpr int kOutOfRange = 0x7FFFFFF0;
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint4 as_uint4(u32x4_t v) { return make_uint4(v.x, v.y, v.z, v.w); }
@@ -654,7 +680,7 @@ struct StreamSplit {
     int nfull;         // full steps of RS rows
     int base, rem;     // steps per block: base, plus one for blocks b < rem
     int RS;            // rows per step
-    int cap_m, cap_v;  // 0x7FFFFFFF / (row stride in bytes) of meta and signs
+    int cap_m, cap_v;  // kExtentCap / (row stride in bytes) of meta and signs
     int row_base;      // first row of this launch in the output
 };
 
@@ -676,22 +702,29 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
     uint32_t* planes = smem;  // plane-major: word (b, w) at b * nwords + w
     int* acc = reinterpret_cast<int*>(smem + 8 * nwords);
     const int acc_slots = (span + RS + 3) & ~3;
+    const int n = s_end - s_begin;
+    const int s_last = n > 0 ? s_end - 1 : 0;
 
     const int tid = threadIdx.x;
     const int ro = static_cast<int>(static_cast<unsigned>(tid) / static_cast<unsigned>(C));
     const int c = tid - ro * C;
     const bool active = ro < RS;
-    // per-thread byte offsets from the step's first row (inactive threads: row 0)
-    const int om = active ? (ro * wt.ms + 4 * c) * 4 : 16 * c;
-    const int ov = active ? (ro * wt.vs + 2 * c) * 4 : 8 * c;
+    // Per-thread byte offsets from the step's first row.  Inactive threads get
+    // an offset past every buffer extent: their loads return zeros and read
+    // no memory.
+    const int om = active ? (ro * wt.ms + 4 * c) * 4 : kOutOfRange;
+    const int ov = active ? (ro * wt.vs + 2 * c) * 4 : kOutOfRange;
 
     // Buffer extents in bytes from the step's first row to the matrix end,
-    // capped below 2^31 (all scalar 32-bit arithmetic).
+    // capped at kExtentCap (all scalar 32-bit arithmetic).
     const int ms4 = wt.ms * 4, vs4 = wt.vs * 4;
     const int cap_m = sp.cap_m, cap_v = sp.cap_v;
+    // Steps past the block's range (the pipeline's loads beyond its last step)
+    // get an empty extent, so they read no memory either.
     auto load = [&](int s) {
-        const int ub = s * RS;
-        const int left = rows - ub;
+        const bool live = s < s_end;
+        const int ub = (live ? s : s_last) * RS;
+        const int left = live ? rows - ub : 0;
         const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint32_t*>(wt.meta + static_cast<long>(ub) * wt.ms), static_cast<short>(0),
             (left < cap_m ? left : cap_m) * ms4, kBufferFlags);
@@ -699,14 +732,11 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
             const_cast<uint32_t*>(wt.values + static_cast<long>(ub) * wt.vs),
             static_cast<short>(0), (left < cap_v ? left : cap_v) * vs4, kBufferFlags);
         StreamLoad L;
-        L.k = as_uint4(__builtin_amdgcn_raw_buffer_load_b128(rm, om, 0, 0));
-        L.v = as_uint2(__builtin_amdgcn_raw_buffer_load_b64(rv, ov, 0, 0));
+        L.k = as_uint4(__builtin_amdgcn_raw_buffer_load_b128(rm, om, 0, kStreamLoadPolicy));
+        L.v = as_uint2(__builtin_amdgcn_raw_buffer_load_b64(rv, ov, 0, kStreamLoadPolicy));
         return L;
     };
 
-    const int n = s_end - s_begin;
-    const int s_last = n > 0 ? s_end - 1 : 0;
-    auto at = [&](int s) { return s < s_end ? s : s_last; };
 
     // The activation loads go first (they head the prologue's chain), then
     // the first D - 1 steps' weights, which arrive while the prologue runs.
@@ -714,7 +744,7 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
     act.issue(tid, regs);
     StreamLoad S[D];
 #pragma unroll
-    for (int i = 0; i < D - 1; ++i) S[i] = load(at(s_begin + i));
+    for (int i = 0; i < D - 1; ++i) S[i] = load(s_begin + i);
     act.prepare();
     sink.prepare();
     act.build(planes, wt.cols, tid,
@@ -736,7 +766,7 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
         // loads in flight, and the compiler's merged wait state would then
         // drain every load each iteration).  In a group, step s + i is reduced
         // from set i after the load of step s + i + D - 1 into the set freed
-        // last.  Loads past the last step re-read the last step.
+        // last.
         // sched_barrier keeps each load where it is written (the scheduler
         // otherwise sinks loads into the reduction before them).
         __builtin_amdgcn_sched_barrier(0);
@@ -744,7 +774,7 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
         for (int q = 0; q < n / D; ++q, s += D) {
 #pragma unroll
             for (int i = 0; i < D; ++i) {
-                S[(i + D - 1) % D] = load(at(s + i + D - 1));
+                S[(i + D - 1) % D] = load(s + i + D - 1);
                 __builtin_amdgcn_sched_barrier(0);
                 reduce(s + i, S[i]);
             }
@@ -766,31 +796,41 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
         sink.store(static_cast<long>(row_base) + row0 + j, acc[j]);
 }
 
-// Grid: one block per CU, each a contiguous range of steps.  On MI355X a
-// cold 265 MB pass (80 x 6912x2560) ran in ~51 us with one 512-thread block
-// per CU and ~61 / ~65 us with two / three (the register limit), so more
-// resident waves lose to fewer, longer streams.  A matrix whose per-block
-// span would exceed kStreamMaxRows is split into consecutive row ranges, one
-// launch each.
+// Grid: kStreamBlocksPerCU blocks per CU where their LDS fits (fewer
+// otherwise), each a contiguous range of steps.  Three 512-thread blocks are
+// six waves per SIMD, the register limit at 73 VGPRs.  On MI355X, with the
+// clocks settled (after ~2 ms of load) and non-temporal loads, a cold 265 MB
+// pass (80 x 6912x2560 alternating with 80 x 2560x6912) ran ~51 / ~49.3 /
+// ~46.8 us per launch with one / two / three blocks per CU.  A matrix whose
+// per-block span would exceed kStreamMaxRows is split into consecutive row
+// ranges, one launch each.
+constexpr int kStreamBlocksPerCU = 3;
+
 template <class Act, class Sink>
 void launch_stream(const Weights& wt, Act act, Sink sink, hipStream_t stream) {
     const int C = wt.cols / kChunk;
     const long RS = kBlock / C;
     const long cus = device_cu_count();
+    const long lds_cu = device_lds_per_cu();
     const long fixed = static_cast<long>(wt.cols) + static_cast<long>(Act::extra_lds(wt.cols)) + 48;
     const long max_rows = cus * (kStreamMaxRows / RS - 1) * RS;  // <= kStreamMaxRows sums per block
     for (long r0 = 0; r0 < wt.rows;) {
         const long n = wt.rows - r0 < max_rows ? wt.rows - r0 : max_rows;
         const long nfull = n / RS;
-        long grid = nfull < cus ? nfull : cus;
-        if (grid < 1) grid = 1;
-        const long steps_per_block = (nfull + grid - 1) / grid;
-        const size_t lds = static_cast<size_t>(fixed + ((steps_per_block + 2) * RS + 8) * 4);
+        long grid = 1, steps_per_block = 0;
+        size_t lds = 0;
+        for (long per_cu = kStreamBlocksPerCU; per_cu >= 1; --per_cu) {
+            grid = nfull < per_cu * cus ? nfull : per_cu * cus;
+            if (grid < 1) grid = 1;
+            steps_per_block = (nfull + grid - 1) / grid;
+            lds = static_cast<size_t>(fixed + ((steps_per_block + 2) * RS + 8) * 4);
+            if (per_cu == 1 || static_cast<long>(lds) * per_cu <= lds_cu) break;
+        }
         Weights part{wt.meta + r0 * wt.ms, wt.values + r0 * wt.vs, static_cast<int>(n), wt.cols,
                      wt.ms, wt.vs};
         const StreamSplit sp{static_cast<int>(nfull), static_cast<int>(nfull / grid),
                              static_cast<int>(nfull % grid), static_cast<int>(RS),
-                             0x7FFFFFFF / (wt.ms * 4), 0x7FFFFFFF / (wt.vs * 4), static_cast<int>(r0)};
+                             kExtentCap / (wt.ms * 4), kExtentCap / (wt.vs * 4), static_cast<int>(r0)};
         hipLaunchKernelGGL((gemv_stream_kernel<Act, Sink, kStreamDepth>), dim3(static_cast<int>(grid)),
                            dim3(kBlock), lds, stream, part, act, sink, sp);
         r0 += n;

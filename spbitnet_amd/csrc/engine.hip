@@ -1189,10 +1189,10 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
 #pragma unroll
         for (int k = 0; k < NC; ++k) {
             const int c = lane + k * kWave;
-            if (kFull)  // every chunk exists: unconditional loads
-                w[k] = wr[c];
+            if (kFull)  // every chunk exists: unconditional loads (non-temporal)
+                w[k] = nt_load(wr + c);
             else
-                w[k] = c < nch ? wr[c] : make_uint4(0, 0, 0, 0);
+                w[k] = c < nch ? nt_load(wr + c) : make_uint4(0, 0, 0, 0);
         }
     };
     // x and the norm weights first (the prologue waits for them alone), then
@@ -1741,9 +1741,10 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
     e->S = (max_seq + kAttnSplit - 1) / kAttnSplit;
     e->lm_kernel = lm_head_for(H);
     // One block per CU: every block streams a contiguous range of rows.  On
-    // MI355X a cold 657 MB pass ran fastest with one 4-wave block per CU
-    // (~123 us) and slower with 2 or 3 (~133 / ~144 us).  At least V / 2048
-    // blocks (the logits of a block are staged in LDS).
+    // MI355X, with non-temporal weight loads in the projections and here,
+    // decode ran 1090 / 1075 / 1061 tok/s with one / two / three 4-wave LM-head
+    // blocks per CU.  At least V / 2048 blocks (the logits of a block are
+    // staged in LDS).
     const long lm_need = (static_cast<long>(V) + kLmBlock / kWave - 1) / (kLmBlock / kWave);
     const long lm_min = (static_cast<long>(V) + kLmMaxRows - 1) / kLmMaxRows;
     long lm_grid = device_cu_count();
