@@ -491,17 +491,24 @@ struct AttnCombine {
     struct Batch {
         float pv[kBatch][8], lv[kBatch], mv[kBatch];
     };
+    static constexpr int kLongBatch = 8;  // splits per load group past the first batch
+    static constexpr int kMaxGroup = 32;  // split maxima per load group
+    struct LongBatch {
+        float pv[kLongBatch][8], lv[kLongBatch], mv[kLongBatch];
+    };
     // batch 0 of the thread's first unit is loaded before pos is known (ahead
     // of the GEMV's weights)
     struct Regs {
         int pos;
         Batch b0;
     };
-    // splits s0 .. s0 + kBatch - 1 of unit (h, d0); unconditional, splits
-    // clamped to S - 1 (those past pos's are dropped)
-    __device__ void load_batch(int h, int d0, int s0, Batch& b) const {
+    // splits s0 .. s0 + N - 1 of unit (h, d0) (N = kBatch or kLongBatch);
+    // unconditional, splits clamped to S - 1 (those past pos's are dropped)
+    template <class B>
+    __device__ void load_batch(int h, int d0, int s0, B& b) const {
+        constexpr int kN = sizeof(b.lv) / sizeof(float);
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
+        for (int k = 0; k < kN; ++k) {
             const int s = s0 + k < S ? s0 + k : S - 1;
             load_f8(pacc + (static_cast<long>(h) * S + s) * hd + d0, b.pv[k]);
             b.lv[k] = pl[h * S + s];
@@ -527,17 +534,13 @@ struct AttnCombine {
         float M = -INFINITY;
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) M = __builtin_fmaxf(M, k < ns ? b0.mv[k] : -INFINITY);
-        for (int s0 = kBatch; s0 < ns; s0 += kBatch) {
-#pragma unroll
-            for (int k = 0; k < kBatch; ++k)
-                M = __builtin_fmaxf(M, s0 + k < ns ? pm[h * S + s0 + k] : -INFINITY);
-        }
         float l = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[e] = 0.0f;
-        auto accumulate = [&](const Batch& b, int s0) {
+        auto accumulate = [&](const auto& b, int s0) {
+            constexpr int kN = sizeof(b.lv) / sizeof(float);
 #pragma unroll
-            for (int k = 0; k < kBatch; ++k) {
+            for (int k = 0; k < kN; ++k) {
                 if (s0 + k < ns) {
                     const float w = exp_neg(b.mv[k] - M);
                     l = __builtin_fmaf(w, b.lv[k], l);
@@ -546,11 +549,29 @@ struct AttnCombine {
                 }
             }
         };
-        accumulate(b0, 0);
-        for (int s0 = kBatch; s0 < ns; s0 += kBatch) {
-            Batch b;
-            load_batch(h, d0, s0, b);
-            accumulate(b, s0);
+        if (ns <= kBatch) {
+            accumulate(b0, 0);
+        } else {
+            // Splits past the first batch (long contexts): every load of a
+            // group is issued before any of it is used -- kMaxGroup maxima at
+            // a time, then kLongBatch splits' partials at a time, the first
+            // group of those together with the maxima -- so 33 splits cost 5
+            // dependent round trips instead of 16.  Same order of arithmetic.
+            LongBatch b;
+            load_batch(h, d0, kBatch, b);
+            for (int s0 = kBatch; s0 < ns; s0 += kMaxGroup) {
+                float t[kMaxGroup];
+#pragma unroll
+                for (int k = 0; k < kMaxGroup; ++k) t[k] = pm[h * S + (s0 + k < ns ? s0 + k : ns - 1)];
+#pragma unroll
+                for (int k = 0; k < kMaxGroup; ++k) M = __builtin_fmaxf(M, t[k]);
+            }
+            accumulate(b0, 0);
+            accumulate(b, kBatch);
+            for (int s0 = kBatch + kLongBatch; s0 < ns; s0 += kLongBatch) {
+                load_batch(h, d0, s0, b);
+                accumulate(b, s0);
+            }
         }
         float mx = 0.0f;
 #pragma unroll

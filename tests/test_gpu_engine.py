@@ -115,6 +115,21 @@ def test_engine_long_context_4096(gpu):
     eng.close()
 
 
+def test_engine_long_context_gqa_groups(gpu):
+    """Past 4 splits the attention kernel's last split block per kv head
+    combines the splits (atomic ticket): GQA groups 1, 2 and 8 with head_dim
+    64 and group 4 with head_dim 128, greedy steps at positions 300-315
+    (5 splits) against the oracle."""
+    for nh, nkv, hd in [(8, 8, 64), (8, 4, 64), (8, 1, 64), (4, 1, 128)]:
+        cfg = _small_config(num_hidden_layers=1, hidden_size=nh * hd, num_attention_heads=nh,
+                            num_key_value_heads=nkv, head_dim=hd, max_position_embeddings=512)
+        print(f"long context nh={nh} nkv={nkv} hd={hd}", flush=True)
+        model, eng, ora = _engine_pair(cfg, seed=51 + nkv + hd, max_seq=320)
+        prompt = _prompt(300, cfg.vocab_size, nkv + hd)
+        assert eng.generate(prompt, 16, stop_at_eos=False) == ora.generate(prompt, 16)
+        eng.close()
+
+
 def test_engine_without_sub_norms_and_gqa_variants(gpu):
     for kw, nkv in [(dict(sub_norms=False), 2), ({}, 8), ({}, 4), ({}, 1)]:
         cfg = _small_config(num_key_value_heads=nkv)
