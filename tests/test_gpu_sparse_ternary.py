@@ -94,7 +94,8 @@ def test_gemv_config_shapes(gpu, rows, cols):
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 128), (7, 256), (333, 384), (1025, 128), (3, 4),
-                                       (5, 8), (9, 36), (64, 100), (130, 132), (31, 2564)])
+                                       (5, 8), (9, 36), (64, 100), (130, 132), (31, 2564),
+                                       (97, 32768), (1501, 16384), (777, 4992)])
 def test_gemv_odd_shapes(gpu, rows, cols):
     L = W.random_layer(rows, cols, W.seed_for("odd", rows, cols))
     x = np.random.default_rng(rows * 7 + cols).integers(-128, 128, cols).astype(np.int8)
