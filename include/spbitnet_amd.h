@@ -321,6 +321,14 @@ int spb_engine_seq_len(const spb_engine* engine);
  * stop_at_eos.  All steps are graph launches; the host waits once. */
 int spb_engine_generate(spb_engine* engine, const int* prompt, int n_prompt, int n_new,
                         int stop_at_eos, int* out_tokens, int* n_generated);
+/* No reference counterpart (the reference feeds a prompt one token at a
+ * time).  spb_engine_generate prefills a prompt with at least min_tokens
+ * tokens before its last in batches through the layers: per-token
+ * producers and sinks of the decode step around the matrix-core GEMM, and a
+ * prefill form of the attention kernel.  The KV cache and every generated
+ * token are identical to one decode step per prompt token.  0 = always one
+ * step per token; default 16. */
+int spb_engine_set_prefill_batch(spb_engine* engine, int min_tokens);
 /* Launches `steps` more token steps continuing the current state (timing
  * loops); no host synchronisation. */
 int spb_engine_decode_steps(spb_engine* engine, int steps);

@@ -32,6 +32,7 @@
 //
 // Every floating-point reduction has a fixed order (listed at each helper), so
 // the CPU oracle in oracle/ reproduces the logits bit for bit.
+#include <algorithm>
 #include <cmath>
 #include <cstddef>
 #include <new>
@@ -45,6 +46,9 @@ namespace {
 
 constexpr int kAttnSplit = 64;    // positions per attention split (one per lane)
 constexpr int kAttnThreads = 256;
+constexpr int kPrefillChunk = 256;       // prompt tokens per batched-prefill pass (at most)
+constexpr long kPrefillPartialBytes = 256L << 20;  // split partials of one pass (at most)
+constexpr int kPrefillMinDefault = 16;   // prompt tokens before the last that switch to it
 constexpr int kAttnMaxGroup = 8;  // q heads per kv head
 constexpr int kLmBlock = 256;
 constexpr int kLmMaxH = 8192;
@@ -423,6 +427,13 @@ struct InputNorm {
     const float* w;
     float eps;
     int n;
+    int writer = 0;  // the block that stores the residual stream (layer 0)
+    // prefill: token t of a batch (x and x_out rows of `stride` elements)
+    __device__ void at(int t, long stride) {
+        x += t * stride;
+        x_out += t * stride;
+        writer = t;
+    }
     struct Regs {
         const uint16_t* src;
         HeldUnits<kBlock> hx;
@@ -437,7 +448,8 @@ struct InputNorm {
     template <bool kOne>
     __device__ float fill_pass(float* vec, int tid, float* red, Regs& r) const {
         const float ss = load_bf16_sumsq<kBlock, kOne>(
-            r.src, vec, n >> 3, tid, embed && blockIdx.x == 0 ? x_out : nullptr, r.hx);
+            r.src, vec, n >> 3, tid,
+            embed && blockIdx.x == static_cast<unsigned>(writer) ? x_out : nullptr, r.hx);
         const float inv = inv_rms(block_sum<kBlock>(ss, red), n, eps);
         return r.hw.template apply<kOne>(vec, w, inv, n >> 3, tid);
     }
@@ -446,7 +458,7 @@ struct InputNorm {
     __device__ float fill_one(float (&v)[kUnits][8], int tid, float* red, const EngineState*,
                               Regs& r) const {
         const int units = n >> 3;
-        uint16_t* copy = embed && blockIdx.x == 0 ? x_out : nullptr;
+        uint16_t* copy = embed && blockIdx.x == static_cast<unsigned>(writer) ? x_out : nullptr;
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < KU; ++k) {
@@ -487,6 +499,14 @@ struct AttnCombine {
     int hd, S;
     int n;        // nh * hd
     int hd_log2;  // head_dim is 64 or 128
+    // prefill: token t of a batch (the partials of token t follow those of
+    // t - 1: [t][nh][S] and [t][nh][S][hd])
+    __device__ void at(int t, long) {
+        const long hs = static_cast<long>(n >> hd_log2) * S;
+        pm += t * hs;
+        pl += t * hs;
+        pacc += t * hs * hd;
+    }
     int units_per_thread() const { return (n >> 3) <= kBlock ? 1 : 0; }  // a thread per unit
     struct Batch {
         float pv[kBatch][8], lv[kBatch], mv[kBatch];
@@ -604,7 +624,8 @@ struct AttnCombine {
         int ns = (opaque(r.pos) >> 6) + 1;  // splits holding positions 0..pos
         ns = ns < S ? ns : S;
         if constexpr (kOne) return tid < (n >> 3) ? combine_to(vec, tid, ns, &r.b0) : 0.0f;
-        float mx = combine_to(vec, tid, ns, &r.b0);  // more units than threads
+        // more units than threads (decode), or any count (prefill)
+        float mx = tid < (n >> 3) ? combine_to(vec, tid, ns, &r.b0) : 0.0f;
         for (int u = tid + kBlock; u < (n >> 3); u += kBlock)
             mx = __builtin_fmaxf(mx, combine_to(vec, u, ns, nullptr));
         return mx;
@@ -623,6 +644,14 @@ struct SubNormResidualNorm {
     const float* w_post;
     float eps;
     int n;
+    int writer = 0;  // the block that stores the new residual stream
+    // prefill: token t of a batch (rows of `stride` elements)
+    __device__ void at(int t, long stride) {
+        o += t * stride;
+        res += t * stride;
+        x_out += t * stride;
+        writer = t;
+    }
     struct Regs {
         HeldUnits<kBlock> ho, hr;
         HeldWeights<kBlock> hs, hp;
@@ -670,7 +699,7 @@ struct SubNormResidualNorm {
                 for (int q = 0; q < 4; ++q)
                     packed[q] = static_cast<uint32_t>(BF16::from_float(v[k][2 * q])) |
                                 (static_cast<uint32_t>(BF16::from_float(v[k][2 * q + 1])) << 16);
-                if (blockIdx.x == 0)
+                if (blockIdx.x == static_cast<unsigned>(writer))
                     reinterpret_cast<uint4*>(x_out)[u] =
                         make_uint4(packed[0], packed[1], packed[2], packed[3]);
             }
@@ -752,7 +781,7 @@ struct SubNormResidualNorm {
                     packed[q] = static_cast<uint32_t>(BF16::from_float(f[2 * q])) |
                                 (static_cast<uint32_t>(BF16::from_float(f[2 * q + 1])) << 16);
                 store_f8(vec + 8 * u, f);
-                if (blockIdx.x == 0)
+                if (blockIdx.x == static_cast<unsigned>(writer))
                     reinterpret_cast<uint4*>(x_out)[u] =
                         make_uint4(packed[0], packed[1], packed[2], packed[3]);
             }
@@ -773,6 +802,11 @@ struct Relu2Norm {
     const float* w_load;  // w, or any buffer of at least n floats when w is absent
     float eps;
     int n;
+    // prefill: token t of a batch (g and u rows of `stride` elements)
+    __device__ void at(int t, long stride) {
+        g += t * stride;
+        u += t * stride;
+    }
     struct Regs {
         HeldUnits<kBlock> hg, hu;
         HeldWeights<kBlock> hw;
@@ -876,6 +910,7 @@ struct SegBf16Sink {
     float g0, g1, g2;
     int end0, end1;
     float dq0, dq1, dq2;
+    __device__ void at(int t, long stride) { out += t * stride; }
     __device__ void offset(long) {}
     __device__ void prepare() {}
     __device__ void prefetch(long, int, int) {}
@@ -903,6 +938,10 @@ struct ResidualSink {
     float dq;
     long pre_row;
     uint16_t pre_res;
+    __device__ void at(int t, long stride) {
+        x_out += t * stride;
+        res += t * stride;
+    }
     __device__ void offset(long) {}
     __device__ void prepare() {}
     __device__ void prefetch(long row0, int n, int tid) {
@@ -946,6 +985,15 @@ struct QkvRopeSink {
     int pos, live;
     long pre_row;
     float2 pre_cs;
+    const float2* rope_tab;  // prefill: the [max_seq][hd/2] table and the batch's first position
+    int rope_pos0;
+    // prefill: token t of a batch at position rope_pos0 + t (its own state
+    // record; out rows of `stride` elements)
+    __device__ void at(int t, long stride) {
+        out += t * stride;
+        st += t;
+        cur_rope = rope_tab + static_cast<long>(rope_pos0 + t) * (hd >> 1);
+    }
     __device__ void offset(long) {}
     __device__ void prepare() {}
     __device__ int rope_pair(long r) const {  // pair index of q/k row r within its head
@@ -1029,12 +1077,24 @@ struct SinkPairs<QkvRopeSink> {
 //   acc[d] = sum_j e_j v_j[d] (j ascending, fma).
 // Reference: attention_scores, softmax, attention_output
 // (inference_kernels.cu:241-371), GQA kv = h * nkv / nh.
-template <int HD, int G>
+//   Prefill (kPre): blockIdx.z = token t of a batch, at position pos0 + t,
+//   with its q at qkv + t * qkv_stride and its partials after those of
+//   t - 1; blocks of splits past the token's position exit before loading.
+template <int HD, int G, bool kPre = false>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, float* __restrict__ pm, float* __restrict__ pl,
     float* __restrict__ pacc, const EngineState* __restrict__ st, int max_seq, int S,
-    float scale) {
+    float scale, int pos0 = 0, int qkv_stride = 0) {
+    if constexpr (kPre) {
+        const int t = blockIdx.z;
+        if (static_cast<int>(blockIdx.x) * kAttnSplit > pos0 + t) return;
+        qkv += static_cast<long>(t) * qkv_stride;
+        const long hs = static_cast<long>(gridDim.y) * G * S;
+        pm += t * hs;
+        pl += t * hs;
+        pacc += t * hs * HD;
+    }
     constexpr int kU = HD / 8;       // 16-byte units per row
     constexpr int kQU = kU / 4;      // units per quarter row
     constexpr int kPG = kAttnSplit / G;  // position groups per head
@@ -1076,7 +1136,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     uint4 qraw = make_uint4(0, 0, 0, 0);
     const bool has_q = tid < G * kU;
     if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + (kvh * G) * HD)[tid];
-    const int done = state_done(st), pos = state_pos(st);
+    const int done = kPre ? 0 : state_done(st);
+    const int pos = kPre ? pos0 + static_cast<int>(blockIdx.z) : state_pos(st);
 #pragma unroll
     for (int t = 0; t < kVPer; ++t) {
         const int idx = tid + t * kAttnThreads;
@@ -1160,6 +1221,78 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
             pm[h * S + s] = hmax[g];
             pl[h * S + s] = hsum[g];
         }
+    }
+}
+
+// ---- batched prefill ---------------------------------------------------------------------
+//
+// The prompt's tokens (all but the last) go through a layer together: the
+// decode GEMV's producers run per token (one kBlock block per token, their
+// general form) and write int8 activations and their absmax instead of bit
+// planes; the matrix-core GEMM multiplies all tokens' activations at once
+// (exact int32, as the GEMV); the decode GEMV's sinks run per token on the
+// GEMM's rows.  Each token has its own decode-state record (pos = its
+// position), so every per-token value is computed by the same device code,
+// in the same order, as a decode step at that position: the KV cache and the
+// residual stream equal those of one decode step per token, bit for bit.
+
+struct AmaxOf {
+    float m;
+    __device__ float absmax() const { return m; }
+};
+
+template <class P>
+__global__ __launch_bounds__(kBlock) void prefill_producer_kernel(P p, long stride,
+                                                                  const EngineState* st, int cols,
+                                                                  int8_t* __restrict__ xq,
+                                                                  float* __restrict__ amax) {
+    extern __shared__ float sh[];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    p.at(t, stride);
+    st += t;
+    typename P::Regs regs;
+    p.template issue<kUnits>(tid, st, regs);
+    float* vec = sh;
+    float* aux = sh + cols;
+    float* red = sh + static_cast<long>(cols) * (1 + P::kAux);
+    const float m = p.template fill<false>(vec, aux, cols, tid, red, st, regs);
+    const float am = block_max<kBlock>(m, red + 2 * kRedSlot);  // its barrier also orders vec
+    const LdsQuantSrc q{vec, quant_scale(am)};
+    uint32_t* out = reinterpret_cast<uint32_t*>(xq + static_cast<long>(t) * cols);
+    for (int c = tid; c < (cols >> 2); c += kBlock) {
+        const float4 v = *reinterpret_cast<const float4*>(vec + 4 * c);
+        out[c] = q.q8(v.x) | (q.q8(v.y) << 8) | (q.q8(v.z) << 16) | (q.q8(v.w) << 24);
+    }
+    if (tid == 0) amax[t] = am;
+}
+
+// Rows [blockIdx.x * R, +R) of token blockIdx.y (R = kBlock, or 2 * kBlock
+// for a pair sink), from up to three GEMM outputs: row r < end0 of y0, r <
+// end1 of y1 (row r - end0), else y2 (row r - end1); y_k is token-major with
+// rows of ld_k.
+template <class Sink>
+__global__ __launch_bounds__(kBlock) void prefill_sink_kernel(
+    Sink sink, long stride, const float* __restrict__ amax, const int32_t* __restrict__ y0,
+    const int32_t* __restrict__ y1, const int32_t* __restrict__ y2, int end0, int end1, int rows,
+    int ld0, int ld1, int ld2) {
+    constexpr bool kPairs = SinkPairs<Sink>::value;
+    constexpr int R = kPairs ? 2 * kBlock : kBlock;
+    const int t = blockIdx.y, tid = threadIdx.x;
+    const long row0 = static_cast<long>(blockIdx.x) * R;
+    const int n = rows - row0 < R ? static_cast<int>(rows - row0) : R;
+    sink.at(t, stride);
+    sink.prepare();
+    sink.prefetch(row0, n, tid);
+    sink.bind(AmaxOf{amax[t]});
+    auto acc = [&](long r) {
+        return r < end0 ? y0[static_cast<long>(t) * ld0 + r]
+                        : (r < end1 ? y1[static_cast<long>(t) * ld1 + r - end0]
+                                    : y2[static_cast<long>(t) * ld2 + r - end1]);
+    };
+    if constexpr (kPairs) {
+        if (2 * tid < n) sink.store_pair(row0 + 2 * tid, acc(row0 + 2 * tid), acc(row0 + 2 * tid + 1));
+    } else {
+        if (tid < n) sink.store(row0 + tid, acc(row0 + tid));
     }
 }
 
@@ -1553,6 +1686,38 @@ void launch_attention_hd(int G, dim3 grid, hipStream_t s, const uint16_t* qkv,
     default: hipLaunchKernelGGL((attention_kernel<HD, 8>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
     }
 }
+// The prefill form: c tokens at positions pos0 .. pos0 + c - 1 (grid.z).
+template <int HD>
+void launch_attention_prefill_hd(int G, dim3 grid, hipStream_t s, const uint16_t* qkv,
+                                 const uint16_t* kc, const uint16_t* vc, float* pm, float* pl,
+                                 float* pacc, int max_seq, int S, float scale, int pos0,
+                                 int qkv_stride) {
+    const dim3 block(kAttnThreads);
+    switch (G) {
+    case 1: hipLaunchKernelGGL((attention_kernel<HD, 1, true>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, nullptr, max_seq, S, scale, pos0, qkv_stride); break;
+    case 2: hipLaunchKernelGGL((attention_kernel<HD, 2, true>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, nullptr, max_seq, S, scale, pos0, qkv_stride); break;
+    case 4: hipLaunchKernelGGL((attention_kernel<HD, 4, true>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, nullptr, max_seq, S, scale, pos0, qkv_stride); break;
+    default: hipLaunchKernelGGL((attention_kernel<HD, 8, true>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, nullptr, max_seq, S, scale, pos0, qkv_stride); break;
+    }
+}
+
+template <class P>
+void launch_prefill_producer(const P& p, long stride, const EngineState* st, int cols, int c,
+                             int8_t* xq, float* amax, hipStream_t s) {
+    const size_t lds = static_cast<size_t>(cols) * 4 * (1 + P::kAux) + 4 * 3 * kRedSlot;
+    hipLaunchKernelGGL((prefill_producer_kernel<P>), dim3(c), dim3(kBlock), lds, s, p, stride, st,
+                       cols, xq, amax);
+}
+
+template <class Sink>
+void launch_prefill_sink(const Sink& sink, long stride, const float* amax, const int32_t* y0,
+                         const int32_t* y1, const int32_t* y2, int end0, int end1, int rows,
+                         int ld0, int ld1, int ld2, int c, hipStream_t s) {
+    constexpr int R = SinkPairs<Sink>::value ? 2 * kBlock : kBlock;
+    hipLaunchKernelGGL((prefill_sink_kernel<Sink>), dim3((rows + R - 1) / R, c), dim3(kBlock), 0, s,
+                       sink, stride, amax, y0, y1, y2, end0, end1, rows, ld0, ld1, ld2);
+}
+
 void launch_attention(int hd, int G, int S, int nkv, hipStream_t s, const uint16_t* qkv,
                       const uint16_t* kc, const uint16_t* vc, float* pm, float* pl, float* pacc,
                       const EngineState* st, int max_seq, float scale) {
@@ -1604,6 +1769,17 @@ struct spb_engine {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int seq_len = 0;
+    // batched prefill: prompts with at least prefill_min tokens before the
+    // last go through the layers kPrefillChunk tokens at a time (0: never)
+    int prefill_min = kPrefillMinDefault;
+    int8_t* pf_x = nullptr;     // [chunk][max cols] int8 activations
+    float* pf_amax = nullptr;   // [chunk]
+    int32_t* pf_y[3] = {nullptr, nullptr, nullptr};  // [chunk][max rows] GEMM outputs
+    uint16_t *pf_qkv = nullptr, *pf_o = nullptr, *pf_r = nullptr, *pf_r2 = nullptr,
+             *pf_gu = nullptr;
+    float *pf_pm = nullptr, *pf_pl = nullptr, *pf_pacc = nullptr;
+    EngineState* pf_st = nullptr;  // [chunk] one decode-state record per token
+    int pf_chunk = 0;  // tokens per prefill pass
 
     ~spb_engine() {
         if (exec) (void)hipGraphExecDestroy(exec);
@@ -1672,6 +1848,107 @@ struct spb_engine {
                            final_norm, eps, logits, part_v, part_i, st, tokens,
                            cfg.vocab_size, cfg.hidden_size, rope, cur_rope, hd / 2, max_seq,
                            cfg.vocab_size / lm_grid, cfg.vocab_size % lm_grid);
+    }
+
+    // Positions pos0 .. pos0 + c - 1 (tokens[] holds their ids) through every
+    // layer, c <= kPrefillChunk: the KV cache of those positions as c decode
+    // steps would write it.  Returns a HIP error or hipSuccess.
+    hipError_t enqueue_prefill(int pos0, int c, hipStream_t s) {
+        const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
+        const int nkv = cfg.num_key_value_heads, H = cfg.hidden_size;
+        const int I = cfg.intermediate_size, kvdim = nkv * hd, qrows = nh * hd;
+        const float eps = cfg.rms_norm_eps;
+        const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+        std::vector<EngineState> hs(c);
+        for (int t = 0; t < c; ++t) {
+            hs[t] = EngineState{};
+            hs[t].pos = pos0 + t;
+            hs[t].prompt_len = max_seq;
+            hs[t].limit = max_seq;
+        }
+        hipError_t err = hipMemcpyAsync(pf_st, hs.data(), sizeof(EngineState) * c,
+                                        hipMemcpyHostToDevice, s);
+        if (err == hipSuccess) err = hipStreamSynchronize(s);  // hs is on this frame
+        if (err != hipSuccess) return err;
+        auto gemm = [&](const spb_sparse_linear& w, int32_t* y) {
+            return spb_sparse_ternary_gemm(w.meta, w.values, pf_x, y, w.rows, w.cols, c,
+                                           w.meta_stride, w.values_stride, s);
+        };
+        for (size_t l = 0; l < layers.size(); ++l) {
+            const spb_transformer_layer& L = layers[l];
+            {
+                InputNorm p{pf_r, l == 0 ? embed : nullptr, tokens, pf_r, L.input_layernorm, eps,
+                            H};
+                launch_prefill_producer(p, H, pf_st, H, c, pf_x, pf_amax, s);
+            }
+            if (gemm(L.q_proj, pf_y[0]) || gemm(L.k_proj, pf_y[1]) || gemm(L.v_proj, pf_y[2]))
+                return hipErrorLaunchFailure;
+            {
+                QkvRopeSink sink{};
+                sink.out = pf_qkv;
+                sink.kc = kcache[l];
+                sink.vc = vcache[l];
+                sink.st = pf_st;
+                sink.g0 = L.q_proj.gamma;
+                sink.g1 = L.k_proj.gamma;
+                sink.g2 = L.v_proj.gamma;
+                sink.end0 = qrows;
+                sink.end1 = qrows + kvdim;
+                sink.hd = hd;
+                sink.hd_log2 = hd == 64 ? 6 : 7;
+                sink.max_seq = max_seq;
+                sink.rope_tab = rope;
+                sink.rope_pos0 = pos0;
+                launch_prefill_sink(sink, qrows + 2 * kvdim, pf_amax, pf_y[0], pf_y[1], pf_y[2],
+                                    qrows, qrows + kvdim, qrows + 2 * kvdim, qrows, kvdim, kvdim,
+                                    c, s);
+            }
+            if (hd == 64)
+                launch_attention_prefill_hd<64>(nh / nkv, dim3(S, nkv, c), s, pf_qkv, kcache[l],
+                                                vcache[l], pf_pm, pf_pl, pf_pacc, max_seq, S,
+                                                scale, pos0, qrows + 2 * kvdim);
+            else
+                launch_attention_prefill_hd<128>(nh / nkv, dim3(S, nkv, c), s, pf_qkv, kcache[l],
+                                                 vcache[l], pf_pm, pf_pl, pf_pacc, max_seq, S,
+                                                 scale, pos0, qrows + 2 * kvdim);
+            {
+                AttnCombine p{pf_pm, pf_pl, pf_pacc, hd, S, qrows, hd == 64 ? 6 : 7};
+                launch_prefill_producer(p, 0, pf_st, qrows, c, pf_x, pf_amax, s);
+            }
+            if (gemm(L.o_proj, pf_y[0])) return hipErrorLaunchFailure;
+            {
+                SegBf16Sink sink{pf_o, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma, H, H,
+                                 0.f, 0.f, 0.f};
+                launch_prefill_sink(sink, H, pf_amax, pf_y[0], pf_y[0], pf_y[0], H, H, H, H, H,
+                                    H, c, s);
+            }
+            {
+                SubNormResidualNorm p{pf_o, pf_r, pf_r2, L.attn_sub_norm,
+                                      L.post_attention_layernorm, eps, H};
+                launch_prefill_producer(p, H, pf_st, H, c, pf_x, pf_amax, s);
+            }
+            if (gemm(L.gate_proj, pf_y[0]) || gemm(L.up_proj, pf_y[1]))
+                return hipErrorLaunchFailure;
+            {
+                SegBf16Sink sink{pf_gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
+                                 I, 2 * I, 0.f, 0.f, 0.f};
+                launch_prefill_sink(sink, 2 * I, pf_amax, pf_y[0], pf_y[1], pf_y[1], I, 2 * I,
+                                    2 * I, I, I, I, c, s);
+            }
+            {
+                Relu2Norm p{pf_gu, pf_gu + I, L.ffn_sub_norm,
+                            L.ffn_sub_norm ? L.ffn_sub_norm : reinterpret_cast<const float*>(pf_gu),
+                            eps, I};
+                launch_prefill_producer(p, 2 * I, pf_st, I, c, pf_x, pf_amax, s);
+            }
+            if (gemm(L.down_proj, pf_y[0])) return hipErrorLaunchFailure;
+            {
+                ResidualSink sink{pf_r, pf_r2, L.down_proj.gamma, 0.f};
+                launch_prefill_sink(sink, H, pf_amax, pf_y[0], pf_y[0], pf_y[0], H, H, H, H, H,
+                                    H, c, s);
+            }
+        }
+        return hipGetLastError();
     }
 };
 
@@ -1793,6 +2070,31 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
          (e->rope = dev_alloc<float2>(static_cast<size_t>(max_seq) * (hd / 2), own)) &&
          (e->cur_rope = dev_alloc<float2>(hd / 2, own)) &&
          (e->st = dev_alloc<EngineState>(1, own));
+    // batched prefill buffers: pf_chunk tokens per pass, the split partials
+    // capped at kPrefillPartialBytes
+    {
+        const long part = static_cast<long>(nh) * e->S * (hd + 2) * 4;  // bytes per token
+        long c = kPrefillPartialBytes / part;
+        c = c < kPrefillChunk ? c : kPrefillChunk;
+        e->pf_chunk = static_cast<int>(c > 0 ? c : 1);
+        const size_t C = static_cast<size_t>(e->pf_chunk);
+        const size_t xmax = static_cast<size_t>(std::max(std::max(H, I), nh * hd));
+        const size_t ymax = static_cast<size_t>(std::max(std::max(nh * hd, kvdim), std::max(H, I)));
+        ok = ok && (e->pf_x = dev_alloc<int8_t>(C * xmax, own)) &&
+             (e->pf_amax = dev_alloc<float>(C, own)) &&
+             (e->pf_y[0] = dev_alloc<int32_t>(C * ymax, own)) &&
+             (e->pf_y[1] = dev_alloc<int32_t>(C * ymax, own)) &&
+             (e->pf_y[2] = dev_alloc<int32_t>(C * ymax, own)) &&
+             (e->pf_qkv = dev_alloc<uint16_t>(C * (nh * hd + 2 * kvdim), own)) &&
+             (e->pf_o = dev_alloc<uint16_t>(C * H, own)) &&
+             (e->pf_r = dev_alloc<uint16_t>(C * H, own)) &&
+             (e->pf_r2 = dev_alloc<uint16_t>(C * H, own)) &&
+             (e->pf_gu = dev_alloc<uint16_t>(C * 2 * I, own)) &&
+             (e->pf_pm = dev_alloc<float>(C * nh * e->S, own)) &&
+             (e->pf_pl = dev_alloc<float>(C * nh * e->S, own)) &&
+             (e->pf_pacc = dev_alloc<float>(C * nh * e->S * hd, own)) &&
+             (e->pf_st = dev_alloc<EngineState>(C, own));
+    }
     if (!ok) {
         delete e;
         return invalid("%s: device allocation failed", fn);
@@ -1909,8 +2211,20 @@ extern "C" int spb_engine_generate(spb_engine* e, const int* prompt, int n_promp
                        e->stream) != hipSuccess)
         return launch_status(fn);
     if (int rc = set_state(e, 0, n_prompt, stop_at_eos ? 1 : 0)) return rc;
-    // Steps 0 .. n_prompt-2 prefill; step n_prompt-1+t produces token t.
-    const int steps = n_prompt - 1 + n_new;
+    // Positions 0 .. n_prompt-2 prefill (in batches through the layers when
+    // there are at least prefill_min of them, else one decode step each);
+    // step n_prompt-1+t produces token t.
+    int start = 0;
+    const int pre = n_prompt - 1;
+    if (e->prefill_min > 0 && pre >= e->prefill_min) {
+        for (int p0 = 0; p0 < pre; p0 += e->pf_chunk) {
+            const int c = pre - p0 < e->pf_chunk ? pre - p0 : e->pf_chunk;
+            if (e->enqueue_prefill(p0, c, e->stream) != hipSuccess) return launch_status(fn);
+        }
+        if (int rc = set_state(e, pre, n_prompt, stop_at_eos ? 1 : 0)) return rc;
+        start = pre;
+    }
+    const int steps = n_prompt - 1 - start + n_new;
     for (int i = 0; i < steps; ++i)
         if (hipGraphLaunch(e->exec, e->stream) != hipSuccess) return launch_status(fn);
     EngineState h{};
@@ -1923,6 +2237,14 @@ extern "C" int spb_engine_generate(spb_engine* e, const int* prompt, int n_promp
         return launch_status(fn);
     if (n_generated) *n_generated = got;
     e->seq_len = h.pos;
+    return 0;
+}
+
+extern "C" int spb_engine_set_prefill_batch(spb_engine* e, int min_tokens) {
+    clear_error();
+    if (!e) return invalid("spb_engine_set_prefill_batch: null engine");
+    if (min_tokens < 0) return invalid("spb_engine_set_prefill_batch: min_tokens < 0");
+    e->prefill_min = min_tokens;
     return 0;
 }
 

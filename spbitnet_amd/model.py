@@ -469,6 +469,13 @@ class InferenceEngine:
                    "spb_engine_generate")
         return list(out[:got.value])
 
+    def set_prefill_batch(self, min_tokens: int) -> None:
+        """generate() prefills a prompt with at least min_tokens tokens before
+        its last in batches through the layers (matrix-core GEMM; the same KV
+        cache and tokens as one step per token); 0 = one step per token."""
+        _lib.check(self._L.spb_engine_set_prefill_batch(self._h, int(min_tokens)),
+                   "spb_engine_set_prefill_batch")
+
     def decode_steps(self, steps: int) -> None:
         """Enqueue `steps` more greedy steps (no host synchronisation)."""
         _lib.check(self._L.spb_engine_decode_steps(self._h, int(steps)),

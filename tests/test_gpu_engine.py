@@ -22,6 +22,19 @@ def _small_config(**kw):
     return ModelConfig(**base)
 
 
+def _last_logits(eng):
+    """The device logits of the engine's last step (a copy)."""
+    import ctypes
+    from spbitnet_amd import _lib
+    lp = ctypes.c_void_p()
+    _lib.check(eng._L.spb_engine_buffers(eng._h, ctypes.byref(lp), None), "spb_engine_buffers")
+    out = torch.empty(eng._logits.numel(), dtype=torch.float32, device=eng._logits.device)
+    torch.cuda.synchronize()
+    _lib.memcpy_d2d(out.data_ptr(), lp.value, out.numel() * 4, None)
+    torch.cuda.synchronize()
+    return out
+
+
 def _prompt(n, vocab, seed):
     return [int(t) for t in np.random.default_rng(seed).integers(0, vocab, n)]
 
@@ -116,10 +129,9 @@ def test_engine_long_context_4096(gpu):
 
 
 def test_engine_long_context_gqa_groups(gpu):
-    """Past 4 splits the attention kernel's last split block per kv head
-    combines the splits (atomic ticket): GQA groups 1, 2 and 8 with head_dim
-    64 and group 4 with head_dim 128, greedy steps at positions 300-315
-    (5 splits) against the oracle."""
+    """Past 4 splits the o projection's prologue loads the remaining splits in
+    groups: GQA groups 1, 2 and 8 with head_dim 64 and group 4 with head_dim
+    128, greedy steps at positions 300-315 (5 splits) against the oracle."""
     for nh, nkv, hd in [(8, 8, 64), (8, 4, 64), (8, 1, 64), (4, 1, 128)]:
         cfg = _small_config(num_hidden_layers=1, hidden_size=nh * hd, num_attention_heads=nh,
                             num_key_value_heads=nkv, head_dim=hd, max_position_embeddings=512)
@@ -127,6 +139,36 @@ def test_engine_long_context_gqa_groups(gpu):
         model, eng, ora = _engine_pair(cfg, seed=51 + nkv + hd, max_seq=320)
         prompt = _prompt(300, cfg.vocab_size, nkv + hd)
         assert eng.generate(prompt, 16, stop_at_eos=False) == ora.generate(prompt, 16)
+        eng.close()
+
+
+def test_engine_batched_prefill_matches_stepwise(gpu):
+    """Batched prefill (per-token producers and sinks around the matrix-core
+    GEMM, the prefill form of the attention kernel) against one decode step
+    per prompt token on the same engine: the logits of the first generated
+    step are bit-identical and the generated tokens equal; prompts that span
+    several prefill passes and attention splits, GQA groups 4 and 1, with and
+    without sub-norms."""
+    cases = [(dict(), 2, 700, 600), (dict(sub_norms=False), 2, 96, 40), (dict(), 8, 320, 300),
+             (dict(), 1, 64, 17)]
+    for kw, nkv, max_seq, n_prompt in cases:
+        cfg = _small_config(num_key_value_heads=nkv, max_position_embeddings=max(max_seq, 1024))
+        print(f"prefill {kw} nkv={nkv} max_seq={max_seq} prompt={n_prompt}", flush=True)
+        model, eng, ora = _engine_pair(cfg, seed=61 + nkv + n_prompt, max_seq=max_seq, **kw)
+        prompt = _prompt(n_prompt, cfg.vocab_size, 5 + nkv)
+        eng.set_prefill_batch(16)
+        got = eng.generate(prompt, 12, stop_at_eos=False)
+        eng.set_prefill_batch(0)
+        want = eng.generate(prompt, 12, stop_at_eos=False)
+        assert got == want
+        eng.set_prefill_batch(16)
+        eng.generate(prompt, 1, stop_at_eos=False)
+        lb = _last_logits(eng)
+        eng.set_prefill_batch(0)
+        eng.generate(prompt, 1, stop_at_eos=False)
+        ls = _last_logits(eng)
+        assert torch.equal(lb.view(torch.int32), ls.view(torch.int32))
+        assert got == ora.generate(prompt, 12)
         eng.close()
 
 
