@@ -72,12 +72,16 @@ def decode_bytes_per_token(cfg) -> int:
     return cfg.num_hidden_layers * per_layer + cfg.vocab_size * H * 2
 
 
-def _decode_run(log, ev, stream, max_seq, prompt_len, n, seed=2025):
+def _decode_run(log, ev, stream, max_seq, prompt_len, n, seed=2025, stepwise_prefill=False):
     """Greedy decode of the BitNet-b1.58-2B-4T shape with random-init weights
     (generated on the device): reset + prefill of a BOS + (prompt_len - 1)
-    seeded-token prompt, then n greedy steps, all as graph replays of the
-    engine's token step; tokens/s over the decode steps only (the reference's
-    convention, src/main.cpp:175-215)."""
+    seeded-token prompt (batched through the layers: per-token producers and
+    sinks around the matrix-core GEMM), then n greedy steps, all as graph
+    replays of the engine's token step; tokens/s over the decode steps only
+    (the reference's convention, src/main.cpp:175-215).  The prefill's wall
+    time (reset, state upload and the prefill, host clock around a
+    synchronised generate with no new tokens) is reported beside it, and with
+    stepwise_prefill also that of one decode step per prompt token."""
     import numpy as np
     import torch
     from spbitnet_amd.model import InferenceEngine, Model, ModelConfig
@@ -87,10 +91,13 @@ def _decode_run(log, ev, stream, max_seq, prompt_len, n, seed=2025):
     eng = InferenceEngine(model, max_seq=max_seq)
     prompt = [cfg.bos_token_id] + [int(t) for t in
                                    np.random.default_rng(seed).integers(0, cfg.vocab_size, prompt_len - 1)]
-    runs = []
+    runs, pre = [], []
     for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
         eng.generate(prompt, 0, stop_at_eos=False)  # reset + prefill
         torch.cuda.synchronize()
+        pre.append((time.perf_counter() - t0) * 1e3)
         a, b = ev(), ev()
         a.record(stream)
         eng.decode_steps(n)
@@ -98,8 +105,19 @@ def _decode_run(log, ev, stream, max_seq, prompt_len, n, seed=2025):
         torch.cuda.synchronize()
         runs.append(a.elapsed_time(b))
     ms = sorted(runs)[len(runs) // 2]
+    pre_ms = sorted(pre)[len(pre) // 2]
     toks = eng.generate(prompt, n, stop_at_eos=False)
     again = eng.generate(prompt, n, stop_at_eos=False)
+    stepwise = None
+    if stepwise_prefill:
+        eng.set_prefill_batch(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.generate(prompt, 0, stop_at_eos=False)
+        torch.cuda.synchronize()
+        stepwise = (time.perf_counter() - t0) * 1e3
+        same = eng.generate(prompt, n, stop_at_eos=False) == toks
+        eng.set_prefill_batch(16)
     nbytes = decode_bytes_per_token(cfg)
     out = {
         "model": "BitNet-b1.58-2B-4T shape, random init (30 layers, hidden 2560, 20/5 heads, "
@@ -116,7 +134,12 @@ def _decode_run(log, ev, stream, max_seq, prompt_len, n, seed=2025):
         "kernels_per_token": 5 * cfg.num_hidden_layers + 1,
         "greedy_repeatable": toks == again,
         "first_tokens": toks[:8],
+        "prefill_ms": round(pre_ms, 2),
+        "prefill_tok_per_s": round((len(prompt) - 1) / (pre_ms * 1e-3), 1),
     }
+    if stepwise is not None:
+        out["prefill_stepwise_ms"] = round(stepwise, 1)
+        out["stepwise_prefill_same_tokens"] = same
     log(f"decode (prompt {len(prompt)}): {out['tok_per_s']} tok/s")
     eng.close()
     del model
@@ -133,10 +156,11 @@ def decode_config3(args, log, ev, stream):
 def decode_config4_bs1(args, log, ev, stream):
     """Config 4 at batch 1: a 2048-token prompt into a 4096-position KV
     cache, then args.decode_tokens greedy steps (attention over ~2050-2180
-    positions, 33-35 splits).  The engine, like the reference's
-    InferenceEngine::forward, decodes one sequence; batch 8 and 32 are not
-    built."""
-    return _decode_run(log, ev, stream, max_seq=4096, prompt_len=2048, n=args.decode_tokens)
+    positions, 33-35 splits); the prefill also timed as one decode step per
+    prompt token.  The engine, like the reference's InferenceEngine::forward,
+    decodes one sequence; batch 8 and 32 are not built."""
+    return _decode_run(log, ev, stream, max_seq=4096, prompt_len=2048, n=args.decode_tokens,
+                       stepwise_prefill=True)
 
 
 def main() -> int:

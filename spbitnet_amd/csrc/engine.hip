@@ -46,8 +46,8 @@ namespace {
 
 constexpr int kAttnSplit = 64;    // positions per attention split (one per lane)
 constexpr int kAttnThreads = 256;
-constexpr int kPrefillChunk = 256;       // prompt tokens per batched-prefill pass (at most)
-constexpr long kPrefillPartialBytes = 256L << 20;  // split partials of one pass (at most)
+constexpr int kPrefillChunk = 1024;      // prompt tokens per batched-prefill pass (at most)
+constexpr long kPrefillPartialBytes = 1L << 30;  // split partials of one pass (at most)
 constexpr int kPrefillMinDefault = 16;   // prompt tokens before the last that switch to it
 constexpr int kAttnMaxGroup = 8;  // q heads per kv head
 constexpr int kLmBlock = 256;
@@ -1903,12 +1903,14 @@ struct spb_engine {
                                     qrows, qrows + kvdim, qrows + 2 * kvdim, qrows, kvdim, kvdim,
                                     c, s);
             }
+            // splits that some token of the pass reaches
+            const int sp = (pos0 + c - 1) / kAttnSplit + 1 < S ? (pos0 + c - 1) / kAttnSplit + 1 : S;
             if (hd == 64)
-                launch_attention_prefill_hd<64>(nh / nkv, dim3(S, nkv, c), s, pf_qkv, kcache[l],
+                launch_attention_prefill_hd<64>(nh / nkv, dim3(sp, nkv, c), s, pf_qkv, kcache[l],
                                                 vcache[l], pf_pm, pf_pl, pf_pacc, max_seq, S,
                                                 scale, pos0, qrows + 2 * kvdim);
             else
-                launch_attention_prefill_hd<128>(nh / nkv, dim3(S, nkv, c), s, pf_qkv, kcache[l],
+                launch_attention_prefill_hd<128>(nh / nkv, dim3(sp, nkv, c), s, pf_qkv, kcache[l],
                                                  vcache[l], pf_pm, pf_pl, pf_pacc, max_seq, S,
                                                  scale, pos0, qrows + 2 * kvdim);
             {

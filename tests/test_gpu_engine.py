@@ -149,10 +149,12 @@ def test_engine_batched_prefill_matches_stepwise(gpu):
     step are bit-identical and the generated tokens equal; prompts that span
     several prefill passes and attention splits, GQA groups 4 and 1, with and
     without sub-norms."""
-    cases = [(dict(), 2, 700, 600), (dict(sub_norms=False), 2, 96, 40), (dict(), 8, 320, 300),
+    # 2100 tokens: three prefill passes (1024, 1024, 51 tokens) and 33 splits
+    cases = [(dict(), 2, 2200, 2100), (dict(sub_norms=False), 2, 96, 40), (dict(), 8, 320, 300),
              (dict(), 1, 64, 17)]
     for kw, nkv, max_seq, n_prompt in cases:
-        cfg = _small_config(num_key_value_heads=nkv, max_position_embeddings=max(max_seq, 1024))
+        cfg = _small_config(num_key_value_heads=nkv, max_position_embeddings=max(max_seq, 1024),
+                            num_hidden_layers=1 if n_prompt > 1000 else 2)
         print(f"prefill {kw} nkv={nkv} max_seq={max_seq} prompt={n_prompt}", flush=True)
         model, eng, ora = _engine_pair(cfg, seed=61 + nkv + n_prompt, max_seq=max_seq, **kw)
         prompt = _prompt(n_prompt, cfg.vocab_size, 5 + nkv)
