@@ -1077,86 +1077,25 @@ struct SinkPairs<QkvRopeSink> {
 //   acc[d] = sum_j e_j v_j[d] (j ascending, fma).
 // Reference: attention_scores, softmax, attention_output
 // (inference_kernels.cu:241-371), GQA kv = h * nkv / nh.
-//   Prefill (kPre): blockIdx.z = token t of a batch, at position pos0 + t,
-//   with its q at qkv + t * qkv_stride and its partials after those of
-//   t - 1; blocks of splits past the token's position exit before loading.
-template <int HD, int G, bool kPre = false>
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(
-    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, float* __restrict__ pm, float* __restrict__ pl,
-    float* __restrict__ pacc, const EngineState* __restrict__ st, int max_seq, int S,
-    float scale, int pos0 = 0, int qkv_stride = 0) {
-    if constexpr (kPre) {
-        const int t = blockIdx.z;
-        if (static_cast<int>(blockIdx.x) * kAttnSplit > pos0 + t) return;
-        qkv += static_cast<long>(t) * qkv_stride;
-        const long hs = static_cast<long>(gridDim.y) * G * S;
-        pm += t * hs;
-        pl += t * hs;
-        pacc += t * hs * HD;
-    }
-    constexpr int kU = HD / 8;       // 16-byte units per row
-    constexpr int kQU = kU / 4;      // units per quarter row
-    constexpr int kPG = kAttnSplit / G;  // position groups per head
-    constexpr int kVRow = HD / 2 + 1;  // 32-bit words per bf16 V row in LDS (+1: no bank conflicts)
-    static_assert(kAttnThreads == 4 * kAttnSplit && kAttnSplit % G == 0, "4 quarters x 64 slots");
-    __shared__ __align__(16) float qs[G][HD];
-    __shared__ uint32_t vs[kAttnSplit][kVRow];
-    __shared__ __align__(16) float sc[G][kAttnSplit];
-    __shared__ float hmax[G], hsum[G];
-    const int s = blockIdx.x, kvh = blockIdx.y;
-    const int j0 = s * kAttnSplit;
+
+// The per-split work of one query (the decode kernel and the prefill kernel
+// share it): once its q (qs, float) and the split's V rows (vs, bf16) are in
+// LDS behind a barrier and the thread holds its quarter K rows (kq), the
+// scores, the split's softmax and the weighted V sum, stored as the split's
+// partials of heads kvh * G .. kvh * G + G - 1.  jn: positions of the split
+// holding positions 0..pos.  A caller that writes qs again barriers first.
+template <int HD, int G>
+__device__ __forceinline__ void attention_split(const uint4 (&kq)[G][HD / 32], float (&qs)[G][HD],
+                                                uint32_t (&vs)[kAttnSplit][HD / 2 + 1],
+                                                float (&sc)[G][kAttnSplit], float (&hmax)[G],
+                                                float (&hsum)[G], int jn, float scale, int s,
+                                                int kvh, int S, float* __restrict__ pm,
+                                                float* __restrict__ pl, float* __restrict__ pacc) {
+    constexpr int kQU = HD / 32;
+    constexpr int kPG = kAttnSplit / G;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const long cache0 = static_cast<long>(kvh) * max_seq * HD;
-    const int jmax = max_seq - 1;
-    // the thread's quarter K rows (positions clamped to the cache)
     const int qq = tid & 3, slot = tid >> 2;
     const int sg = slot / kPG, pb = (slot - sg * kPG) * G;
-    uint4 kq[G][kQU];
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-        const int j = j0 + pb + i <= jmax ? j0 + pb + i : jmax;
-        const uint4* kr =
-            reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) + qq * kQU;
-#pragma unroll
-        for (int u = 0; u < kQU; ++u) kq[i][u] = kr[u];
-    }
-    // V rows of the split: kVPer 16-byte units per thread, all loads issued
-    // before the first LDS store
-    constexpr int kVPer = kAttnSplit * kU / kAttnThreads;
-    static_assert(kVPer * kAttnThreads == kAttnSplit * kU, "V units per thread");
-    uint4 vraw[kVPer];
-#pragma unroll
-    for (int t = 0; t < kVPer; ++t) {
-        const int idx = tid + t * kAttnThreads;
-        const int jj = idx / kU, c = idx - jj * kU;
-        const int j = j0 + jj <= jmax ? j0 + jj : jmax;
-        vraw[t] = reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
-    }
-    uint4 qraw = make_uint4(0, 0, 0, 0);
-    const bool has_q = tid < G * kU;
-    if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + (kvh * G) * HD)[tid];
-    const int done = kPre ? 0 : state_done(st);
-    const int pos = kPre ? pos0 + static_cast<int>(blockIdx.z) : state_pos(st);
-#pragma unroll
-    for (int t = 0; t < kVPer; ++t) {
-        const int idx = tid + t * kAttnThreads;
-        const int jj = idx / kU, c = idx - jj * kU;
-        uint32_t* row = &vs[jj][4 * c];
-        row[0] = vraw[t].x;
-        row[1] = vraw[t].y;
-        row[2] = vraw[t].z;
-        row[3] = vraw[t].w;
-    }
-    if (has_q) {
-        float f[8];
-        unpack_bf16x8(qraw, f);
-        store_f8(&qs[tid / kU][8 * (tid % kU)], f);
-    }
-    if (done || j0 > pos) return;  // uniform
-    const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
-    __syncthreads();
-
     // scores (every lane active: the quads combine through DPP)
     {
         float qv[HD / 4];
@@ -1221,6 +1160,159 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
             pm[h * S + s] = hmax[g];
             pl[h * S + s] = hsum[g];
         }
+    }
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, float* __restrict__ pm, float* __restrict__ pl,
+    float* __restrict__ pacc, const EngineState* __restrict__ st, int max_seq, int S,
+    float scale) {
+    constexpr int kU = HD / 8;       // 16-byte units per row
+    constexpr int kQU = kU / 4;      // units per quarter row
+    constexpr int kPG = kAttnSplit / G;  // position groups per head
+    constexpr int kVRow = HD / 2 + 1;  // 32-bit words per bf16 V row in LDS (+1: no bank conflicts)
+    static_assert(kAttnThreads == 4 * kAttnSplit && kAttnSplit % G == 0, "4 quarters x 64 slots");
+    __shared__ __align__(16) float qs[G][HD];
+    __shared__ uint32_t vs[kAttnSplit][kVRow];
+    __shared__ __align__(16) float sc[G][kAttnSplit];
+    __shared__ float hmax[G], hsum[G];
+    const int s = blockIdx.x, kvh = blockIdx.y;
+    const int j0 = s * kAttnSplit;
+    const int tid = threadIdx.x;
+    const long cache0 = static_cast<long>(kvh) * max_seq * HD;
+    const int jmax = max_seq - 1;
+    // the thread's quarter K rows (positions clamped to the cache)
+    const int qq = tid & 3, slot = tid >> 2;
+    const int sg = slot / kPG, pb = (slot - sg * kPG) * G;
+    uint4 kq[G][kQU];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const int j = j0 + pb + i <= jmax ? j0 + pb + i : jmax;
+        const uint4* kr =
+            reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) + qq * kQU;
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) kq[i][u] = kr[u];
+    }
+    // V rows of the split: kVPer 16-byte units per thread, all loads issued
+    // before the first LDS store
+    constexpr int kVPer = kAttnSplit * kU / kAttnThreads;
+    static_assert(kVPer * kAttnThreads == kAttnSplit * kU, "V units per thread");
+    uint4 vraw[kVPer];
+#pragma unroll
+    for (int t = 0; t < kVPer; ++t) {
+        const int idx = tid + t * kAttnThreads;
+        const int jj = idx / kU, c = idx - jj * kU;
+        const int j = j0 + jj <= jmax ? j0 + jj : jmax;
+        vraw[t] = reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
+    }
+    uint4 qraw = make_uint4(0, 0, 0, 0);
+    const bool has_q = tid < G * kU;
+    if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + (kvh * G) * HD)[tid];
+    const int done = state_done(st), pos = state_pos(st);
+#pragma unroll
+    for (int t = 0; t < kVPer; ++t) {
+        const int idx = tid + t * kAttnThreads;
+        const int jj = idx / kU, c = idx - jj * kU;
+        uint32_t* row = &vs[jj][4 * c];
+        row[0] = vraw[t].x;
+        row[1] = vraw[t].y;
+        row[2] = vraw[t].z;
+        row[3] = vraw[t].w;
+    }
+    if (has_q) {
+        float f[8];
+        unpack_bf16x8(qraw, f);
+        store_f8(&qs[tid / kU][8 * (tid % kU)], f);
+    }
+    if (done || j0 > pos) return;  // uniform
+    const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
+    __syncthreads();
+
+    attention_split<HD, G>(kq, qs, vs, sc, hmax, hsum, jn, scale, s, kvh, S, pm, pl, pacc);
+}
+
+// Prefill form: the queries of the tokens of a batch (token t at position
+// pos0 + t, its q at qkv + t * qkv_stride, its partials after those of
+// t - 1).  A block (split s, kv head, kQ consecutive tokens) loads the
+// split's K and V once and runs attention_split for each of its tokens whose
+// position reaches the split, the next token's q loaded while the current
+// one is processed.
+template <int HD, int G, int kQ>
+__global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, float* __restrict__ pm, float* __restrict__ pl,
+    float* __restrict__ pacc, int max_seq, int S, float scale, int pos0, int nt,
+    int qkv_stride) {
+    constexpr int kU = HD / 8;
+    constexpr int kQU = kU / 4;
+    constexpr int kPG = kAttnSplit / G;
+    constexpr int kVRow = HD / 2 + 1;
+    __shared__ __align__(16) float qs[G][HD];
+    __shared__ uint32_t vs[kAttnSplit][kVRow];
+    __shared__ __align__(16) float sc[G][kAttnSplit];
+    __shared__ float hmax[G], hsum[G];
+    const int s = blockIdx.x, kvh = blockIdx.y;
+    const int j0 = s * kAttnSplit;
+    const int t0 = blockIdx.z * kQ;
+    const int t1 = t0 + kQ < nt ? t0 + kQ : nt;
+    if (j0 > pos0 + t1 - 1) return;  // no token of the block reaches the split
+    const int tid = threadIdx.x;
+    const long cache0 = static_cast<long>(kvh) * max_seq * HD;
+    const int jmax = max_seq - 1;
+    const int qq = tid & 3, slot = tid >> 2;
+    const int sg = slot / kPG, pb = (slot - sg * kPG) * G;
+    uint4 kq[G][kQU];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const int j = j0 + pb + i <= jmax ? j0 + pb + i : jmax;
+        const uint4* kr =
+            reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) + qq * kQU;
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) kq[i][u] = kr[u];
+    }
+    constexpr int kVPer = kAttnSplit * kU / kAttnThreads;
+    uint4 vraw[kVPer];
+#pragma unroll
+    for (int t = 0; t < kVPer; ++t) {
+        const int idx = tid + t * kAttnThreads;
+        const int jj = idx / kU, c = idx - jj * kU;
+        const int j = j0 + jj <= jmax ? j0 + jj : jmax;
+        vraw[t] = reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
+    }
+    const bool has_q = tid < G * kU;
+    // the first token of the block that reaches the split
+    int t = t0;
+    if (j0 > pos0 + t) t = j0 - pos0;
+    uint4 qraw = make_uint4(0, 0, 0, 0);
+    if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + static_cast<long>(t) * qkv_stride + (kvh * G) * HD)[tid];
+#pragma unroll
+    for (int i = 0; i < kVPer; ++i) {
+        const int idx = tid + i * kAttnThreads;
+        const int jj = idx / kU, c = idx - jj * kU;
+        uint32_t* row = &vs[jj][4 * c];
+        row[0] = vraw[i].x;
+        row[1] = vraw[i].y;
+        row[2] = vraw[i].z;
+        row[3] = vraw[i].w;
+    }
+    const long hs = static_cast<long>(gridDim.y) * G * S;
+    for (; t < t1; ++t) {
+        if (t > t0) __syncthreads();  // the previous token's reads of qs and sc are done
+        if (has_q) {
+            float f[8];
+            unpack_bf16x8(qraw, f);
+            store_f8(&qs[tid / kU][8 * (tid % kU)], f);
+        }
+        // the next token's q (clamped to the block's last token)
+        const int tn = t + 1 < t1 ? t + 1 : t;
+        if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + static_cast<long>(tn) * qkv_stride + (kvh * G) * HD)[tid];
+        const int pos = pos0 + t;
+        const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
+        __syncthreads();
+        attention_split<HD, G>(kq, qs, vs, sc, hmax, hsum, jn, scale, s, kvh, S, pm + t * hs,
+                               pl + t * hs, pacc + t * hs * HD);
     }
 }
 
@@ -1687,17 +1779,20 @@ void launch_attention_hd(int G, dim3 grid, hipStream_t s, const uint16_t* qkv,
     }
 }
 // The prefill form: c tokens at positions pos0 .. pos0 + c - 1 (grid.z).
+constexpr int kPrefillQueries = 16;  // tokens per block of the prefill attention
+
 template <int HD>
-void launch_attention_prefill_hd(int G, dim3 grid, hipStream_t s, const uint16_t* qkv,
-                                 const uint16_t* kc, const uint16_t* vc, float* pm, float* pl,
-                                 float* pacc, int max_seq, int S, float scale, int pos0,
-                                 int qkv_stride) {
-    const dim3 block(kAttnThreads);
+void launch_attention_prefill_hd(int G, int sp, int nkv, int c, hipStream_t s,
+                                 const uint16_t* qkv, const uint16_t* kc, const uint16_t* vc,
+                                 float* pm, float* pl, float* pacc, int max_seq, int S,
+                                 float scale, int pos0, int qkv_stride) {
+    constexpr int Q = kPrefillQueries;
+    const dim3 grid(sp, nkv, (c + Q - 1) / Q), block(kAttnThreads);
     switch (G) {
-    case 1: hipLaunchKernelGGL((attention_kernel<HD, 1, true>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, nullptr, max_seq, S, scale, pos0, qkv_stride); break;
-    case 2: hipLaunchKernelGGL((attention_kernel<HD, 2, true>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, nullptr, max_seq, S, scale, pos0, qkv_stride); break;
-    case 4: hipLaunchKernelGGL((attention_kernel<HD, 4, true>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, nullptr, max_seq, S, scale, pos0, qkv_stride); break;
-    default: hipLaunchKernelGGL((attention_kernel<HD, 8, true>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, nullptr, max_seq, S, scale, pos0, qkv_stride); break;
+    case 1: hipLaunchKernelGGL((attention_prefill_kernel<HD, 1, Q>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, max_seq, S, scale, pos0, c, qkv_stride); break;
+    case 2: hipLaunchKernelGGL((attention_prefill_kernel<HD, 2, Q>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, max_seq, S, scale, pos0, c, qkv_stride); break;
+    case 4: hipLaunchKernelGGL((attention_prefill_kernel<HD, 4, Q>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, max_seq, S, scale, pos0, c, qkv_stride); break;
+    default: hipLaunchKernelGGL((attention_prefill_kernel<HD, 8, Q>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, max_seq, S, scale, pos0, c, qkv_stride); break;
     }
 }
 
@@ -1906,11 +2001,11 @@ struct spb_engine {
             // splits that some token of the pass reaches
             const int sp = (pos0 + c - 1) / kAttnSplit + 1 < S ? (pos0 + c - 1) / kAttnSplit + 1 : S;
             if (hd == 64)
-                launch_attention_prefill_hd<64>(nh / nkv, dim3(sp, nkv, c), s, pf_qkv, kcache[l],
+                launch_attention_prefill_hd<64>(nh / nkv, sp, nkv, c, s, pf_qkv, kcache[l],
                                                 vcache[l], pf_pm, pf_pl, pf_pacc, max_seq, S,
                                                 scale, pos0, qrows + 2 * kvdim);
             else
-                launch_attention_prefill_hd<128>(nh / nkv, dim3(sp, nkv, c), s, pf_qkv, kcache[l],
+                launch_attention_prefill_hd<128>(nh / nkv, sp, nkv, c, s, pf_qkv, kcache[l],
                                                  vcache[l], pf_pm, pf_pl, pf_pacc, max_seq, S,
                                                  scale, pos0, qrows + 2 * kvdim);
             {
