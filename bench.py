@@ -160,7 +160,7 @@ def decode_config4_bs1(args, log, ev, stream):
     prompt token.  The engine, like the reference's InferenceEngine::forward,
     decodes one sequence; batch 8 and 32 are not built."""
     return _decode_run(log, ev, stream, max_seq=4096, prompt_len=2048, n=args.decode_tokens,
-                       stepwise_prefill=True)
+                       stepwise_prefill=not args.no_stepwise_prefill)
 
 
 def main() -> int:
@@ -180,6 +180,10 @@ def main() -> int:
     ap.add_argument("--decode-tokens", type=int, default=128)
     ap.add_argument("--no-long-decode", action="store_true",
                     help="skip the config-4 (2048-token prompt, 4096 KV) batch-1 decode")
+    ap.add_argument("--no-short-decode", action="store_true",
+                    help="skip the config-3 decode (keep config 4)")
+    ap.add_argument("--no-stepwise-prefill", action="store_true",
+                    help="config 4: skip timing the prefill as one decode step per token")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB once (known bytes, for scaling rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE) and exit")
@@ -443,7 +447,8 @@ def main() -> int:
         detail["gemm_config2_6912x2560_warm_b2b"] = g2
 
     if not args.no_decode:
-        detail["decode_config3"] = decode_config3(args, log, ev, stream)
+        if not args.no_short_decode:
+            detail["decode_config3"] = decode_config3(args, log, ev, stream)
         if not args.no_long_decode:
             detail["decode_config4_bs1"] = decode_config4_bs1(args, log, ev, stream)
 
