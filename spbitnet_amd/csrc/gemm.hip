@@ -240,7 +240,20 @@ extern "C" int spb_sparse_ternary_gemm(const uint32_t* meta, const uint32_t* val
             launch_smfmac<2, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
         } else {
             if ((n + 63) / 64 > 65535) return invalid("%s: batch %d too large", fn, n);
-            launch_smfmac<8, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
+            // The deepest row tile whose grid still gives ~0.6 blocks per CU:
+            // on MI355X, 6912x2560 ran 21 us at n=256 with 8 strips (216
+            // blocks) against 25 with 4; 2560x2560-class and 640-row shapes,
+            // whose 8-strip grids leave most CUs idle, ran up to 2x faster
+            // with 4 or 2 strips (640x2560, n=256: 19.3 -> 9.5 us).
+            const long cus = device_cu_count();
+            const long tiles = (n + 63) / 64;
+            auto blocks = [&](int strips) { return (rows + 16L * strips - 1) / (16L * strips) * tiles; };
+            if (blocks(8) * 5 >= cus * 3)
+                launch_smfmac<8, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
+            else if (blocks(4) * 5 >= cus * 3)
+                launch_smfmac<4, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
+            else
+                launch_smfmac<2, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
         }
     } else {
         if (n > 65535) return invalid("%s: batch %d exceeds 65535", fn, n);

@@ -57,7 +57,8 @@ def test_gemm_config2(gpu, n):
 
 @pytest.mark.parametrize("rows,cols,n", [(2560, 6912, 16), (7, 128, 1), (333, 384, 5),
                                          (100, 256, 17), (16, 512, 100), (45, 100, 3),
-                                         (9, 36, 20)])
+                                         (9, 36, 20), (640, 2560, 200), (2560, 2560, 129),
+                                         (6912, 2560, 1023), (1000, 1024, 300)])
 def test_gemm_odd_shapes(gpu, rows, cols, n):
     L = W.random_layer(rows, cols, W.seed_for("gemm-odd", rows, cols, n))
     X = np.random.default_rng(rows + cols + n).integers(-128, 128, (n, cols)).astype(np.int8)
