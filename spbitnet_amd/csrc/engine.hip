@@ -1865,7 +1865,7 @@ struct spb_engine {
     hipGraphExec_t exec = nullptr;
     int seq_len = 0;
     // batched prefill: prompts with at least prefill_min tokens before the
-    // last go through the layers kPrefillChunk tokens at a time (0: never)
+    // last go through the layers pf_chunk tokens at a time (0: never)
     int prefill_min = kPrefillMinDefault;
     int8_t* pf_x = nullptr;     // [chunk][max cols] int8 activations
     float* pf_amax = nullptr;   // [chunk]
@@ -1946,7 +1946,7 @@ struct spb_engine {
     }
 
     // Positions pos0 .. pos0 + c - 1 (tokens[] holds their ids) through every
-    // layer, c <= kPrefillChunk: the KV cache of those positions as c decode
+    // layer, c <= pf_chunk: the KV cache of those positions as c decode
     // steps would write it.  Returns a HIP error or hipSuccess.
     hipError_t enqueue_prefill(int pos0, int c, hipStream_t s) {
         const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
