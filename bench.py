@@ -12,11 +12,11 @@ streams from HBM) reduced by one launch of the drop-in GEMV entry point
 The JSON line reports
   value      algorithmic GB/s of the step (packed weight bytes + x + y per
              launch, divided by the step time; inputs resident in HBM; the
-             K timed steps are one HIP graph, replayed once)
+             K timed steps are back-to-back replays of a 10-step HIP graph)
   roofline   the streaming GEMV kernel: algorithmic bytes per launch / its
              average launch duration over the timed region (HIP events on
-             the launch stream around the K-step graph, 2K launches),
-             against the 8 TB/s HBM peak
+             the launch stream around the K steps, 2K launches), against
+             the 8 TB/s HBM peak
   cpu_baseline  the reference's CPU GEMV (its own unpack_to_int8 + int32 MAC,
              built from the reference sources into oracle/_ref) on the
              6912x2560 matrix, single thread, on this host
@@ -166,7 +166,7 @@ def decode_config4_bs1(args, log, ev, stream):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--prewarm-ms", type=float, default=30.0,
                     help="run the step this long before the warmup steps (clock ramp)")
@@ -282,10 +282,12 @@ def main() -> int:
     # The GPU's clocks settle only after ~2 ms of sustained load following an
     # idle period (launches of this step measured 55-64 us at first, then
     # ~47-51 us), so the step first runs for --prewarm-ms from a one-step
-    # graph.  The W warmup steps and the K timed steps are then each one HIP
-    # graph holding W (K) steps, replayed once: consecutive launches run back
-    # to back as in a decode, without the ~8 us a graph replay adds at its
-    # start, and the host's per-launch cost stays out of the GPU timeline.
+    # graph.  The W warmup steps and the K timed steps then run as replays of
+    # a graph of kGraphSteps steps (and one graph of the remainder), back to
+    # back: the ~8 us a replay adds at its start is spread over 20 launches,
+    # the host's per-launch cost stays out of the GPU timeline, and the graph
+    # stays small (one graph of 200 steps measured ~5 % slower per launch
+    # than replays of a 10-step graph on the same box).
     def step_graph(n):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
@@ -293,6 +295,18 @@ def main() -> int:
                 step()
         return g
 
+    kGraphSteps = 10
+
+    def run_steps(k):
+        """Launch k steps as replays of kGraphSteps-step graphs (no host sync)."""
+        if k // kGraphSteps:
+            for _ in range(k // kGraphSteps):
+                g_block.replay()
+        if k % kGraphSteps:
+            g_rem[k % kGraphSteps].replay()
+
+    g_block = step_graph(kGraphSteps)
+    g_rem = {r: step_graph(r) for r in {args.steps % kGraphSteps, args.warmup % kGraphSteps} if r}
     g_one = step_graph(1)
     t_pre = time.perf_counter()
     while time.perf_counter() - t_pre < args.prewarm_ms * 1e-3:
@@ -300,25 +314,21 @@ def main() -> int:
             g_one.replay()
         torch.cuda.synchronize()
     del g_one
-    if args.warmup > 0:
-        g_warm = step_graph(args.warmup)
-        g_warm.replay()
-        del g_warm
-    g_timed = step_graph(args.steps)
+    run_steps(args.warmup)
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps")
     e0, e1 = ev(), ev()
     e0.record(stream)
-    g_timed.replay()
+    run_steps(args.steps)
     e1.record(stream)
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
     value_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
-    del g_timed
+    del g_block, g_rem
 
     # Average launch duration of the GEMV kernel over the timed region: the
-    # events bracket the 2K launches of the timed graph (back to back; the
-    # average includes the ~1 us between consecutive graph kernels).
+    # events bracket its 2K launches (back to back; the average includes the
+    # gaps between consecutive graph kernels and between replays).
     avg_us = ms_per_step * 1e3 / len(launches)
     avg_bytes = step_bytes / len(launches)
     kernel_gbs = avg_bytes / (avg_us * 1e-6) / 1e9
