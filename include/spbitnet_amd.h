@@ -27,6 +27,7 @@
 #ifndef SPBITNET_AMD_H
 #define SPBITNET_AMD_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -101,6 +102,26 @@ int spb_dequantize_f16(const int32_t* input, uint16_t* output, const float* d_ab
                        float gamma, int size, spb_stream_t stream);
 int spb_dequantize_bf16(const int32_t* input, uint16_t* output, const float* d_absmax,
                         float gamma, int size, spb_stream_t stream);
+
+/* Replaces InferenceEngine::bitlinear (reference src/inference.cu:106-117:
+ * absmax_reduce_gpu into the engine's d_absmax_ scratch, then
+ * fused_sparse_bitlinear_gpu) as one call; the scratch comes in as a caller
+ * workspace of at least spb_bitlinear_workspace_size(cols) bytes, 16-byte
+ * aligned (the absmax, then the quantised activations as bit planes, built
+ * once instead of in every GEMV workgroup when cols % 8 == 0 and x is 16-byte
+ * aligned).  Output bits equal the reference pair's:
+ * output[r] = 16-bit(float(W q) * ((gamma * absmax) / 127)),
+ * q = clamp(rint(x * (absmax > 0 ? 127/absmax : 0)), -128, 127).
+ * Calls that share a workspace must be ordered (same stream). */
+size_t spb_bitlinear_workspace_size(int cols);
+int spb_bitlinear_f16(const uint32_t* meta, const uint32_t* values, const uint16_t* x,
+                      uint16_t* output, float gamma, int rows, int cols, int meta_row_stride,
+                      int values_row_stride, void* workspace, size_t workspace_size,
+                      spb_stream_t stream);
+int spb_bitlinear_bf16(const uint32_t* meta, const uint32_t* values, const uint16_t* x,
+                       uint16_t* output, float gamma, int rows, int cols, int meta_row_stride,
+                       int values_row_stride, void* workspace, size_t workspace_size,
+                       spb_stream_t stream);
 
 /* ---- Batched GEMM ---------------------------------------------------------------
  * Replaces the cuSPARSELt path CuSparseLtGemm(m,k,n) + execute
@@ -311,9 +332,12 @@ int spb_engine_set_stream(spb_engine* engine, spb_stream_t stream);
 int spb_engine_reset(spb_engine* engine);
 /* InferenceEngine::forward (inference.h:33; inference.cu:126-283): one token
  * at the next position; *d_logits = device float32 [vocab] (valid until the
- * next call; ordered on the engine stream). */
+ * next call; ordered on the engine stream).  After spb_engine_generate or
+ * spb_engine_decode_steps it continues at the position those reached (read
+ * back from the device), in forward mode: no EOS stop, no token writes. */
 int spb_engine_forward(spb_engine* engine, int token_id, const float** d_logits);
-/* InferenceEngine::seq_len (inference.h:38). */
+/* InferenceEngine::seq_len (inference.h:38).  After spb_engine_decode_steps
+ * it synchronises the engine stream to read the position back (-1 on error). */
 int spb_engine_seq_len(const spb_engine* engine);
 /* Greedy generation (src/main.cpp:133-155): reset, prefill prompt[0..n-1)
  * one token at a time, then n_new greedy steps starting from the last prompt
@@ -330,7 +354,8 @@ int spb_engine_generate(spb_engine* engine, const int* prompt, int n_prompt, int
  * step per token; default 16. */
 int spb_engine_set_prefill_batch(spb_engine* engine, int min_tokens);
 /* Launches `steps` more token steps continuing the current state (timing
- * loops); no host synchronisation. */
+ * loops); no host synchronisation.  The host learns the new position when
+ * spb_engine_seq_len or spb_engine_forward is next called. */
 int spb_engine_decode_steps(spb_engine* engine, int steps);
 /* Device buffers: logits float32 [vocab], tokens int32 [max_seq + 1]. */
 int spb_engine_buffers(const spb_engine* engine, const float** logits, const int** tokens);

@@ -4,7 +4,8 @@ sparse-ternary linear-layer hot path.
 * ``include/spbitnet_amd.h``        C ABI of the HIP library (the drop-in boundary)
 * ``spbitnet_amd/csrc/*.hip``       hand-written gfx950 kernels behind it
 * ``spbitnet_amd.kernels``          the reference's kernel API, in Python, over the C ABI
-* ``spbitnet_amd.layer``            SparseLinear weight handle and BitLinear call
+* ``spbitnet_amd.model``            Model / InferenceEngine: loader, random-init
+                                    models and the decode engines over the C ABI
 * ``spbitnet_amd.weights``          host-side format: generation and packing
 """
 from .weights import (  # noqa: F401

@@ -42,6 +42,9 @@ SIGNATURES = {
     "spb_sparse_ternary_gemv_planes": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "spb_fused_sparse_bitlinear_planes_f16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
     "spb_fused_sparse_bitlinear_planes_bf16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
+    "spb_bitlinear_workspace_size": [_I],
+    "spb_bitlinear_f16": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "spb_bitlinear_bf16": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
     # per-op inference kernels
     "spb_rms_norm_f16": [_P, _P, _P, _I, _F, _P],
     "spb_rms_norm_bf16": [_P, _P, _P, _I, _F, _P],
@@ -83,7 +86,8 @@ SIGNATURES = {
     "spb_generate_sparse_ternary": [ctypes.c_uint64, _I, _I, _P, _P, _I, _I, _P, _P, _P],
     "spb_generate_normal_bf16": [ctypes.c_uint64, ctypes.c_long, _F, _P, _P],
 }
-_RESTYPES = {"spb_last_error_string": ctypes.c_char_p}
+_RESTYPES = {"spb_last_error_string": ctypes.c_char_p,
+             "spb_bitlinear_workspace_size": ctypes.c_size_t}
 
 
 class SparseLinearC(ctypes.Structure):

@@ -6,6 +6,7 @@ whose exported symbols are the C ABI declared in include/spbitnet_amd.h.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import glob
 import os
 import subprocess
@@ -39,15 +40,22 @@ def build(verbose: bool = False) -> str:
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     objdir = os.path.join(PKG, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = []
-    for src in sources():
+    def compile_one(src):
         obj = os.path.join(objdir, os.path.basename(src) + ".o")
         cmd = [hipcc, *HIPCC_FLAGS, "-c", src, "-o", obj]
-        if verbose:
-            print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)
         msgs = [l for l in (r.stderr or "").splitlines() if "packed-fp32-ops" not in l]
-        if r.returncode != 0:
+        return src, obj, cmd, r.returncode, msgs
+
+    # one hipcc per source, in parallel (engine.hip alone takes ~20 s)
+    jobs = min(len(sources()), max(1, min(8, os.cpu_count() or 1)))
+    with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
+        results = list(pool.map(compile_one, sources()))
+    objs = []
+    for src, obj, cmd, rc, msgs in results:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        if rc != 0:
             raise RuntimeError(f"hipcc failed on {src}:\n" + "\n".join(msgs))
         if verbose and msgs:
             print("\n".join(msgs))

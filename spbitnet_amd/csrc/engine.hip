@@ -1864,6 +1864,12 @@ struct spb_engine {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int seq_len = 0;
+    // The device state is in generate mode (prompt_len, stop_eos, done as
+    // spb_engine_generate left them) or advanced by spb_engine_decode_steps
+    // without the host knowing its position: spb_engine_forward first reads
+    // the position back and re-arms forward mode.
+    bool device_mode = false;
+    bool pos_stale = false;
     // batched prefill: prompts with at least prefill_min tokens before the
     // last go through the layers pf_chunk tokens at a time (0: never)
     int prefill_min = kPrefillMinDefault;
@@ -2056,6 +2062,12 @@ int check_linear(const char* fn, const char* name, const spb_sparse_linear& l, i
     if (l.rows != rows || l.cols != cols)
         return invalid("%s: %s is %dx%d, expected %dx%d", fn, name, l.rows, l.cols, rows, cols);
     if (!l.meta || !l.values) return invalid("%s: %s has null weights", fn, name);
+    // strides must cover a row (the projection kernels read whole rows)
+    char where[128];
+    snprintf(where, sizeof(where), "%s: %s", fn, name);
+    if (int rc = check_weights(where, l.meta, l.values, l.rows, l.cols, l.meta_stride,
+                               l.values_stride))
+        return rc;
     if (!bitplane_ok(l.meta, l.values, l.cols, l.meta_stride, l.values_stride))
         return invalid("%s: %s must have cols %% 128 == 0, cols <= %d, meta_stride %% 4 == 0, "
                        "values_stride %% 2 == 0 and 16/8-byte aligned meta/values",
@@ -2081,6 +2093,18 @@ int set_state(spb_engine* e, int pos, int prompt_len, int stop_eos) {
                        sizeof(float2) * half, hipMemcpyDeviceToDevice, e->stream) != hipSuccess ||
         hipStreamSynchronize(e->stream) != hipSuccess)
         return launch_status("spb_engine: state upload");
+    return 0;
+}
+
+// Reads the device position back after spb_engine_decode_steps (host sync).
+int sync_seq_len(spb_engine* e, const char* fn) {
+    if (!e->pos_stale) return 0;
+    EngineState h{};
+    if (hipMemcpyAsync(&h, e->st, sizeof(h), hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
+        hipStreamSynchronize(e->stream) != hipSuccess)
+        return launch_status(fn);
+    e->seq_len = h.pos < e->max_seq ? h.pos : e->max_seq;
+    e->pos_stale = false;
     return 0;
 }
 
@@ -2266,10 +2290,16 @@ extern "C" int spb_engine_reset(spb_engine* e) {
             hipMemsetAsync(e->vcache[l], 0, kv, e->stream) != hipSuccess)
             return launch_status("spb_engine_reset");
     }
+    e->device_mode = false;
+    e->pos_stale = false;
     return set_state(e, 0, 0x7FFFFFFF, 0);
 }
 
-extern "C" int spb_engine_seq_len(const spb_engine* e) { return e ? e->seq_len : -1; }
+extern "C" int spb_engine_seq_len(const spb_engine* e) {
+    if (!e) return -1;
+    if (e->pos_stale && sync_seq_len(const_cast<spb_engine*>(e), "spb_engine_seq_len")) return -1;
+    return e->seq_len;
+}
 
 extern "C" int spb_engine_forward(spb_engine* e, int token_id, const float** d_logits) {
     clear_error();
@@ -2277,6 +2307,13 @@ extern "C" int spb_engine_forward(spb_engine* e, int token_id, const float** d_l
     if (!e) return invalid("%s: null engine", fn);
     if (token_id < 0 || token_id >= e->cfg.vocab_size)
         return invalid("%s: token %d outside [0, %d)", fn, token_id, e->cfg.vocab_size);
+    if (e->device_mode || e->pos_stale) {
+        // after generate / decode_steps: continue at the device position in
+        // forward mode (no EOS stop, no token writes, done cleared)
+        if (int rc = sync_seq_len(e, fn)) return rc;
+        if (int rc = set_state(e, e->seq_len, 0x7FFFFFFF, 0)) return rc;
+        e->device_mode = false;
+    }
     if (e->seq_len >= e->max_seq) return invalid("%s: sequence is full (%d)", fn, e->max_seq);
     const int pos = e->seq_len;
     if (hipMemcpyAsync(e->tokens + pos, &token_id, sizeof(int), hipMemcpyHostToDevice,
@@ -2333,7 +2370,9 @@ extern "C" int spb_engine_generate(spb_engine* e, const int* prompt, int n_promp
                              hipMemcpyDeviceToHost) != hipSuccess)
         return launch_status(fn);
     if (n_generated) *n_generated = got;
-    e->seq_len = h.pos;
+    e->seq_len = h.pos < e->max_seq ? h.pos : e->max_seq;
+    e->device_mode = true;
+    e->pos_stale = false;
     return 0;
 }
 
@@ -2348,9 +2387,13 @@ extern "C" int spb_engine_set_prefill_batch(spb_engine* e, int min_tokens) {
 extern "C" int spb_engine_decode_steps(spb_engine* e, int steps) {
     clear_error();
     if (!e) return invalid("spb_engine_decode_steps: null engine");
+    if (steps < 0) return invalid("spb_engine_decode_steps: steps < 0");
     for (int i = 0; i < steps; ++i)
         if (hipGraphLaunch(e->exec, e->stream) != hipSuccess)
             return launch_status("spb_engine_decode_steps");
+    // the device advanced pos (unless the state is done): seq_len and forward
+    // read it back when next asked
+    if (steps > 0) e->pos_stale = true;
     return 0;
 }
 

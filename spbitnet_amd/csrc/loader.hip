@@ -291,9 +291,26 @@ bool load_linear(spb_model* m, const std::string& dir, const Json& e, int rows, 
               ", expected " + std::to_string(rows) + "x" + std::to_string(cols);
         return false;
     }
-    out.meta_stride = static_cast<int>(num_or(e, "meta_stride", 0));
-    out.values_stride = static_cast<int>(num_or(e, "values_stride", 0));
-    out.gamma = static_cast<float>(num_or(e, "gamma", 0));
+    // meta_stride, values_stride and gamma are required, as in the
+    // reference (src/model.cu:107-109 reads them with entry.at()), and the
+    // strides must cover a row (ceil(cols/32) meta and ceil(cols/64) sign
+    // words): an understated stride would make every kernel read past its row.
+    for (const char* key : {"meta_stride", "values_stride", "gamma"}) {
+        const Json* v = e.get(key);
+        if (!v || v->kind != Json::kNum) {
+            err = std::string("sparse entry without numeric ") + key;
+            return false;
+        }
+    }
+    out.meta_stride = static_cast<int>(e.get("meta_stride")->num);
+    out.values_stride = static_cast<int>(e.get("values_stride")->num);
+    out.gamma = static_cast<float>(e.get("gamma")->num);
+    if (out.meta_stride < (cols + 31) / 32 || out.values_stride < (cols + 63) / 64) {
+        err = "sparse entry strides " + std::to_string(out.meta_stride) + "/" +
+              std::to_string(out.values_stride) + " do not cover a row of " +
+              std::to_string(cols) + " columns";
+        return false;
+    }
     const Json* mf = e.get("meta_file");
     const Json* vf = e.get("values_file");
     if (!mf || !vf || mf->kind != Json::kStr || vf->kind != Json::kStr) {

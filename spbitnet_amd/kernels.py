@@ -213,3 +213,28 @@ def gemv_kernel_id(meta, values, rows, cols, meta_row_stride, values_row_stride)
     """1 if the bit-plane GEMV kernel would run for these arguments, else 0."""
     return _lib.load().spb_sparse_ternary_gemv_kernel_id(
         meta.data_ptr(), values.data_ptr(), rows, cols, meta_row_stride, values_row_stride)
+
+
+def bitlinear_workspace_size(cols: int) -> int:
+    """Bytes of the workspace bitlinear_gpu needs for `cols` input columns."""
+    return int(_lib.load().spb_bitlinear_workspace_size(int(cols)))
+
+
+def bitlinear_gpu(meta, values, x, output, gamma, rows, cols, meta_row_stride,
+                  values_row_stride, workspace, stream=None):
+    """InferenceEngine::bitlinear (reference src/inference.cu:106-117) as one
+    call: absmax, quantisation, sparse GEMV and dequantisation, with the
+    absmax scratch (and the activation planes) in `workspace`, a uint8 GPU
+    tensor of at least bitlinear_workspace_size(cols) bytes."""
+    pm, pv = _weights(meta, values, rows, cols, meta_row_stride, values_row_stride)
+    empty = rows == 0 or cols == 0
+    kind = _HALF_KIND.get(x.dtype)
+    if kind is None:
+        raise TypeError(f"x has dtype {x.dtype}, expected float16 or bfloat16")
+    px = _dev(x, "x", x.dtype, 0 if empty else cols)
+    po = _dev(output, "output", x.dtype, 0 if empty else rows)
+    need = 0 if empty else bitlinear_workspace_size(cols)
+    pw = _dev(workspace, "workspace", torch.uint8, need)
+    fn = getattr(_lib.load(), f"spb_bitlinear_{kind}")
+    _lib.check(fn(pm, pv, px, po, float(gamma), rows, cols, meta_row_stride, values_row_stride,
+                  pw, workspace.numel(), _stream_ptr(stream)), "bitlinear_gpu")

@@ -358,7 +358,13 @@ def load_model(model_dir: str, device="cuda") -> "Model":
             rows, cols = e["shape"]
             if (rows, cols) != shapes[attr]:
                 raise ValueError(f"layers.{li}.{name}: shape {rows}x{cols}, expected {shapes[attr]}")
-            ms, vs = e["meta_stride"], e["values_stride"]
+            for key in ("meta_stride", "values_stride", "gamma"):
+                if key not in e:  # required, as in src/model.cu:107-109
+                    raise ValueError(f"layers.{li}.{name}: manifest entry lacks {key}")
+            ms, vs = int(e["meta_stride"]), int(e["values_stride"])
+            if ms < (cols + 31) // 32 or vs < (cols + 63) // 64:
+                raise ValueError(f"layers.{li}.{name}: strides {ms}/{vs} do not cover a row of "
+                                 f"{cols} columns")
             m = torch.from_numpy(raw(e["meta_file"], "<u4", rows * ms).view(np.int32).reshape(rows, ms).copy())
             v = torch.from_numpy(raw(e["values_file"], "<u4", rows * vs).view(np.int32).reshape(rows, vs).copy())
             lin[attr] = SparseLinear(m.to(dev), v.to(dev), float(np.float32(e["gamma"])), rows, cols,

@@ -75,6 +75,19 @@ def test_host_validation_without_gpu(lib):
     assert lib.spb_absmax_reduce_bf16(fake, None, 16, None) == 1
     assert lib.spb_absmax_quantize_f16(fake, fake, fake, -3, None) == 1
     assert lib.spb_dequantize_bf16(fake, fake, fake, ctypes.c_float(1.0), 0, None) == 0
+    # one-call BitLinear: workspace = 256 bytes of absmax + the planes (cols bytes, 32-rounded)
+    assert lib.spb_bitlinear_workspace_size(2560) == 256 + 2560
+    assert lib.spb_bitlinear_workspace_size(100) == 256 + 128
+    assert lib.spb_bitlinear_workspace_size(0) == 0
+    bl = lib.spb_bitlinear_bf16
+    ws = ctypes.c_void_p(0x20000)
+    assert bl(fake, fake, fake, fake, ctypes.c_float(1.0), 4, 256, 8, 4, ws, 511, None) == 1
+    assert b"workspace" in lib.spb_last_error_string()
+    assert bl(fake, fake, fake, fake, ctypes.c_float(1.0), 4, 256, 8, 4, None, 512, None) == 1
+    assert bl(fake, fake, fake, fake, ctypes.c_float(1.0), 4, 256, 8, 4,
+              ctypes.c_void_p(0x20004), 512, None) == 1  # not 16-byte aligned
+    assert bl(fake, fake, fake, fake, ctypes.c_float(1.0), 4, 256, 7, 4, ws, 512, None) == 1
+    assert bl(fake, fake, fake, fake, ctypes.c_float(1.0), 0, 256, 8, 4, None, 0, None) == 0
 
 
 def test_gemv_kernel_selection(lib):

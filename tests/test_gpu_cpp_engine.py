@@ -37,3 +37,35 @@ def test_cpp_engine_program(gpu, tmp_path):
     assert cpp_tokens == eng.generate(prompt, 32, stop_at_eos=False)
     assert cpp_tokens == O.EngineOracle(model.to_host(), 256).generate(prompt, 32)
     eng.close()
+
+
+BITLINEAR_EXE = os.path.join(ROOT, "tests", "cpp", "bitlinear_api")
+
+
+def test_cpp_bitlinear_pair(gpu, tmp_path):
+    """The reference's InferenceEngine::bitlinear pair (absmax_reduce_gpu, then
+    fused_sparse_bitlinear_gpu; src/inference.cu:106-117) compiled in a C++
+    host program against this build's mirror headers, on the 6912x2560 FFN
+    shape in fp16 and bf16: output bits equal the oracle's."""
+    from spbitnet_amd import weights as W
+    assert os.path.exists(BITLINEAR_EXE), "tests/cpp/bitlinear_api is not built"
+    rows, cols = 6912, 2560
+    L = W.random_layer(rows, cols, W.seed_for("cpp-bitlinear", rows, cols))
+    a = W.normal_f32(W.seed_for("cpp-bitlinear-x", cols), cols)
+    L.meta.astype("<u4").tofile(tmp_path / "meta.bin")
+    L.values.astype("<u4").tofile(tmp_path / "values.bin")
+    x16 = a.astype(np.float16)
+    xb = O.to_bf16_bits(a)
+    x16.view(np.uint16).tofile(tmp_path / "x_f16.bin")
+    xb.tofile(tmp_path / "x_bf16.bin")
+    print("running the C++ bitlinear program", flush=True)
+    r = subprocess.run([BITLINEAR_EXE, str(tmp_path), str(rows), str(cols), str(L.meta_stride),
+                        str(L.values_stride), repr(float(L.gamma))],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    for tag, xf, to_bits in (("f16", x16.astype(np.float32), O.to_f16_bits),
+                             ("bf16", O.bf16_bits_to_f32(xb), O.to_bf16_bits)):
+        want, _ = O.fused_bitlinear(L.meta, L.values, xf, O.absmax(xf), L.gamma, rows, cols)
+        got = np.fromfile(tmp_path / f"out_{tag}.bin", dtype=np.uint16)
+        assert got.size == rows
+        assert (got == to_bits(want)).all(), tag

@@ -225,3 +225,68 @@ def test_engine_bitnet_2b4t_shape(gpu):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
             f"step {i}: max |diff| {np.abs(got - want).max()}"
     eng.close()
+
+
+def test_engine_forward_after_generate_at_eos(gpu):
+    """generate() stopping at EOS leaves its generate-mode state (done, the
+    prompt length, the EOS stop) on the device; a later forward() continues
+    at the position generate reached, in forward mode, with logits equal to
+    the oracle's after the same tokens."""
+    from spbitnet_amd.model import InferenceEngine
+    cfg = _small_config(num_hidden_layers=1)
+    model, eng, ora = _engine_pair(cfg, seed=43, max_seq=128)
+    prompt = _prompt(6, cfg.vocab_size, 2)
+    free = ora.generate(prompt, 24)
+    eos = free[9]
+    eng.close()
+    model.config = _small_config(num_hidden_layers=1, eos_token_id=eos)
+    eng = InferenceEngine(model, max_seq=128)
+    got = eng.generate(prompt, 24, stop_at_eos=True)
+    want = ora.generate(prompt, 24, eos=eos)
+    assert got == want and got[-1] == eos
+    assert eng.seq_len() == len(prompt) - 1 + len(got)
+    for i, t in enumerate([eos, 17, eos, 3]):
+        print(f"forward after generate {i}", flush=True)
+        g = eng.forward(t).cpu().numpy()
+        wt, w = ora.step(t)
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"step {i}"
+    assert eng.seq_len() == len(prompt) - 1 + len(got) + 4
+    eng.close()
+
+
+def test_engine_decode_steps_then_forward(gpu):
+    """decode_steps() advances the device position without a host sync;
+    seq_len() reads it back and forward() continues there."""
+    cfg = _small_config(num_hidden_layers=1)
+    model, eng, ora = _engine_pair(cfg, seed=47, max_seq=128)
+    prompt = _prompt(7, cfg.vocab_size, 3)
+    assert eng.generate(prompt, 0, stop_at_eos=False) == []
+    assert eng.seq_len() == len(prompt) - 1
+    eng.decode_steps(5)
+    assert eng.seq_len() == len(prompt) - 1 + 5
+    want = ora.generate(prompt, 5)
+    g = eng.forward(want[-1]).cpu().numpy()
+    wt, w = ora.step(want[-1])
+    assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
+    eng.close()
+
+
+def test_engine_rejects_short_strides(gpu):
+    """spb_engine_create checks that every projection's strides cover a row
+    before anything is launched (an understated stride would make the
+    projection kernels read past each row)."""
+    from spbitnet_amd import _lib
+    from spbitnet_amd.model import InferenceEngine, Model
+    cfg = _small_config(num_hidden_layers=1)
+    model = Model.random(cfg, seed=5)
+    q = model.layers[0].q_proj
+    q.meta_stride, keep = 4, q.meta_stride  # cols 512 need 16 meta words per row
+    with pytest.raises(_lib.SpbError, match="q_proj"):
+        InferenceEngine(model, max_seq=16)
+    q.meta_stride = keep
+    d = model.layers[0].down_proj
+    d.values_stride, keep = 2, d.values_stride
+    with pytest.raises(_lib.SpbError, match="down_proj"):
+        InferenceEngine(model, max_seq=16)
+    d.values_stride = keep
+    InferenceEngine(model, max_seq=16).close()

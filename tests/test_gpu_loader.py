@@ -63,3 +63,71 @@ def test_native_loader_errors(gpu, tmp_path):
         NativeModel(str(tmp_path))
     with pytest.raises(_lib.SpbError, match="config.json"):
         NativeModel(str(tmp_path / "missing"))
+
+
+FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "loader_model")
+
+
+def test_native_loader_reference_fixture(gpu):
+    """The native loader (spb_model_load) on the directory of the reference's
+    loader test (tests/test_model_loader.cu:52-191), with that test's
+    expectations (:199-284) and the device words its pattern fixes; an engine
+    on it is refused (hidden 8 is not a multiple of 128) before any launch."""
+    import ctypes
+    from spbitnet_amd import _lib
+    from spbitnet_amd.model import InferenceEngine, NativeModel
+    nat = NativeModel(FIXTURE)
+    c = nat.config
+    assert (c.hidden_size, c.num_hidden_layers, c.num_attention_heads, c.num_key_value_heads,
+            c.intermediate_size, c.vocab_size, c.head_dim) == (8, 1, 1, 1, 16, 32, 8)
+    assert nat._lm is None and nat._embed and nat._final  # tied LM head
+    assert nat.gpu_bytes > 0
+    layer = ctypes.cast(nat._layers_ptr, ctypes.POINTER(_lib.TransformerLayerC))[0]
+    assert layer.input_layernorm and layer.post_attention_layernorm
+    assert not layer.attn_sub_norm and not layer.ffn_sub_norm
+    q, g, d = layer.q_proj, layer.gate_proj, layer.down_proj
+    assert (q.rows, q.cols, q.gamma) == (8, 8, 0.5)
+    assert (g.rows, g.cols) == (16, 8) and (d.rows, d.cols) == (8, 16)
+
+    def words(ptr, n):
+        t = torch.empty(n, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        _lib.memcpy_d2d(t.data_ptr(), ptr, 4 * n, None)
+        torch.cuda.synchronize()
+        return t.cpu().numpy().view(np.uint32)
+
+    assert (words(q.meta, 8) == 0x33).all() and (words(q.values, 8) == 0xA).all()
+    assert (words(d.meta, 8) == 0x3333).all() and (words(d.values, 8) == 0xAA).all()
+    emb = torch.empty(32 * 8, dtype=torch.int16, device="cuda")
+    _lib.memcpy_d2d(emb.data_ptr(), nat._embed, 32 * 8 * 2, None)
+    torch.cuda.synchronize()
+    assert (emb.view(torch.bfloat16).float().cpu() == 1.0).all()  # fp16 1.0 -> bf16 1.0
+    with pytest.raises(_lib.SpbError):
+        InferenceEngine(nat, max_seq=16)
+    nat.close()
+
+
+def test_native_loader_requires_strides_and_gamma(gpu, tmp_path):
+    """meta_stride, values_stride and gamma are required (src/model.cu:107-109)
+    and the strides must cover a row: the native loader refuses the manifest
+    on the host, naming the tensor."""
+    import shutil
+    from spbitnet_amd import _lib
+    from spbitnet_amd.model import NativeModel
+    cases = [("layers.0.mlp.down_proj", "meta_stride", None),
+             ("layers.0.mlp.down_proj", "values_stride", None),
+             ("layers.0.self_attn.o_proj", "gamma", None),
+             ("layers.0.mlp.down_proj", "meta_stride", 0),
+             ("layers.0.self_attn.q_proj", "values_stride", 0)]
+    for i, (name, key, val) in enumerate(cases):
+        d = tmp_path / str(i)
+        shutil.copytree(FIXTURE, d)
+        man = json.load(open(d / "manifest.json"))
+        if val is None:
+            del man["weights"][name][key]
+        else:
+            man["weights"][name][key] = val
+        json.dump(man, open(d / "manifest.json", "w"))
+        print(f"native loader without {name}.{key}", flush=True)
+        with pytest.raises(_lib.SpbError, match=name):
+            NativeModel(str(d))

@@ -282,3 +282,26 @@ def test_fused_bitlinear(gpu, kind, rows, cols):
     want, acc = O.fused_bitlinear(L.meta, L.values, xf, amax, L.gamma, rows, cols)
     # Bit-exact 16-bit outputs: stricter than the contract's 1e-3 relative bound.
     assert (half_bits(out) == oracle_half_bits(want, kind)).all()
+
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+@pytest.mark.parametrize("rows,cols,shift", [(6912, 2560, 0), (2560, 6912, 0), (640, 2048, 0),
+                                             (96, 100, 0), (300, 2560, 1)])
+def test_one_call_bitlinear(gpu, kind, rows, cols, shift):
+    """spb_bitlinear_* (InferenceEngine::bitlinear as one call, the absmax
+    scratch and the activation planes in a caller workspace): output bits
+    equal the oracle's fused BitLinear.  cols % 8 != 0 and an x that is not
+    16-byte aligned (shift) take the reference's pair on the workspace's
+    absmax instead of the planes."""
+    L = W.random_layer(rows, cols, W.seed_for("bitlinear1", rows, cols))
+    a = W.normal_f32(W.seed_for("bitlinear1-x", rows, cols), cols + shift)
+    xt, xf = half_tensor(a, kind, gpu)
+    x = xt[shift:]
+    xf = xf[shift:]
+    out = torch.zeros(rows, dtype=HALF[kind], device=gpu)
+    ws = torch.full((K.bitlinear_workspace_size(cols),), 0xA5, dtype=torch.uint8, device=gpu)
+    K.bitlinear_gpu(dev_u32(L.meta, gpu), dev_u32(L.values, gpu), x, out, L.gamma, rows, cols,
+                    L.meta_stride, L.values_stride, ws)
+    torch.cuda.synchronize()
+    want, _ = O.fused_bitlinear(L.meta, L.values, xf, O.absmax(xf), L.gamma, rows, cols)
+    assert (half_bits(out) == oracle_half_bits(want, kind)).all()

@@ -88,3 +88,70 @@ def test_round_trip_without_sub_norms(tmp_path):
     save_model(m, str(tmp_path))
     r = load_model(str(tmp_path), device="cpu")
     assert r.layers[0].attn_sub_norm is None and r.layers[1].ffn_sub_norm is None
+
+
+FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "loader_model")
+
+
+def test_reference_loader_fixture():
+    """The directory the reference's loader test writes (create_test_model,
+    tests/test_model_loader.cu:52-191) read by the Python loader, with that
+    test's expectations (:199-284) and the packed words its pattern fixes:
+    {+1, -1, 0, 0} groups are bitmap 0x3 and signs 0b10 per group."""
+    m = load_model(FIXTURE, device="cpu")
+    c = m.config
+    assert (c.hidden_size, c.num_hidden_layers, c.num_attention_heads, c.num_key_value_heads,
+            c.intermediate_size, c.vocab_size, c.head_dim) == (8, 1, 1, 1, 16, 32, 8)
+    assert c.hidden_act == "relu2" and c.tie_word_embeddings
+    assert m.lm_head_weight is None and m.lm_head() is m.embed_tokens  # tied
+    assert torch.equal(m.embed_tokens.float(), torch.ones(32, 8))
+    assert torch.equal(m.final_norm, torch.ones(8))
+    L = m.layers[0]
+    assert torch.equal(L.input_layernorm, torch.ones(8))
+    assert torch.equal(L.post_attention_layernorm, torch.ones(8))
+    assert L.attn_sub_norm is None and L.ffn_sub_norm is None
+    assert (L.q_proj.rows, L.q_proj.cols, L.q_proj.gamma) == (8, 8, 0.5)
+    assert (L.gate_proj.rows, L.gate_proj.cols) == (16, 8)
+    assert (L.down_proj.rows, L.down_proj.cols) == (8, 16)
+    assert (L.q_proj.meta.view(-1) == 0x33).all() and (L.q_proj.values.view(-1) == 0xA).all()
+    assert (L.down_proj.meta.view(-1) == 0x3333).all()
+    assert (L.down_proj.values.view(-1) == 0xAA).all()
+    # unpacked rows are +1, -1, 0, 0 repeated
+    from spbitnet_amd import weights as Wt
+    dense = Wt.unpack(L.down_proj.meta.numpy().view(np.uint32),
+                      L.down_proj.values.numpy().view(np.uint32), 8, 16)
+    assert (dense == np.tile(np.array([1, -1, 0, 0], np.int8), (8, 4))).all()
+    assert m.total_gpu_bytes() > 0
+
+
+def _fixture_copy(tmp_path, edit):
+    import shutil
+    d = tmp_path / "model"
+    shutil.copytree(FIXTURE, d)
+    man = json.load(open(d / "manifest.json"))
+    edit(man["weights"])
+    json.dump(man, open(d / "manifest.json", "w"))
+    return str(d)
+
+
+def test_loader_rejects_missing_or_short_strides(tmp_path):
+    """meta_stride, values_stride and gamma are required (src/model.cu:107-109
+    reads them with entry.at()) and the strides must cover a row; a manifest
+    that understates them is rejected before any weight reaches a kernel."""
+    import pytest
+    cases = [
+        ("layers.0.mlp.down_proj", "meta_stride", None),
+        ("layers.0.mlp.down_proj", "values_stride", None),
+        ("layers.0.self_attn.o_proj", "gamma", None),
+        ("layers.0.mlp.down_proj", "meta_stride", 0),
+        ("layers.0.self_attn.q_proj", "values_stride", 0),
+    ]
+    for i, (name, key, val) in enumerate(cases):
+        def edit(w):
+            if val is None:
+                del w[name][key]
+            else:
+                w[name][key] = val
+        d = _fixture_copy(tmp_path / str(i), edit)
+        with pytest.raises(ValueError, match=name):
+            load_model(d, device="cpu")
