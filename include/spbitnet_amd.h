@@ -123,6 +123,22 @@ int spb_bitlinear_bf16(const uint32_t* meta, const uint32_t* values, const uint1
                        int values_row_stride, void* workspace, size_t workspace_size,
                        spb_stream_t stream);
 
+/* No counterpart in the reference: spb_bitlinear_* for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops or
+ * harnesses that forbid hipMalloc).  The workspace is a static device array
+ * of the library (spb_bitlinear_workspace_size(32768) bytes, one copy per
+ * GPU, held until the process ends); cols above 32768 are rejected.  No
+ * allocation happens in the call.  Every call on a GPU shares that GPU's
+ * copy: calls that overlap on one GPU (several streams or host threads)
+ * race and must be serialised by the caller.  Output bits equal
+ * spb_bitlinear_*'s. */
+int spb_bitlinear_f16_noalloc(const uint32_t* meta, const uint32_t* values, const uint16_t* x,
+                              uint16_t* output, float gamma, int rows, int cols,
+                              int meta_row_stride, int values_row_stride, spb_stream_t stream);
+int spb_bitlinear_bf16_noalloc(const uint32_t* meta, const uint32_t* values, const uint16_t* x,
+                               uint16_t* output, float gamma, int rows, int cols,
+                               int meta_row_stride, int values_row_stride, spb_stream_t stream);
+
 /* ---- Batched GEMM ---------------------------------------------------------------
  * Replaces the cuSPARSELt path CuSparseLtGemm(m,k,n) + execute
  * (reference include/spbitnet/cusparselt_backend.h:28-77,

@@ -45,6 +45,8 @@ SIGNATURES = {
     "spb_bitlinear_workspace_size": [_I],
     "spb_bitlinear_f16": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
     "spb_bitlinear_bf16": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "spb_bitlinear_f16_noalloc": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
+    "spb_bitlinear_bf16_noalloc": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
     # per-op inference kernels
     "spb_rms_norm_f16": [_P, _P, _P, _I, _F, _P],
     "spb_rms_norm_bf16": [_P, _P, _P, _I, _F, _P],

@@ -13,6 +13,7 @@
 // workspace's absmax.  Both orders give the reference's bits:
 //   q = clamp(rint(x * (absmax > 0 ? 127/absmax : 0)), -128, 127),
 //   out[r] = 16-bit(float(W q) * ((gamma * absmax) / 127)).
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -88,6 +89,75 @@ int bitlinear(const char* fn, const uint32_t* meta, const uint32_t* values, cons
                            static_cast<uint8_t*>(workspace), as_stream(stream));
 }
 
+// ---- allocation-free form -------------------------------------------------------
+// For callers that cannot allocate (code under HIP graph capture, serving
+// loops that forbid hipMalloc): the workspace is `scratch`, a file-scope
+// device array of workspace_bytes(kNoAllocMaxCols) bytes.  Each GPU the
+// library runs on holds its own copy until the process ends.  Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in
+// symbol, not a device address): the entry point looks up the copy's device
+// address once per device with hipGetSymbolAddress, with that device
+// current, and uses that pointer.  Every call on a GPU shares its copy, which
+// keeps the last call's contents; nothing in it needs to start at zero (each
+// call writes the absmax and every plane word the GEMV reads before reading
+// them).  Calls that overlap on one GPU (different streams, host threads)
+// race on it.
+constexpr int kNoAllocMaxCols = kMaxPlaneCols;  // 32768
+constexpr size_t kScratchBytes = kAbsmaxBytes + 32 * (kNoAllocMaxCols / 32);
+static_assert(kNoAllocMaxCols % 32 == 0, "planes of the largest vector fill whole groups");
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[kScratchDevices] = {};
+
+// The device address of the current device's copy of `scratch` (looked up on
+// the first call on each device); nullptr with the error recorded on failure.
+uint8_t* scratch_on_current_device(const char* fn, int* rc) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error("%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+        *rc = static_cast<int>(e);
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kScratchDevices) {
+        *rc = invalid("%s: device %d beyond the %d devices the scratch table covers", fn, dev,
+                      kScratchDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            set_error("%s: hipGetSymbolAddress(scratch): %s", fn, hipGetErrorString(e));
+            *rc = static_cast<int>(e != hipSuccess ? e : hipErrorInvalidSymbol);
+            return nullptr;
+        }
+        g_scratch[dev] = static_cast<uint8_t*>(ptr);
+    }
+    return g_scratch[dev];
+}
+
+template <class T>
+int bitlinear_noalloc(const char* fn, const uint32_t* meta, const uint32_t* values,
+                      const uint16_t* x, uint16_t* output, float gamma, int rows, int cols,
+                      int ms, int vs, spb_stream_t stream) {
+    clear_error();
+    if (int e = check_bitlinear(fn, meta, values, x, output, rows, cols, ms, vs)) return e;
+    if (rows == 0 || cols == 0) return 0;
+    if (cols > kNoAllocMaxCols)
+        return invalid("%s: cols=%d exceeds the %d columns the static scratch holds (use "
+                       "spb_bitlinear_* with a workspace)", fn, cols, kNoAllocMaxCols);
+    int rc = 0;
+    uint8_t* ws = scratch_on_current_device(fn, &rc);
+    if (!ws) return rc;
+    return bitlinear_ws<T>(fn, meta, values, x, output, gamma, rows, cols, ms, vs, ws,
+                           as_stream(stream));
+}
+
 }  // namespace
 }  // namespace spb
 
@@ -109,4 +179,20 @@ extern "C" int spb_bitlinear_bf16(const uint32_t* meta, const uint32_t* values, 
                                   size_t workspace_size, spb_stream_t stream) {
     return bitlinear<BF16>("spb_bitlinear_bf16", meta, values, x, output, gamma, rows, cols,
                            meta_row_stride, values_row_stride, workspace, workspace_size, stream);
+}
+
+extern "C" int spb_bitlinear_f16_noalloc(const uint32_t* meta, const uint32_t* values,
+                                         const uint16_t* x, uint16_t* output, float gamma,
+                                         int rows, int cols, int meta_row_stride,
+                                         int values_row_stride, spb_stream_t stream) {
+    return bitlinear_noalloc<F16>("spb_bitlinear_f16_noalloc", meta, values, x, output, gamma,
+                                  rows, cols, meta_row_stride, values_row_stride, stream);
+}
+
+extern "C" int spb_bitlinear_bf16_noalloc(const uint32_t* meta, const uint32_t* values,
+                                          const uint16_t* x, uint16_t* output, float gamma,
+                                          int rows, int cols, int meta_row_stride,
+                                          int values_row_stride, spb_stream_t stream) {
+    return bitlinear_noalloc<BF16>("spb_bitlinear_bf16_noalloc", meta, values, x, output, gamma,
+                                   rows, cols, meta_row_stride, values_row_stride, stream);
 }
