@@ -376,6 +376,42 @@ int spb_engine_decode_steps(spb_engine* engine, int steps);
 /* Device buffers: logits float32 [vocab], tokens int32 [max_seq + 1]. */
 int spb_engine_buffers(const spb_engine* engine, const float** logits, const int** tokens);
 
+/* ---- batched decode engine --------------------------------------------------
+ * No reference counterpart: the reference decodes one sequence per engine
+ * (InferenceEngine::forward, src/inference.cu:123-283).  BASELINE config 4
+ * decodes several sequences at once; this engine steps `batch` independent
+ * sequences per HIP-graph replay, each with its own KV cache of max_seq
+ * positions, position and token buffer.  Every value of a sequence's step is
+ * computed by the same device code, in the same order, as the bs=1 engine,
+ * so each sequence's greedy tokens equal those of spb_engine_generate on
+ * that sequence alone.  Same model constraints as spb_engine_create, plus
+ * hidden_size <= 4096 (the batched LM head keeps 8 normalised vectors in
+ * LDS); 1 <= batch <= 1024. */
+typedef struct spb_batch_engine spb_batch_engine;
+int spb_batch_engine_create(const spb_model_config* config, const spb_transformer_layer* layers,
+                            const uint16_t* embed_tokens, const uint16_t* lm_head,
+                            const float* final_norm, int max_seq, int batch,
+                            spb_batch_engine** engine);
+int spb_batch_engine_destroy(spb_batch_engine* engine);
+int spb_batch_engine_set_stream(spb_batch_engine* engine, spb_stream_t stream);
+/* Greedy generation of n_seq <= batch sequences: prompts concatenated,
+ * prompt_lens[n_seq] (each >= 1, prompt + n_new <= max_seq).  Each prompt's
+ * tokens before its last are prefilled through the layers into the
+ * sequence's cache (the batched prefill of spb_engine_generate); then n_new
+ * graph steps each advance every sequence by one token (src/main.cpp:133-155
+ * per sequence).  out_tokens [n_seq][n_new] (-1 after a sequence stopped at
+ * EOS when stop_at_eos), n_generated [n_seq] (nullable).  The host waits once. */
+int spb_batch_engine_generate(spb_batch_engine* engine, const int* prompts,
+                              const int* prompt_lens, int n_seq, int n_new, int stop_at_eos,
+                              int* out_tokens, int* n_generated);
+/* `steps` more batched steps continuing the current states (timing loops);
+ * no host synchronisation. */
+int spb_batch_engine_decode_steps(spb_batch_engine* engine, int steps);
+/* Device buffers: logits float32 [batch][vocab], tokens int32
+ * [batch][max_seq + 1]. */
+int spb_batch_engine_buffers(const spb_batch_engine* engine, const float** logits,
+                             const int** tokens);
+
 /* ---- model loading ----------------------------------------------------------
  * Model::load (reference include/spbitnet/model.h:99-103, src/model.cu:72-311)
  * for the on-disk format of python/convert_model.py (docs/compression_format.md

@@ -47,6 +47,7 @@ def lib():
         L.spbo_unpack.argtypes = [_P, _P, _I, _I, _I, _I, _P]
         L.spbo_gemv.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I]
         L.spbo_gemm.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I]
+        L.spbo_dense_mac.argtypes = [_P, _P, _P, _I, _I]
         L.spbo_absmax.argtypes = [_P, _I]
         L.spbo_absmax.restype = _F
         L.spbo_quant_scale.argtypes = [_F]
@@ -152,6 +153,16 @@ def gemv(meta, values, x, rows, cols) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.int8)
     y = np.zeros(rows, np.int32)
     lib().spbo_gemv(_p(meta), _p(values), _p(x), _p(y), rows, cols, meta.shape[-1], values.shape[-1])
+    return y
+
+
+def dense_mac(dense: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """y = dense @ x in int32 (the MAC of cpu_sparse_gemv without its unpack)."""
+    dense = np.ascontiguousarray(dense, dtype=np.int8)
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    rows, cols = dense.shape
+    y = np.zeros(rows, np.int32)
+    lib().spbo_dense_mac(_p(dense), _p(x), _p(y), rows, cols)
     return y
 
 
@@ -351,7 +362,10 @@ class EngineOracle:
 
     def __del__(self):
         if getattr(self, "_e", None):
-            _elib().spbo_engine_free(self._e)
+            try:
+                _elib().spbo_engine_free(self._e)
+            except Exception:  # interpreter shutdown: the module is gone
+                pass
             self._e = None
 
     def reset(self):

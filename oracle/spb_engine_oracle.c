@@ -136,6 +136,7 @@ typedef struct {
     float *x, *xb, *vec, *qkv, *o, *gu, *attn, *h_in, *m_in;
     int8_t* q8;
     int32_t* acc;
+    float* logit_buf; /* [V] */
 } spbo_engine;
 
 /* absmax, quantise (spb_oracle.c rules), GEMV, dequantise to bf16 with gamma;
@@ -220,6 +221,7 @@ spbo_engine* spbo_engine_new(const int* icfg, const float* fcfg, const uint32_t*
     e->m_in = (float*)calloc((size_t)I, 4);
     e->q8 = (int8_t*)calloc((size_t)mx, 1);
     e->acc = (int32_t*)calloc((size_t)mx, 4);
+    e->logit_buf = (float*)calloc((size_t)e->V, 4);
     e->pos = 0;
     return e;
 }
@@ -245,6 +247,7 @@ void spbo_engine_free(spbo_engine* e) {
     free(e->m_in);
     free(e->q8);
     free(e->acc);
+    free(e->logit_buf);
     free(e);
 }
 
@@ -402,11 +405,12 @@ int spbo_engine_step(spbo_engine* e, int token, float* logits) {
         const float dq3 = spbo_dequant_scale(L->p[6].gamma, a3);
         for (int r = 0; r < H; ++r) e->x[r] = bfr(bfr((float)acc[r] * dq3) + e->xb[r]);
     }
-    /* final norm and LM head (:268-277; half_gemv_kernel :488-531) */
+    /* final norm and LM head (:268-277; half_gemv_kernel :488-531); rows are
+     * independent, so they run in parallel (OpenMP) and the argmax follows */
     rmsnorm(e->x, e->final_norm, H, eps, LM_THREADS, vec);
     const int nch = H / 8;
-    int best = -1;
-    float bv = -INFINITY;
+    float* lg = e->logit_buf;
+#pragma omp parallel for schedule(static) if ((long)e->V * H >= (1L << 22))
     for (int r = 0; r < e->V; ++r) {
         const uint16_t* w = e->lm + (size_t)r * H;
         float lanes[64];
@@ -416,10 +420,14 @@ int spbo_engine_step(spbo_engine* e, int token, float* logits) {
                 for (int k = 0; k < 8; ++k) a = fmaf(bf2f(w[8 * c + k]), vec[8 * c + k], a);
             lanes[ln] = a;
         }
-        const float lg = tree64(lanes);
-        if (logits) logits[r] = lg;
-        if (lg > bv) {
-            bv = lg;
+        lg[r] = tree64(lanes);
+    }
+    int best = -1;
+    float bv = -INFINITY;
+    for (int r = 0; r < e->V; ++r) {
+        if (logits) logits[r] = lg[r];
+        if (lg[r] > bv) {
+            bv = lg[r];
             best = r;
         }
     }

@@ -140,19 +140,56 @@ void spbo_unpack(const uint32_t* meta, const uint32_t* values, int rows, int col
 
 /*
  * cpu_sparse_gemv (tests/test_sparse_ternary.cu:17-33): unpack to dense int8,
- * then a dense int32 multiply-accumulate.  |acc| <= (cols/2)*128 < 2^31.
+ * then a dense int32 multiply-accumulate.  Computed here group by group on
+ * the packed words, each group decoded exactly as spbo_unpack decodes it
+ * (kept positions ascending, sign bit nz of the group for the nz-th kept
+ * position), without the dense copy: the int32 sum is exact, so the result
+ * is the unpack-then-MAC value bit for bit.  |acc| <= (cols/2)*128 < 2^31.
+ * Rows run in parallel (OpenMP) for large matrices; each row's sum is
+ * independent.
  */
 void spbo_gemv(const uint32_t* meta, const uint32_t* values, const int8_t* x,
                int32_t* y, int rows, int cols, int ms, int vs) {
-    int8_t* dense = (int8_t*)malloc((size_t)rows * cols + 1);
-    spbo_unpack(meta, values, rows, cols, ms, vs, dense);
+    const long work = (long)rows * cols;
+#pragma omp parallel for schedule(static) if (work >= (1L << 22))
     for (int r = 0; r < rows; ++r) {
+        const uint32_t* mr = meta + (size_t)r * ms;
+        const uint32_t* vr = values + (size_t)r * vs;
         int32_t s = 0;
-        for (int c = 0; c < cols; ++c)
-            s += (int32_t)dense[(size_t)r * cols + c] * (int32_t)x[c];
+        for (int g = 0; g < cols / 4; ++g) {
+            const uint32_t bitmap = (mr[g / 8] >> ((g % 8) * 4)) & 0xFu;
+            const uint32_t signs = (vr[g / 16] >> ((g % 16) * 2)) & 0x3u;
+            if (__builtin_popcount(bitmap) == 2) {
+                /* the format's case: lower kept position p0 takes sign bit 0,
+                 * the higher p1 sign bit 1; -v = (v ^ -1) + 1 */
+                const int p0 = __builtin_ctz(bitmap), p1 = __builtin_ctz(bitmap & (bitmap - 1));
+                const int32_t m0 = -(int32_t)(signs & 1u), m1 = -(int32_t)(signs >> 1);
+                s += (((int32_t)x[4 * g + p0] ^ m0) - m0) + (((int32_t)x[4 * g + p1] ^ m1) - m1);
+                continue;
+            }
+            int nz = 0; /* malformed bitmaps: spbo_unpack's decode, position by position */
+            for (int i = 0; i < 4; ++i) {
+                if (!(bitmap & (1u << i))) continue;
+                const int32_t xv = (int32_t)x[4 * g + i];
+                s += ((signs >> nz) & 1u) ? -xv : xv;
+                ++nz;
+            }
+        }
         y[r] = s;
     }
-    free(dense);
+}
+
+/*
+ * The multiply-accumulate half of cpu_sparse_gemv (tests/test_sparse_ternary.cu:
+ * 26-32) on an already unpacked int8 matrix: the CPU baseline timed without
+ * the per-call unpack.
+ */
+void spbo_dense_mac(const int8_t* dense, const int8_t* x, int32_t* y, int rows, int cols) {
+    for (int r = 0; r < rows; ++r) {
+        int32_t s = 0;
+        for (int c = 0; c < cols; ++c) s += (int32_t)dense[(size_t)r * cols + c] * (int32_t)x[c];
+        y[r] = s;
+    }
 }
 
 /*

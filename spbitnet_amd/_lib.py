@@ -82,6 +82,12 @@ SIGNATURES = {
     "spb_engine_decode_steps": [_P, _I],
     "spb_engine_set_prefill_batch": [_P, _I],
     "spb_engine_buffers": [_P, _P, _P],
+    "spb_batch_engine_create": [_P, _P, _P, _P, _P, _I, _I, _P],
+    "spb_batch_engine_destroy": [_P],
+    "spb_batch_engine_set_stream": [_P, _P],
+    "spb_batch_engine_generate": [_P, _P, _P, _I, _I, _I, _P, _P],
+    "spb_batch_engine_decode_steps": [_P, _I],
+    "spb_batch_engine_buffers": [_P, _P, _P],
     "spb_model_load": [ctypes.c_char_p, _P],
     "spb_model_destroy": [_P],
     "spb_model_info": [_P, _P, _P, _P, _P, _P, _P],

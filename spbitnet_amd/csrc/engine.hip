@@ -428,10 +428,13 @@ struct InputNorm {
     float eps;
     int n;
     int writer = 0;  // the block that stores the residual stream (layer 0)
-    // prefill: token t of a batch (x and x_out rows of `stride` elements)
+    long tok_stride = 0;  // batched decode: token buffer of sequence t at tokens + t * tok_stride
+    // prefill / batched decode: token t of a batch (x and x_out rows of
+    // `stride` elements)
     __device__ void at(int t, long stride) {
         x += t * stride;
         x_out += t * stride;
+        tokens += t * tok_stride;
         writer = t;
     }
     struct Regs {
@@ -987,12 +990,18 @@ struct QkvRopeSink {
     float2 pre_cs;
     const float2* rope_tab;  // prefill: the [max_seq][hd/2] table and the batch's first position
     int rope_pos0;
-    // prefill: token t of a batch at position rope_pos0 + t (its own state
-    // record; out rows of `stride` elements)
+    long kv_stride;  // batched decode: cache elements per sequence (0 in the prefill)
+    // token t of a batch (its own state record; out rows of `stride`
+    // elements).  Prefill (rope_tab set): one sequence, token t at position
+    // rope_pos0 + t.  Batched decode (rope_tab null): sequence t, with its
+    // own RoPE row (cur_rope + t * hd/2) and its own KV cache (kv_stride).
     __device__ void at(int t, long stride) {
         out += t * stride;
         st += t;
-        cur_rope = rope_tab + static_cast<long>(rope_pos0 + t) * (hd >> 1);
+        kc += t * kv_stride;
+        vc += t * kv_stride;
+        cur_rope = rope_tab ? rope_tab + static_cast<long>(rope_pos0 + t) * (hd >> 1)
+                            : cur_rope + static_cast<long>(t) * (hd >> 1);
     }
     __device__ void offset(long) {}
     __device__ void prepare() {}
@@ -1316,6 +1325,86 @@ __global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
     }
 }
 
+// Batched decode form: one block per (64-position split, kv head, sequence
+// b = blockIdx.z), each sequence with its own decode state (st + b), query
+// (qkv + b * qkv_stride), KV cache (kc / vc + b * kv_stride) and partials
+// (after those of sequence b - 1).  Unlike the bs=1 kernel it reads the
+// sequence's position before loading K and V: with many sequences most
+// blocks lie past their sequence's position (splits up to max_seq), and
+// their loads would be wasted.  The per-split arithmetic is attention_split,
+// as in the bs=1 and prefill kernels.
+template <int HD, int G>
+__global__ __launch_bounds__(kAttnThreads) void attention_batch_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, float* __restrict__ pm, float* __restrict__ pl,
+    float* __restrict__ pacc, const EngineState* __restrict__ st, int max_seq, int S,
+    float scale, int qkv_stride, long kv_stride) {
+    constexpr int kU = HD / 8;
+    constexpr int kQU = kU / 4;
+    constexpr int kPG = kAttnSplit / G;
+    constexpr int kVRow = HD / 2 + 1;
+    __shared__ __align__(16) float qs[G][HD];
+    __shared__ uint32_t vs[kAttnSplit][kVRow];
+    __shared__ __align__(16) float sc[G][kAttnSplit];
+    __shared__ float hmax[G], hsum[G];
+    const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int j0 = s * kAttnSplit;
+    const int tid = threadIdx.x;
+    st += b;
+    const int done = state_done(st), pos = state_pos(st);
+    if (done || j0 > pos) return;  // uniform
+    kc += b * kv_stride;
+    vc += b * kv_stride;
+    qkv += static_cast<long>(b) * qkv_stride;
+    const long hs = static_cast<long>(gridDim.y) * G * S;
+    pm += b * hs;
+    pl += b * hs;
+    pacc += b * hs * HD;
+    const long cache0 = static_cast<long>(kvh) * max_seq * HD;
+    const int jmax = max_seq - 1;
+    const int qq = tid & 3, slot = tid >> 2;
+    const int sg = slot / kPG, pb = (slot - sg * kPG) * G;
+    uint4 kq[G][kQU];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const int j = j0 + pb + i <= jmax ? j0 + pb + i : jmax;
+        const uint4* kr =
+            reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) + qq * kQU;
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) kq[i][u] = kr[u];
+    }
+    constexpr int kVPer = kAttnSplit * kU / kAttnThreads;
+    uint4 vraw[kVPer];
+#pragma unroll
+    for (int t = 0; t < kVPer; ++t) {
+        const int idx = tid + t * kAttnThreads;
+        const int jj = idx / kU, c = idx - jj * kU;
+        const int j = j0 + jj <= jmax ? j0 + jj : jmax;
+        vraw[t] = reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
+    }
+    uint4 qraw = make_uint4(0, 0, 0, 0);
+    const bool has_q = tid < G * kU;
+    if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + (kvh * G) * HD)[tid];
+#pragma unroll
+    for (int t = 0; t < kVPer; ++t) {
+        const int idx = tid + t * kAttnThreads;
+        const int jj = idx / kU, c = idx - jj * kU;
+        uint32_t* row = &vs[jj][4 * c];
+        row[0] = vraw[t].x;
+        row[1] = vraw[t].y;
+        row[2] = vraw[t].z;
+        row[3] = vraw[t].w;
+    }
+    if (has_q) {
+        float f[8];
+        unpack_bf16x8(qraw, f);
+        store_f8(&qs[tid / kU][8 * (tid % kU)], f);
+    }
+    const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
+    __syncthreads();
+    attention_split<HD, G>(kq, qs, vs, sc, hmax, hsum, jn, scale, s, kvh, S, pm, pl, pacc);
+}
+
 // ---- batched prefill ---------------------------------------------------------------------
 //
 // The prompt's tokens (all but the last) go through a layer together: the
@@ -1634,6 +1723,242 @@ LmKernel lm_head_for(int H) {
     return (H % 512 == 0) ? lm_head_for_nc<true>(nc) : lm_head_for_nc<false>(nc);
 }
 
+// Batched decode: the LM head for a group of gn <= kLmGroup sequences
+// (g0 .. g0 + gn - 1) of a batch.  Every row is computed exactly as
+// lm_head_kernel computes it (final RMSNorm in the unit order of kLmBlock
+// threads; lane l takes the 8-element chunks l, l + 64, ... of the row with
+// fma in element order; the 64-lane tree), once per sequence of the group,
+// so each sequence's logits equal those of a bs=1 step bit for bit.  The
+// normalised vectors of the group sit in LDS as float [gn][H]; a row's
+// weights are unpacked once and used for every sequence.  Per-sequence
+// argmax (lowest index among maxima) and decode-state update by the last
+// block to finish (ticket of the group's first sequence), as in the bs=1
+// kernel; sequences whose state is done are not updated.
+constexpr int kLmGroup = 8;          // sequences per batched LM-head launch (at most)
+constexpr int kLmBatchMaxRows = 512;  // rows per block (grid >= vocab / 512)
+
+template <int NC, bool kFull>
+__global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
+    const float* __restrict__ wn, float eps, float* __restrict__ logits,
+    float* __restrict__ part_v, int* __restrict__ part_i, EngineState* __restrict__ st,
+    int* __restrict__ tokens, long tok_stride, int V, int H, const float2* __restrict__ rope,
+    float2* __restrict__ cur_rope, int half_hd, int max_seq, int rbase, int rrem, int g0,
+    int gn) {
+    constexpr int kWaves = kLmBlock / kWave;
+    extern __shared__ __align__(16) float lds[];
+    float* xs = lds;                                          // [gn][H]
+    float* lg = lds + static_cast<long>(kLmGroup) * H;        // [gn][kLmBatchMaxRows]
+    __shared__ float red[kLmGroup][kWaves];
+    __shared__ float wv[kWaves];
+    __shared__ int wi[kWaves];
+    __shared__ int last;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int nch = H >> 3;
+    const int blk = blockIdx.x;
+    const long b0 = static_cast<long>(blk) * rbase + (blk < rrem ? blk : rrem);
+    const long b1 = b0 + rbase + (blk < rrem ? 1 : 0);
+    const long n = (b1 - b0 - wave + kWaves - 1) / kWaves;
+    const long i_last = n > 0 ? n - 1 : 0;
+    auto row_of = [&](long i) { return b0 + wave + (i <= i_last ? i : i_last) * kWaves; };
+    auto load_row = [&](long i, uint4 (&w)[NC]) {
+        const long r = row_of(i);
+        const uint4* wr = reinterpret_cast<const uint4*>(W + (r < V ? r : V - 1) * H);
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+            const int c = lane + k * kWave;
+            if (kFull)
+                w[k] = nt_load(wr + c);
+            else
+                w[k] = c < nch ? nt_load(wr + c) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    uint4 wa[NC], wb[NC];
+    load_row(0, wa);
+    // final RMSNorm of each sequence of the group (lm_head_kernel's order)
+    constexpr bool kOne = NC * kWave <= kUnits * kLmBlock;
+    for (int g = 0; g < gn; ++g) {
+        const uint16_t* xg = x + static_cast<long>(g0 + g) * H;
+        HeldWeights<kLmBlock> hw;
+        HeldUnits<kLmBlock> hx;
+        hx.load(xg, H >> 3, tid);
+        hw.load(wn, H >> 3, tid);
+        const float ss = load_bf16_sumsq<kLmBlock, kOne>(xg, xs + static_cast<long>(g) * H, H >> 3,
+                                                         tid, nullptr, hx);
+        const float inv = inv_rms(block_sum<kLmBlock>(ss, red[g]), H, eps);
+        hw.template apply<kOne>(xs + static_cast<long>(g) * H, wn, inv, H >> 3, tid);
+    }
+    __syncthreads();
+
+    float best[kLmGroup];
+    int best_i[kLmGroup];
+#pragma unroll
+    for (int g = 0; g < kLmGroup; ++g) {
+        best[g] = -INFINITY;
+        best_i[g] = 0x7FFFFFFF;
+    }
+    auto reduce_row = [&](long i, const uint4 (&w)[NC]) {
+        float wf[NC][8];
+#pragma unroll
+        for (int k = 0; k < NC; ++k) unpack_bf16x8(w[k], wf[k]);
+        const long r = row_of(i);
+#pragma unroll
+        for (int g = 0; g < kLmGroup; ++g) {
+            if (g < gn) {
+                const float* xg = xs + static_cast<long>(g) * H;
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < NC; ++k) {
+                    const int c = lane + k * kWave;
+                    if (kFull || c < nch) {
+                        float xv[8];
+                        load_f8(xg + 8 * c, xv);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[k][e], xv[e], acc);
+                    }
+                }
+                acc = wave_sum_tree(acc);
+                if (lane == 0) lg[g * kLmBatchMaxRows + (r - b0)] = acc;
+                if (acc > best[g]) {  // rows ascend within a wave: the first maximum stays
+                    best[g] = acc;
+                    best_i[g] = static_cast<int>(r);
+                }
+            }
+        }
+    };
+    long i = 0;
+    for (long p = 0; p < n / 2; ++p, i += 2) {
+        load_row(i + 1, wb);
+        __builtin_amdgcn_sched_barrier(0);
+        reduce_row(i, wa);
+        load_row(i + 2, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        reduce_row(i + 1, wb);
+    }
+    if (n > 0 && (n & 1)) reduce_row(i, wa);
+    __syncthreads();
+    for (int g = 0; g < gn; ++g)
+        for (long j = tid; j < b1 - b0; j += kLmBlock)
+            logits[static_cast<long>(g0 + g) * V + b0 + j] = lg[g * kLmBatchMaxRows + j];
+    // per-sequence block maxima
+#pragma unroll
+    for (int g = 0; g < kLmGroup; ++g) {
+        if (g < gn) {
+            if (lane == 0) {
+                wv[wave] = best[g];
+                wi[wave] = best_i[g];
+            }
+            __syncthreads();
+            if (tid == 0) {
+                float bv = wv[0];
+                int bi = wi[0];
+                for (int w = 1; w < kWaves; ++w)
+                    if (wv[w] > bv || (wv[w] == bv && wi[w] < bi)) {
+                        bv = wv[w];
+                        bi = wi[w];
+                    }
+                part_v[static_cast<long>(g0 + g) * gridDim.x + blockIdx.x] = bv;
+                part_i[static_cast<long>(g0 + g) * gridDim.x + blockIdx.x] = bi;
+            }
+            __syncthreads();
+        }
+    }
+    if (tid == 0) {
+        __threadfence();
+        const unsigned t = atomicAdd(&st[g0].ticket, 1u);
+        last = t == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    for (int g = 0; g < gn; ++g) {
+        EngineState* sg = st + g0 + g;
+        const float* pv = part_v + static_cast<long>(g0 + g) * gridDim.x;
+        const int* pi = part_i + static_cast<long>(g0 + g) * gridDim.x;
+        float bv = -INFINITY;
+        int bi = 0x7FFFFFFF;
+        for (int k = tid; k < static_cast<int>(gridDim.x); k += kLmBlock) {
+            const float v = __hip_atomic_load(&pv[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int ii = __hip_atomic_load(&pi[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (v > bv || (v == bv && ii < bi)) {
+                bv = v;
+                bi = ii;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, kWave);
+            const int oi = __shfl_xor(bi, off, kWave);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) {
+            wv[wave] = bv;
+            wi[wave] = bi;
+        }
+        __syncthreads();
+        const int done = sg->done, pos_old = sg->pos;
+        __syncthreads();  // every thread has read the state before thread 0 changes it
+        if (done) continue;  // uniform
+        if (tid == 0) {
+            for (int w = 1; w < kWaves; ++w)
+                if (wv[w] > bv || (wv[w] == bv && wi[w] < bi)) {
+                    bv = wv[w];
+                    bi = wi[w];
+                }
+            const int tok = bi == 0x7FFFFFFF ? 0 : bi;  // all-NaN logits: token 0
+            const int nxt = pos_old + 1;
+            int* tk = tokens + static_cast<long>(g0 + g) * tok_stride;
+            if (nxt >= sg->prompt_len && nxt < sg->limit) {
+                tk[nxt] = tok;
+                sg->generated += 1;
+                if (sg->stop_eos && tok == sg->eos) sg->done = 1;
+            }
+            sg->pos = nxt;
+            if (nxt >= sg->limit) sg->done = 1;
+        }
+        const int p = pos_old + 1 < max_seq ? pos_old + 1 : max_seq - 1;
+        float2* cr = cur_rope + static_cast<long>(g0 + g) * half_hd;
+        for (int k = tid; k < half_hd; k += kLmBlock) cr[k] = rope[static_cast<long>(p) * half_hd + k];
+        __syncthreads();  // wv / wi are reused by the next sequence
+    }
+    if (tid == 0) st[g0].ticket = 0u;
+}
+
+typedef void (*LmBatchKernel)(const uint16_t*, const uint16_t*, const float*, float, float*,
+                              float*, int*, EngineState*, int*, long, int, int, const float2*,
+                              float2*, int, int, int, int, int, int);
+
+template <bool kFull>
+LmBatchKernel lm_head_batch_for_nc(int nc) {
+    switch (nc) {
+        case 1: return lm_head_batch_kernel<1, kFull>;
+        case 2: return lm_head_batch_kernel<2, kFull>;
+        case 3: return lm_head_batch_kernel<3, kFull>;
+        case 4: return lm_head_batch_kernel<4, kFull>;
+        case 5: return lm_head_batch_kernel<5, kFull>;
+        case 6: return lm_head_batch_kernel<6, kFull>;
+        case 7: return lm_head_batch_kernel<7, kFull>;
+        default: return lm_head_batch_kernel<8, kFull>;
+    }
+}
+
+// The batched LM head holds the group's normalised vectors in LDS, so it
+// takes hidden sizes up to kLmBatchMaxH (NC <= 8 chunks per lane).
+constexpr int kLmBatchMaxH = 4096;
+
+LmBatchKernel lm_head_batch_for(int H) {
+    const int nc = (H / 8 + kWave - 1) / kWave;
+    return (H % 512 == 0) ? lm_head_batch_for_nc<true>(nc) : lm_head_batch_for_nc<false>(nc);
+}
+
+size_t lm_head_batch_lds(int H) {
+    return (static_cast<size_t>(kLmGroup) * H + static_cast<size_t>(kLmGroup) * kLmBatchMaxRows) *
+           sizeof(float);
+}
+
 // ---- random-init weights (model generation on the device) ------------------------
 
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
@@ -1730,6 +2055,46 @@ T* dev_alloc(size_t n, std::vector<void*>& owned) {
     if (hipMalloc(&p, n * sizeof(T) < 16 ? 16 : n * sizeof(T)) != hipSuccess) return nullptr;
     owned.push_back(p);
     return static_cast<T*>(p);
+}
+
+// Buffers of the batched prefill (chunk tokens per pass).
+struct PrefillBufs {
+    int8_t* x = nullptr;     // [chunk][max cols] int8 activations
+    float* amax = nullptr;   // [chunk]
+    int32_t* y[3] = {nullptr, nullptr, nullptr};  // [chunk][max rows] GEMM outputs
+    uint16_t *qkv = nullptr, *o = nullptr, *r = nullptr, *r2 = nullptr, *gu = nullptr;
+    float *pm = nullptr, *pl = nullptr, *pacc = nullptr;
+    EngineState* st = nullptr;  // [chunk] one decode-state record per token
+    int chunk = 0;  // tokens per prefill pass
+};
+
+// The batched prefill's buffers: up to kPrefillChunk tokens per pass, fewer
+// when the split partials of a pass would exceed kPrefillPartialBytes; or,
+// with tokens > 0, exactly that many (the batched decode step's buffers).
+bool alloc_prefill(PrefillBufs& pf, const spb_model_config& cfg, int S, std::vector<void*>& own,
+                   int tokens = 0) {
+    const int H = cfg.hidden_size, nh = cfg.num_attention_heads, hd = cfg.head_dim;
+    const int I = cfg.intermediate_size, kvdim = cfg.num_key_value_heads * hd;
+    const long part = static_cast<long>(nh) * S * (hd + 2) * 4;  // bytes per token
+    long c = kPrefillPartialBytes / part;
+    c = c < kPrefillChunk ? c : kPrefillChunk;
+    if (tokens > 0) c = tokens;
+    pf.chunk = static_cast<int>(c > 0 ? c : 1);
+    const size_t C = static_cast<size_t>(pf.chunk);
+    const size_t xmax = static_cast<size_t>(std::max(std::max(H, I), nh * hd));
+    const size_t ymax = static_cast<size_t>(std::max(std::max(nh * hd, kvdim), std::max(H, I)));
+    return (pf.x = dev_alloc<int8_t>(C * xmax, own)) && (pf.amax = dev_alloc<float>(C, own)) &&
+           (pf.y[0] = dev_alloc<int32_t>(C * ymax, own)) &&
+           (pf.y[1] = dev_alloc<int32_t>(C * ymax, own)) &&
+           (pf.y[2] = dev_alloc<int32_t>(C * ymax, own)) &&
+           (pf.qkv = dev_alloc<uint16_t>(C * (nh * hd + 2 * kvdim), own)) &&
+           (pf.o = dev_alloc<uint16_t>(C * H, own)) && (pf.r = dev_alloc<uint16_t>(C * H, own)) &&
+           (pf.r2 = dev_alloc<uint16_t>(C * H, own)) &&
+           (pf.gu = dev_alloc<uint16_t>(C * 2 * I, own)) &&
+           (pf.pm = dev_alloc<float>(C * nh * S, own)) &&
+           (pf.pl = dev_alloc<float>(C * nh * S, own)) &&
+           (pf.pacc = dev_alloc<float>(C * nh * S * hd, own)) &&
+           (pf.st = dev_alloc<EngineState>(C, own));
 }
 
 SegWeights seg_weights(const spb_sparse_linear* a, const spb_sparse_linear* b,
@@ -1840,6 +2205,133 @@ void launch_projection(const W& wt, const P& p, const EngineState* st, Sink sink
     }
 }
 
+
+// What a prefill pass reads of the model and the sequence it fills: every
+// layer's KV cache at kcache[l] + kv_off, the sequence's token buffer.
+struct PrefillTarget {
+    const spb_model_config* cfg;
+    const std::vector<spb_transformer_layer>* layers;
+    const uint16_t* embed;
+    const float2* rope;
+    int max_seq, S;
+    const std::vector<uint16_t*>* kcache;
+    const std::vector<uint16_t*>* vcache;
+    long kv_off;
+    const int* tokens;
+};
+
+// Positions pos0 .. pos0 + c - 1 of one sequence (t.tokens holds their ids)
+// through every layer, c <= pf.chunk: the KV cache of those positions as c
+// decode steps would write it.  Returns a HIP error or hipSuccess.
+hipError_t enqueue_prefill_pass(const PrefillTarget& t, const PrefillBufs& pf, int pos0, int c,
+                            hipStream_t s) {
+const spb_model_config& cfg = *t.cfg;
+const std::vector<spb_transformer_layer>& layers = *t.layers;
+const uint16_t* embed = t.embed;
+const int* tokens = t.tokens;
+const int max_seq = t.max_seq, S = t.S;
+const float2* rope = t.rope;
+auto kcache = [&](size_t l) { return (*t.kcache)[l] + t.kv_off; };
+auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
+    const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
+    const int nkv = cfg.num_key_value_heads, H = cfg.hidden_size;
+    const int I = cfg.intermediate_size, kvdim = nkv * hd, qrows = nh * hd;
+    const float eps = cfg.rms_norm_eps;
+    const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+    std::vector<EngineState> hs(c);
+    for (int t = 0; t < c; ++t) {
+        hs[t] = EngineState{};
+        hs[t].pos = pos0 + t;
+        hs[t].prompt_len = max_seq;
+        hs[t].limit = max_seq;
+    }
+    hipError_t err = hipMemcpyAsync(pf.st, hs.data(), sizeof(EngineState) * c,
+                                    hipMemcpyHostToDevice, s);
+    if (err == hipSuccess) err = hipStreamSynchronize(s);  // hs is on this frame
+    if (err != hipSuccess) return err;
+    auto gemm = [&](const spb_sparse_linear& w, int32_t* y) {
+        return spb_sparse_ternary_gemm(w.meta, w.values, pf.x, y, w.rows, w.cols, c,
+                                       w.meta_stride, w.values_stride, s);
+    };
+    for (size_t l = 0; l < layers.size(); ++l) {
+        const spb_transformer_layer& L = layers[l];
+        {
+            InputNorm p{pf.r, l == 0 ? embed : nullptr, tokens, pf.r, L.input_layernorm, eps,
+                        H};
+            launch_prefill_producer(p, H, pf.st, H, c, pf.x, pf.amax, s);
+        }
+        if (gemm(L.q_proj, pf.y[0]) || gemm(L.k_proj, pf.y[1]) || gemm(L.v_proj, pf.y[2]))
+            return hipErrorLaunchFailure;
+        {
+            QkvRopeSink sink{};
+            sink.out = pf.qkv;
+            sink.kc = kcache(l);
+            sink.vc = vcache(l);
+            sink.st = pf.st;
+            sink.g0 = L.q_proj.gamma;
+            sink.g1 = L.k_proj.gamma;
+            sink.g2 = L.v_proj.gamma;
+            sink.end0 = qrows;
+            sink.end1 = qrows + kvdim;
+            sink.hd = hd;
+            sink.hd_log2 = hd == 64 ? 6 : 7;
+            sink.max_seq = max_seq;
+            sink.rope_tab = rope;
+            sink.rope_pos0 = pos0;
+            launch_prefill_sink(sink, qrows + 2 * kvdim, pf.amax, pf.y[0], pf.y[1], pf.y[2],
+                                qrows, qrows + kvdim, qrows + 2 * kvdim, qrows, kvdim, kvdim,
+                                c, s);
+        }
+        // splits that some token of the pass reaches
+        const int sp = (pos0 + c - 1) / kAttnSplit + 1 < S ? (pos0 + c - 1) / kAttnSplit + 1 : S;
+        if (hd == 64)
+            launch_attention_prefill_hd<64>(nh / nkv, sp, nkv, c, s, pf.qkv, kcache(l),
+                                            vcache(l), pf.pm, pf.pl, pf.pacc, max_seq, S,
+                                            scale, pos0, qrows + 2 * kvdim);
+        else
+            launch_attention_prefill_hd<128>(nh / nkv, sp, nkv, c, s, pf.qkv, kcache(l),
+                                             vcache(l), pf.pm, pf.pl, pf.pacc, max_seq, S,
+                                             scale, pos0, qrows + 2 * kvdim);
+        {
+            AttnCombine p{pf.pm, pf.pl, pf.pacc, hd, S, qrows, hd == 64 ? 6 : 7};
+            launch_prefill_producer(p, 0, pf.st, qrows, c, pf.x, pf.amax, s);
+        }
+        if (gemm(L.o_proj, pf.y[0])) return hipErrorLaunchFailure;
+        {
+            SegBf16Sink sink{pf.o, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma, H, H,
+                             0.f, 0.f, 0.f};
+            launch_prefill_sink(sink, H, pf.amax, pf.y[0], pf.y[0], pf.y[0], H, H, H, H, H,
+                                H, c, s);
+        }
+        {
+            SubNormResidualNorm p{pf.o, pf.r, pf.r2, L.attn_sub_norm,
+                                  L.post_attention_layernorm, eps, H};
+            launch_prefill_producer(p, H, pf.st, H, c, pf.x, pf.amax, s);
+        }
+        if (gemm(L.gate_proj, pf.y[0]) || gemm(L.up_proj, pf.y[1]))
+            return hipErrorLaunchFailure;
+        {
+            SegBf16Sink sink{pf.gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
+                             I, 2 * I, 0.f, 0.f, 0.f};
+            launch_prefill_sink(sink, 2 * I, pf.amax, pf.y[0], pf.y[1], pf.y[1], I, 2 * I,
+                                2 * I, I, I, I, c, s);
+        }
+        {
+            Relu2Norm p{pf.gu, pf.gu + I, L.ffn_sub_norm,
+                        L.ffn_sub_norm ? L.ffn_sub_norm : reinterpret_cast<const float*>(pf.gu),
+                        eps, I};
+            launch_prefill_producer(p, 2 * I, pf.st, I, c, pf.x, pf.amax, s);
+        }
+        if (gemm(L.down_proj, pf.y[0])) return hipErrorLaunchFailure;
+        {
+            ResidualSink sink{pf.r, pf.r2, L.down_proj.gamma, 0.f};
+            launch_prefill_sink(sink, H, pf.amax, pf.y[0], pf.y[0], pf.y[0], H, H, H, H, H,
+                                H, c, s);
+        }
+    }
+    return hipGetLastError();
+}
+
 struct spb_engine {
     spb_model_config cfg{};
     std::vector<spb_transformer_layer> layers;
@@ -1871,16 +2363,9 @@ struct spb_engine {
     bool device_mode = false;
     bool pos_stale = false;
     // batched prefill: prompts with at least prefill_min tokens before the
-    // last go through the layers pf_chunk tokens at a time (0: never)
+    // last go through the layers pf.chunk tokens at a time (0: never)
     int prefill_min = kPrefillMinDefault;
-    int8_t* pf_x = nullptr;     // [chunk][max cols] int8 activations
-    float* pf_amax = nullptr;   // [chunk]
-    int32_t* pf_y[3] = {nullptr, nullptr, nullptr};  // [chunk][max rows] GEMM outputs
-    uint16_t *pf_qkv = nullptr, *pf_o = nullptr, *pf_r = nullptr, *pf_r2 = nullptr,
-             *pf_gu = nullptr;
-    float *pf_pm = nullptr, *pf_pl = nullptr, *pf_pacc = nullptr;
-    EngineState* pf_st = nullptr;  // [chunk] one decode-state record per token
-    int pf_chunk = 0;  // tokens per prefill pass
+    PrefillBufs pf;
 
     ~spb_engine() {
         if (exec) (void)hipGraphExecDestroy(exec);
@@ -1952,106 +2437,11 @@ struct spb_engine {
     }
 
     // Positions pos0 .. pos0 + c - 1 (tokens[] holds their ids) through every
-    // layer, c <= pf_chunk: the KV cache of those positions as c decode
+    // layer, c <= pf.chunk: the KV cache of those positions as c decode
     // steps would write it.  Returns a HIP error or hipSuccess.
     hipError_t enqueue_prefill(int pos0, int c, hipStream_t s) {
-        const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
-        const int nkv = cfg.num_key_value_heads, H = cfg.hidden_size;
-        const int I = cfg.intermediate_size, kvdim = nkv * hd, qrows = nh * hd;
-        const float eps = cfg.rms_norm_eps;
-        const float scale = 1.0f / sqrtf(static_cast<float>(hd));
-        std::vector<EngineState> hs(c);
-        for (int t = 0; t < c; ++t) {
-            hs[t] = EngineState{};
-            hs[t].pos = pos0 + t;
-            hs[t].prompt_len = max_seq;
-            hs[t].limit = max_seq;
-        }
-        hipError_t err = hipMemcpyAsync(pf_st, hs.data(), sizeof(EngineState) * c,
-                                        hipMemcpyHostToDevice, s);
-        if (err == hipSuccess) err = hipStreamSynchronize(s);  // hs is on this frame
-        if (err != hipSuccess) return err;
-        auto gemm = [&](const spb_sparse_linear& w, int32_t* y) {
-            return spb_sparse_ternary_gemm(w.meta, w.values, pf_x, y, w.rows, w.cols, c,
-                                           w.meta_stride, w.values_stride, s);
-        };
-        for (size_t l = 0; l < layers.size(); ++l) {
-            const spb_transformer_layer& L = layers[l];
-            {
-                InputNorm p{pf_r, l == 0 ? embed : nullptr, tokens, pf_r, L.input_layernorm, eps,
-                            H};
-                launch_prefill_producer(p, H, pf_st, H, c, pf_x, pf_amax, s);
-            }
-            if (gemm(L.q_proj, pf_y[0]) || gemm(L.k_proj, pf_y[1]) || gemm(L.v_proj, pf_y[2]))
-                return hipErrorLaunchFailure;
-            {
-                QkvRopeSink sink{};
-                sink.out = pf_qkv;
-                sink.kc = kcache[l];
-                sink.vc = vcache[l];
-                sink.st = pf_st;
-                sink.g0 = L.q_proj.gamma;
-                sink.g1 = L.k_proj.gamma;
-                sink.g2 = L.v_proj.gamma;
-                sink.end0 = qrows;
-                sink.end1 = qrows + kvdim;
-                sink.hd = hd;
-                sink.hd_log2 = hd == 64 ? 6 : 7;
-                sink.max_seq = max_seq;
-                sink.rope_tab = rope;
-                sink.rope_pos0 = pos0;
-                launch_prefill_sink(sink, qrows + 2 * kvdim, pf_amax, pf_y[0], pf_y[1], pf_y[2],
-                                    qrows, qrows + kvdim, qrows + 2 * kvdim, qrows, kvdim, kvdim,
-                                    c, s);
-            }
-            // splits that some token of the pass reaches
-            const int sp = (pos0 + c - 1) / kAttnSplit + 1 < S ? (pos0 + c - 1) / kAttnSplit + 1 : S;
-            if (hd == 64)
-                launch_attention_prefill_hd<64>(nh / nkv, sp, nkv, c, s, pf_qkv, kcache[l],
-                                                vcache[l], pf_pm, pf_pl, pf_pacc, max_seq, S,
-                                                scale, pos0, qrows + 2 * kvdim);
-            else
-                launch_attention_prefill_hd<128>(nh / nkv, sp, nkv, c, s, pf_qkv, kcache[l],
-                                                 vcache[l], pf_pm, pf_pl, pf_pacc, max_seq, S,
-                                                 scale, pos0, qrows + 2 * kvdim);
-            {
-                AttnCombine p{pf_pm, pf_pl, pf_pacc, hd, S, qrows, hd == 64 ? 6 : 7};
-                launch_prefill_producer(p, 0, pf_st, qrows, c, pf_x, pf_amax, s);
-            }
-            if (gemm(L.o_proj, pf_y[0])) return hipErrorLaunchFailure;
-            {
-                SegBf16Sink sink{pf_o, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma, H, H,
-                                 0.f, 0.f, 0.f};
-                launch_prefill_sink(sink, H, pf_amax, pf_y[0], pf_y[0], pf_y[0], H, H, H, H, H,
-                                    H, c, s);
-            }
-            {
-                SubNormResidualNorm p{pf_o, pf_r, pf_r2, L.attn_sub_norm,
-                                      L.post_attention_layernorm, eps, H};
-                launch_prefill_producer(p, H, pf_st, H, c, pf_x, pf_amax, s);
-            }
-            if (gemm(L.gate_proj, pf_y[0]) || gemm(L.up_proj, pf_y[1]))
-                return hipErrorLaunchFailure;
-            {
-                SegBf16Sink sink{pf_gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
-                                 I, 2 * I, 0.f, 0.f, 0.f};
-                launch_prefill_sink(sink, 2 * I, pf_amax, pf_y[0], pf_y[1], pf_y[1], I, 2 * I,
-                                    2 * I, I, I, I, c, s);
-            }
-            {
-                Relu2Norm p{pf_gu, pf_gu + I, L.ffn_sub_norm,
-                            L.ffn_sub_norm ? L.ffn_sub_norm : reinterpret_cast<const float*>(pf_gu),
-                            eps, I};
-                launch_prefill_producer(p, 2 * I, pf_st, I, c, pf_x, pf_amax, s);
-            }
-            if (gemm(L.down_proj, pf_y[0])) return hipErrorLaunchFailure;
-            {
-                ResidualSink sink{pf_r, pf_r2, L.down_proj.gamma, 0.f};
-                launch_prefill_sink(sink, H, pf_amax, pf_y[0], pf_y[0], pf_y[0], H, H, H, H, H,
-                                    H, c, s);
-            }
-        }
-        return hipGetLastError();
+        const PrefillTarget t{&cfg, &layers, embed, rope, max_seq, S, &kcache, &vcache, 0, tokens};
+        return enqueue_prefill_pass(t, pf, pos0, c, s);
     }
 };
 
@@ -2073,6 +2463,61 @@ int check_linear(const char* fn, const char* name, const spb_sparse_linear& l, i
                        "values_stride %% 2 == 0 and 16/8-byte aligned meta/values",
                        fn, name, kMaxPlaneCols);
     return 0;
+}
+
+// The model shapes both engines take (every projection on the bit-plane
+// kernel, head_dim 64 or 128, GQA groups 1/2/4/8, H <= kLmMaxH).
+int check_model(const char* fn, const spb_model_config* cfg, const spb_transformer_layer* layers,
+                const uint16_t* embed_tokens, const uint16_t* lm_head, int max_seq) {
+    const int H = cfg->hidden_size, nh = cfg->num_attention_heads, nkv = cfg->num_key_value_heads;
+    const int hd = cfg->head_dim, I = cfg->intermediate_size, V = cfg->vocab_size;
+    if (cfg->num_hidden_layers <= 0 || H <= 0 || nh <= 0 || nkv <= 0 || hd <= 0 || I <= 0 ||
+        V <= 0)
+        return invalid("%s: non-positive model dimension", fn);
+    if (nh * hd != H) return invalid("%s: num_attention_heads * head_dim != hidden_size", fn);
+    if (nh % nkv || (nh / nkv) & (nh / nkv - 1) || nh / nkv > kAttnMaxGroup)
+        return invalid("%s: heads per kv head must divide evenly and be 1, 2, 4 or %d", fn,
+                       kAttnMaxGroup);
+    if (hd != 64 && hd != 128) return invalid("%s: head_dim must be 64 or 128", fn);
+    if (H > kLmMaxH || H % 8) return invalid("%s: hidden_size must be a multiple of 8, <= %d", fn,
+                                             kLmMaxH);
+    if (max_seq <= 0 || max_seq > cfg->max_position_embeddings)
+        return invalid("%s: max_seq must be in [1, max_position_embeddings]", fn);
+    if (!aligned_to(embed_tokens, 16) || (lm_head && !aligned_to(lm_head, 16)))
+        return invalid("%s: embedding / lm_head must be 16-byte aligned", fn);
+    const int kvdim = nkv * hd;
+    for (int l = 0; l < cfg->num_hidden_layers; ++l) {
+        const spb_transformer_layer& L = layers[l];
+        int rc = 0;
+        if ((rc = check_linear(fn, "q_proj", L.q_proj, H, H)) ||
+            (rc = check_linear(fn, "k_proj", L.k_proj, kvdim, H)) ||
+            (rc = check_linear(fn, "v_proj", L.v_proj, kvdim, H)) ||
+            (rc = check_linear(fn, "o_proj", L.o_proj, H, H)) ||
+            (rc = check_linear(fn, "gate_proj", L.gate_proj, I, H)) ||
+            (rc = check_linear(fn, "up_proj", L.up_proj, I, H)) ||
+            (rc = check_linear(fn, "down_proj", L.down_proj, H, I)))
+            return rc;
+        if (!L.input_layernorm || !L.post_attention_layernorm)
+            return invalid("%s: layer %d lacks its RMSNorm weights", fn, l);
+    }
+    return 0;
+}
+
+// RoPE table (inference_kernels.cu:195-198): freq_i = 1 / theta^(2i/hd) in
+// float32, angle = float(pos) * freq_i, cos/sin evaluated in double.
+std::vector<float2> rope_table(const spb_model_config& cfg, int max_seq) {
+    const int hd = cfg.head_dim;
+    std::vector<float2> rope(static_cast<size_t>(max_seq) * (hd / 2));
+    for (int p = 0; p < max_seq; ++p)
+        for (int i = 0; i < hd / 2; ++i) {
+            const float freq = 1.0f / powf(cfg.rope_theta,
+                                           static_cast<float>(2 * i) / static_cast<float>(hd));
+            const float angle = static_cast<float>(p) * freq;
+            rope[static_cast<size_t>(p) * (hd / 2) + i] =
+                make_float2(static_cast<float>(cos(static_cast<double>(angle))),
+                            static_cast<float>(sin(static_cast<double>(angle))));
+        }
+    return rope;
 }
 
 int set_state(spb_engine* e, int pos, int prompt_len, int stop_eos) {
@@ -2118,37 +2563,10 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
     if (!cfg || !layers || !embed_tokens || !final_norm || !out)
         return invalid("%s: null argument", fn);
     *out = nullptr;
+    if (int rc = check_model(fn, cfg, layers, embed_tokens, lm_head, max_seq)) return rc;
     const int H = cfg->hidden_size, nh = cfg->num_attention_heads, nkv = cfg->num_key_value_heads;
     const int hd = cfg->head_dim, I = cfg->intermediate_size, V = cfg->vocab_size;
-    if (cfg->num_hidden_layers <= 0 || H <= 0 || nh <= 0 || nkv <= 0 || hd <= 0 || I <= 0 ||
-        V <= 0)
-        return invalid("%s: non-positive model dimension", fn);
-    if (nh * hd != H) return invalid("%s: num_attention_heads * head_dim != hidden_size", fn);
-    if (nh % nkv || (nh / nkv) & (nh / nkv - 1) || nh / nkv > kAttnMaxGroup)
-        return invalid("%s: heads per kv head must divide evenly and be 1, 2, 4 or %d", fn,
-                       kAttnMaxGroup);
-    if (hd != 64 && hd != 128) return invalid("%s: head_dim must be 64 or 128", fn);
-    if (H > kLmMaxH || H % 8) return invalid("%s: hidden_size must be a multiple of 8, <= %d", fn,
-                                             kLmMaxH);
-    if (max_seq <= 0 || max_seq > cfg->max_position_embeddings)
-        return invalid("%s: max_seq must be in [1, max_position_embeddings]", fn);
-    if (!aligned_to(embed_tokens, 16) || (lm_head && !aligned_to(lm_head, 16)))
-        return invalid("%s: embedding / lm_head must be 16-byte aligned", fn);
     const int kvdim = nkv * hd;
-    for (int l = 0; l < cfg->num_hidden_layers; ++l) {
-        const spb_transformer_layer& L = layers[l];
-        int rc = 0;
-        if ((rc = check_linear(fn, "q_proj", L.q_proj, H, H)) ||
-            (rc = check_linear(fn, "k_proj", L.k_proj, kvdim, H)) ||
-            (rc = check_linear(fn, "v_proj", L.v_proj, kvdim, H)) ||
-            (rc = check_linear(fn, "o_proj", L.o_proj, H, H)) ||
-            (rc = check_linear(fn, "gate_proj", L.gate_proj, I, H)) ||
-            (rc = check_linear(fn, "up_proj", L.up_proj, I, H)) ||
-            (rc = check_linear(fn, "down_proj", L.down_proj, H, I)))
-            return rc;
-        if (!L.input_layernorm || !L.post_attention_layernorm)
-            return invalid("%s: layer %d lacks its RMSNorm weights", fn, l);
-    }
     spb_engine* e = new (std::nothrow) spb_engine();
     if (!e) return invalid("%s: out of host memory", fn);
     e->cfg = *cfg;
@@ -2191,47 +2609,12 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
          (e->rope = dev_alloc<float2>(static_cast<size_t>(max_seq) * (hd / 2), own)) &&
          (e->cur_rope = dev_alloc<float2>(hd / 2, own)) &&
          (e->st = dev_alloc<EngineState>(1, own));
-    // batched prefill buffers: pf_chunk tokens per pass, the split partials
-    // capped at kPrefillPartialBytes
-    {
-        const long part = static_cast<long>(nh) * e->S * (hd + 2) * 4;  // bytes per token
-        long c = kPrefillPartialBytes / part;
-        c = c < kPrefillChunk ? c : kPrefillChunk;
-        e->pf_chunk = static_cast<int>(c > 0 ? c : 1);
-        const size_t C = static_cast<size_t>(e->pf_chunk);
-        const size_t xmax = static_cast<size_t>(std::max(std::max(H, I), nh * hd));
-        const size_t ymax = static_cast<size_t>(std::max(std::max(nh * hd, kvdim), std::max(H, I)));
-        ok = ok && (e->pf_x = dev_alloc<int8_t>(C * xmax, own)) &&
-             (e->pf_amax = dev_alloc<float>(C, own)) &&
-             (e->pf_y[0] = dev_alloc<int32_t>(C * ymax, own)) &&
-             (e->pf_y[1] = dev_alloc<int32_t>(C * ymax, own)) &&
-             (e->pf_y[2] = dev_alloc<int32_t>(C * ymax, own)) &&
-             (e->pf_qkv = dev_alloc<uint16_t>(C * (nh * hd + 2 * kvdim), own)) &&
-             (e->pf_o = dev_alloc<uint16_t>(C * H, own)) &&
-             (e->pf_r = dev_alloc<uint16_t>(C * H, own)) &&
-             (e->pf_r2 = dev_alloc<uint16_t>(C * H, own)) &&
-             (e->pf_gu = dev_alloc<uint16_t>(C * 2 * I, own)) &&
-             (e->pf_pm = dev_alloc<float>(C * nh * e->S, own)) &&
-             (e->pf_pl = dev_alloc<float>(C * nh * e->S, own)) &&
-             (e->pf_pacc = dev_alloc<float>(C * nh * e->S * hd, own)) &&
-             (e->pf_st = dev_alloc<EngineState>(C, own));
-    }
+    ok = ok && alloc_prefill(e->pf, *cfg, e->S, own);
     if (!ok) {
         delete e;
         return invalid("%s: device allocation failed", fn);
     }
-    // RoPE table (inference_kernels.cu:195-198): freq_i = 1 / theta^(2i/hd) in
-    // float32, angle = float(pos) * freq_i, cos/sin evaluated in double.
-    std::vector<float2> rope(static_cast<size_t>(max_seq) * (hd / 2));
-    for (int p = 0; p < max_seq; ++p)
-        for (int i = 0; i < hd / 2; ++i) {
-            const float freq = 1.0f / powf(cfg->rope_theta,
-                                           static_cast<float>(2 * i) / static_cast<float>(hd));
-            const float angle = static_cast<float>(p) * freq;
-            rope[static_cast<size_t>(p) * (hd / 2) + i] =
-                make_float2(static_cast<float>(cos(static_cast<double>(angle))),
-                            static_cast<float>(sin(static_cast<double>(angle))));
-        }
+    const std::vector<float2> rope = rope_table(*cfg, max_seq);
     hipError_t err = hipMemcpy(e->rope, rope.data(), rope.size() * sizeof(float2),
                                hipMemcpyHostToDevice);
     for (size_t l = 0; l < e->kcache.size() && err == hipSuccess; ++l) {
@@ -2351,8 +2734,8 @@ extern "C" int spb_engine_generate(spb_engine* e, const int* prompt, int n_promp
     int start = 0;
     const int pre = n_prompt - 1;
     if (e->prefill_min > 0 && pre >= e->prefill_min) {
-        for (int p0 = 0; p0 < pre; p0 += e->pf_chunk) {
-            const int c = pre - p0 < e->pf_chunk ? pre - p0 : e->pf_chunk;
+        for (int p0 = 0; p0 < pre; p0 += e->pf.chunk) {
+            const int c = pre - p0 < e->pf.chunk ? pre - p0 : e->pf.chunk;
             if (e->enqueue_prefill(p0, c, e->stream) != hipSuccess) return launch_status(fn);
         }
         if (int rc = set_state(e, pre, n_prompt, stop_at_eos ? 1 : 0)) return rc;
@@ -2437,4 +2820,415 @@ extern "C" int spb_generate_normal_bf16(uint64_t seed, long n, float std_, uint1
     hipLaunchKernelGGL(gen_normal_bf16_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
                        seed, n, std_, out);
     return launch_status(fn);
+}
+
+// ---- batched decode engine ------------------------------------------------------------
+//
+// B independent sequences per step (BASELINE config 4 at batch 8 / 32).  The
+// reference engine decodes one sequence (InferenceEngine::forward,
+// src/inference.cu:123-283); this engine computes, for each sequence, every
+// value of that step with the same device code in the same order as the bs=1
+// engine: the decode producers per token around the matrix-core GEMM over
+// the B tokens (the batched prefill's building blocks, with the token of
+// sequence t at that sequence's own position), the per-split attention body
+// over each sequence's own KV cache, and an LM head whose rows are computed
+// exactly as the bs=1 kernel computes them.  So every sequence's tokens equal
+// those of a bs=1 generation of that sequence alone.
+
+namespace {
+
+void launch_attention_batch(int hd, int G, int S, int nkv, int B, hipStream_t s,
+                            const uint16_t* qkv, const uint16_t* kc, const uint16_t* vc, float* pm,
+                            float* pl, float* pacc, const EngineState* st, int max_seq,
+                            float scale, int qkv_stride, long kv_stride) {
+    const dim3 grid(S, nkv, B), block(kAttnThreads);
+#define SPB_ATTN_BATCH(HD, GG)                                                                     \
+    hipLaunchKernelGGL((attention_batch_kernel<HD, GG>), grid, block, 0, s, qkv, kc, vc, pm, pl,  \
+                       pacc, st, max_seq, S, scale, qkv_stride, kv_stride)
+    if (hd == 64) {
+        switch (G) {
+        case 1: SPB_ATTN_BATCH(64, 1); break;
+        case 2: SPB_ATTN_BATCH(64, 2); break;
+        case 4: SPB_ATTN_BATCH(64, 4); break;
+        default: SPB_ATTN_BATCH(64, 8); break;
+        }
+    } else {
+        switch (G) {
+        case 1: SPB_ATTN_BATCH(128, 1); break;
+        case 2: SPB_ATTN_BATCH(128, 2); break;
+        case 4: SPB_ATTN_BATCH(128, 4); break;
+        default: SPB_ATTN_BATCH(128, 8); break;
+        }
+    }
+#undef SPB_ATTN_BATCH
+}
+
+}  // namespace
+
+struct spb_batch_engine {
+    spb_model_config cfg{};
+    std::vector<spb_transformer_layer> layers;
+    const uint16_t* embed = nullptr;
+    const uint16_t* lm_head = nullptr;
+    const float* final_norm = nullptr;
+    int max_seq = 0, S = 0, batch = 0, lm_grid = 0;
+    long kv_seq = 0;  // cache elements of one sequence in one layer's K (or V) cache
+    LmBatchKernel lm_kernel = nullptr;
+    std::vector<void*> owned;
+    std::vector<uint16_t*> kcache, vcache;  // per layer: [batch][kv head][max_seq][head_dim]
+    PrefillBufs step;  // the decode step's per-token buffers (batch tokens)
+    PrefillBufs pf;    // the prompt prefill's buffers
+    float* logits = nullptr;              // [batch][vocab]
+    float* part_v = nullptr;              // [batch][lm_grid]
+    int* part_i = nullptr;                // [batch][lm_grid]
+    int* tokens = nullptr;                // [batch][max_seq + 1]
+    float2* rope = nullptr;               // [max_seq][head_dim / 2]
+    float2* cur_rope = nullptr;           // [batch][head_dim / 2]
+    EngineState* st = nullptr;            // [batch]
+    std::vector<float2> rope_host;
+    hipStream_t stream = nullptr;
+    hipStream_t cap_stream = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+
+    ~spb_batch_engine() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (cap_stream) (void)hipStreamDestroy(cap_stream);
+        for (void* p : owned) (void)hipFree(p);
+    }
+
+    long tok_stride() const { return static_cast<long>(max_seq) + 1; }
+
+    // One decode step of every sequence: per layer the producer, GEMM(s)
+    // and sink of each projection over the batch's tokens and the batched
+    // attention; then the LM head in groups of kLmGroup sequences.
+    hipError_t enqueue_step(hipStream_t s) const {
+        const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
+        const int nkv = cfg.num_key_value_heads, H = cfg.hidden_size;
+        const int I = cfg.intermediate_size, kvdim = nkv * hd, qrows = nh * hd;
+        const float eps = cfg.rms_norm_eps;
+        const float scale = 1.0f / sqrtf(static_cast<float>(hd));  // inference.cu:182
+        const int B = batch;
+        auto gemm = [&](const spb_sparse_linear& w, int32_t* y) {
+            return spb_sparse_ternary_gemm(w.meta, w.values, step.x, y, w.rows, w.cols, B,
+                                           w.meta_stride, w.values_stride, s);
+        };
+        for (size_t l = 0; l < layers.size(); ++l) {
+            const spb_transformer_layer& L = layers[l];
+            {
+                InputNorm p{step.r, l == 0 ? embed : nullptr, tokens, step.r, L.input_layernorm,
+                            eps, H};
+                p.tok_stride = tok_stride();
+                launch_prefill_producer(p, H, st, H, B, step.x, step.amax, s);
+            }
+            if (gemm(L.q_proj, step.y[0]) || gemm(L.k_proj, step.y[1]) ||
+                gemm(L.v_proj, step.y[2]))
+                return hipErrorLaunchFailure;
+            {
+                QkvRopeSink sink{};
+                sink.out = step.qkv;
+                sink.kc = kcache[l];
+                sink.vc = vcache[l];
+                sink.cur_rope = cur_rope;
+                sink.st = st;
+                sink.g0 = L.q_proj.gamma;
+                sink.g1 = L.k_proj.gamma;
+                sink.g2 = L.v_proj.gamma;
+                sink.end0 = qrows;
+                sink.end1 = qrows + kvdim;
+                sink.hd = hd;
+                sink.hd_log2 = hd == 64 ? 6 : 7;
+                sink.max_seq = max_seq;
+                sink.rope_tab = nullptr;  // each sequence's own RoPE row (cur_rope)
+                sink.kv_stride = kv_seq;
+                launch_prefill_sink(sink, qrows + 2 * kvdim, step.amax, step.y[0], step.y[1],
+                                    step.y[2], qrows, qrows + kvdim, qrows + 2 * kvdim, qrows,
+                                    kvdim, kvdim, B, s);
+            }
+            launch_attention_batch(hd, nh / nkv, S, nkv, B, s, step.qkv, kcache[l], vcache[l],
+                                   step.pm, step.pl, step.pacc, st, max_seq, scale,
+                                   qrows + 2 * kvdim, kv_seq);
+            {
+                AttnCombine p{step.pm, step.pl, step.pacc, hd, S, qrows, hd == 64 ? 6 : 7};
+                launch_prefill_producer(p, 0, st, qrows, B, step.x, step.amax, s);
+            }
+            if (gemm(L.o_proj, step.y[0])) return hipErrorLaunchFailure;
+            {
+                SegBf16Sink sink{step.o, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma, H, H,
+                                 0.f, 0.f, 0.f};
+                launch_prefill_sink(sink, H, step.amax, step.y[0], step.y[0], step.y[0], H, H, H,
+                                    H, H, H, B, s);
+            }
+            {
+                SubNormResidualNorm p{step.o, step.r, step.r2, L.attn_sub_norm,
+                                      L.post_attention_layernorm, eps, H};
+                launch_prefill_producer(p, H, st, H, B, step.x, step.amax, s);
+            }
+            if (gemm(L.gate_proj, step.y[0]) || gemm(L.up_proj, step.y[1]))
+                return hipErrorLaunchFailure;
+            {
+                SegBf16Sink sink{step.gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
+                                 I, 2 * I, 0.f, 0.f, 0.f};
+                launch_prefill_sink(sink, 2 * I, step.amax, step.y[0], step.y[1], step.y[1], I,
+                                    2 * I, 2 * I, I, I, I, B, s);
+            }
+            {
+                Relu2Norm p{step.gu, step.gu + I, L.ffn_sub_norm,
+                            L.ffn_sub_norm ? L.ffn_sub_norm
+                                           : reinterpret_cast<const float*>(step.gu),
+                            eps, I};
+                launch_prefill_producer(p, 2 * I, st, I, B, step.x, step.amax, s);
+            }
+            if (gemm(L.down_proj, step.y[0])) return hipErrorLaunchFailure;
+            {
+                ResidualSink sink{step.r, step.r2, L.down_proj.gamma, 0.f};
+                launch_prefill_sink(sink, H, step.amax, step.y[0], step.y[0], step.y[0], H, H, H,
+                                    H, H, H, B, s);
+            }
+        }
+        const int V = cfg.vocab_size;
+        for (int g0 = 0; g0 < B; g0 += kLmGroup) {
+            const int gn = B - g0 < kLmGroup ? B - g0 : kLmGroup;
+            hipLaunchKernelGGL(lm_kernel, dim3(lm_grid), dim3(kLmBlock), lm_head_batch_lds(H), s,
+                               lm_head, step.r, final_norm, eps, logits, part_v, part_i, st,
+                               tokens, tok_stride(), V, H, rope, cur_rope, hd / 2, max_seq,
+                               V / lm_grid, V % lm_grid, g0, gn);
+        }
+        return hipGetLastError();
+    }
+};
+
+extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
+                                       const spb_transformer_layer* layers,
+                                       const uint16_t* embed_tokens, const uint16_t* lm_head,
+                                       const float* final_norm, int max_seq, int batch,
+                                       spb_batch_engine** out) {
+    clear_error();
+    const char* fn = "spb_batch_engine_create";
+    if (!cfg || !layers || !embed_tokens || !final_norm || !out)
+        return invalid("%s: null argument", fn);
+    *out = nullptr;
+    if (int rc = check_model(fn, cfg, layers, embed_tokens, lm_head, max_seq)) return rc;
+    if (batch < 1 || batch > kPrefillChunk)
+        return invalid("%s: batch must be in [1, %d]", fn, kPrefillChunk);
+    const int H = cfg->hidden_size, nh = cfg->num_attention_heads, nkv = cfg->num_key_value_heads;
+    const int hd = cfg->head_dim, V = cfg->vocab_size;
+    if (H > kLmBatchMaxH)
+        return invalid("%s: hidden_size %d exceeds the batched LM head's %d", fn, H, kLmBatchMaxH);
+    spb_batch_engine* e = new (std::nothrow) spb_batch_engine();
+    if (!e) return invalid("%s: out of host memory", fn);
+    e->cfg = *cfg;
+    e->layers.assign(layers, layers + cfg->num_hidden_layers);
+    e->embed = embed_tokens;
+    e->lm_head = lm_head ? lm_head : embed_tokens;
+    e->final_norm = final_norm;
+    e->max_seq = max_seq;
+    e->batch = batch;
+    e->S = (max_seq + kAttnSplit - 1) / kAttnSplit;
+    e->kv_seq = static_cast<long>(nkv) * max_seq * hd;
+    e->lm_kernel = lm_head_batch_for(H);
+    // one block per CU, at least vocab / kLmBatchMaxRows blocks (the rows of
+    // a block are staged in LDS)
+    const long lm_need = (static_cast<long>(V) + kLmBlock / kWave - 1) / (kLmBlock / kWave);
+    const long lm_min = (static_cast<long>(V) + kLmBatchMaxRows - 1) / kLmBatchMaxRows;
+    long lm_grid = device_cu_count();
+    if (lm_grid > lm_need) lm_grid = lm_need;
+    e->lm_grid = static_cast<int>(lm_grid > lm_min ? lm_grid : lm_min);
+
+    auto& own = e->owned;
+    const size_t kv = static_cast<size_t>(batch) * e->kv_seq;
+    bool ok = true;
+    for (int l = 0; l < cfg->num_hidden_layers && ok; ++l) {
+        e->kcache.push_back(dev_alloc<uint16_t>(kv, own));
+        e->vcache.push_back(dev_alloc<uint16_t>(kv, own));
+        ok = e->kcache.back() && e->vcache.back();
+    }
+    const size_t B = static_cast<size_t>(batch);
+    ok = ok && alloc_prefill(e->step, *cfg, e->S, own, batch) &&
+         alloc_prefill(e->pf, *cfg, e->S, own) &&
+         (e->logits = dev_alloc<float>(B * V, own)) &&
+         (e->part_v = dev_alloc<float>(B * e->lm_grid, own)) &&
+         (e->part_i = dev_alloc<int>(B * e->lm_grid, own)) &&
+         (e->tokens = dev_alloc<int>(B * (max_seq + 1), own)) &&
+         (e->rope = dev_alloc<float2>(static_cast<size_t>(max_seq) * (hd / 2), own)) &&
+         (e->cur_rope = dev_alloc<float2>(B * (hd / 2), own)) &&
+         (e->st = dev_alloc<EngineState>(B, own));
+    if (!ok) {
+        delete e;
+        return invalid("%s: device allocation failed", fn);
+    }
+    (void)nh;
+    // the LM head's dynamic LDS (8 normalised vectors + staged logits) may
+    // exceed 64 KB (96 KB at hidden 2560)
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(e->lm_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lm_head_batch_lds(H))) != hipSuccess) {
+        delete e;
+        return launch_status(fn);
+    }
+    e->rope_host = rope_table(*cfg, max_seq);
+    hipError_t err = hipMemcpy(e->rope, e->rope_host.data(), e->rope_host.size() * sizeof(float2),
+                               hipMemcpyHostToDevice);
+    for (size_t l = 0; l < e->kcache.size() && err == hipSuccess; ++l) {
+        err = hipMemset(e->kcache[l], 0, kv * 2);
+        if (err == hipSuccess) err = hipMemset(e->vcache[l], 0, kv * 2);
+    }
+    if (err == hipSuccess) err = hipMemset(e->st, 0, B * sizeof(EngineState));
+    if (err == hipSuccess) err = hipMemset(e->tokens, 0, B * (max_seq + 1) * sizeof(int));
+    if (err == hipSuccess) err = hipStreamCreateWithFlags(&e->cap_stream, hipStreamNonBlocking);
+    if (err != hipSuccess) {
+        delete e;
+        return launch_status(fn);
+    }
+    err = hipStreamBeginCapture(e->cap_stream, hipStreamCaptureModeThreadLocal);
+    if (err == hipSuccess) {
+        const hipError_t le = e->enqueue_step(e->cap_stream);
+        err = hipStreamEndCapture(e->cap_stream, &e->graph);
+        if (err == hipSuccess && le != hipSuccess) err = le;
+    }
+    if (err == hipSuccess) err = hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0);
+    if (err != hipSuccess) {
+        set_error("%s: graph capture failed: %s", fn, hipGetErrorString(err));
+        delete e;
+        return static_cast<int>(err);
+    }
+    // every slot done until a generate arms it
+    std::vector<EngineState> hs(B);
+    for (auto& h : hs) {
+        h = EngineState{};
+        h.limit = max_seq;
+        h.prompt_len = max_seq;
+        h.done = 1;
+    }
+    if (hipMemcpy(e->st, hs.data(), B * sizeof(EngineState), hipMemcpyHostToDevice) !=
+        hipSuccess) {
+        delete e;
+        return launch_status(fn);
+    }
+    *out = e;
+    return 0;
+}
+
+extern "C" int spb_batch_engine_destroy(spb_batch_engine* e) {
+    clear_error();
+    if (e) {
+        (void)hipStreamSynchronize(e->stream);
+        delete e;
+    }
+    return 0;
+}
+
+extern "C" int spb_batch_engine_set_stream(spb_batch_engine* e, spb_stream_t stream) {
+    clear_error();
+    if (!e) return invalid("spb_batch_engine_set_stream: null engine");
+    e->stream = as_stream(stream);
+    return 0;
+}
+
+extern "C" int spb_batch_engine_generate(spb_batch_engine* e, const int* prompts,
+                                         const int* prompt_lens, int n_seq, int n_new,
+                                         int stop_at_eos, int* out_tokens, int* n_generated) {
+    clear_error();
+    const char* fn = "spb_batch_engine_generate";
+    if (!e || !prompts || !prompt_lens || (!out_tokens && n_new > 0))
+        return invalid("%s: null argument", fn);
+    if (n_seq < 1 || n_seq > e->batch)
+        return invalid("%s: n_seq %d outside [1, %d]", fn, n_seq, e->batch);
+    if (n_new < 0) return invalid("%s: n_new < 0", fn);
+    std::vector<long> off(n_seq + 1, 0);
+    for (int b = 0; b < n_seq; ++b) {
+        const int n = prompt_lens[b];
+        if (n < 1) return invalid("%s: sequence %d has an empty prompt", fn, b);
+        if (static_cast<long>(n) + n_new > e->max_seq)
+            return invalid("%s: sequence %d: prompt + new tokens (%ld) exceed max_seq %d", fn, b,
+                           static_cast<long>(n) + n_new, e->max_seq);
+        off[b + 1] = off[b] + n;
+    }
+    for (long i = 0; i < off[n_seq]; ++i)
+        if (prompts[i] < 0 || prompts[i] >= e->cfg.vocab_size)
+            return invalid("%s: prompt token %d outside [0, %d)", fn, prompts[i],
+                           e->cfg.vocab_size);
+    hipStream_t s = e->stream;
+    const long ts = e->tok_stride();
+    const int half = e->cfg.head_dim / 2;
+    // token buffers, then each prompt's positions 0 .. n-2 through the layers
+    // (the batched prefill, into the sequence's own KV cache)
+    std::vector<int> tok(static_cast<size_t>(n_seq) * ts, 0);
+    for (int b = 0; b < n_seq; ++b)
+        std::copy(prompts + off[b], prompts + off[b + 1], tok.begin() + b * ts);
+    if (hipMemcpyAsync(e->tokens, tok.data(), tok.size() * sizeof(int), hipMemcpyHostToDevice, s) !=
+            hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return launch_status(fn);
+    for (int b = 0; b < n_seq; ++b) {
+        const int pre = prompt_lens[b] - 1;
+        const PrefillTarget t{&e->cfg, &e->layers, e->embed, e->rope, e->max_seq, e->S,
+                              &e->kcache, &e->vcache, b * e->kv_seq, e->tokens + b * ts};
+        for (int p0 = 0; p0 < pre; p0 += e->pf.chunk) {
+            const int c = pre - p0 < e->pf.chunk ? pre - p0 : e->pf.chunk;
+            if (enqueue_prefill_pass(t, e->pf, p0, c, s) != hipSuccess) return launch_status(fn);
+        }
+    }
+    // decode states: sequence b continues at its last prompt token; unused
+    // slots are done
+    std::vector<EngineState> hs(e->batch);
+    std::vector<float2> cr(static_cast<size_t>(e->batch) * half);
+    for (int b = 0; b < e->batch; ++b) {
+        EngineState& h = hs[b];
+        h = EngineState{};
+        h.limit = e->max_seq;
+        h.eos = e->cfg.eos_token_id;
+        if (b < n_seq) {
+            h.pos = prompt_lens[b] - 1;
+            h.prompt_len = prompt_lens[b];
+            h.stop_eos = stop_at_eos ? 1 : 0;
+        } else {
+            h.prompt_len = e->max_seq;
+            h.done = 1;
+        }
+        std::copy(e->rope_host.begin() + static_cast<long>(h.pos) * half,
+                  e->rope_host.begin() + static_cast<long>(h.pos + 1) * half,
+                  cr.begin() + static_cast<long>(b) * half);
+    }
+    if (hipMemcpyAsync(e->st, hs.data(), hs.size() * sizeof(EngineState), hipMemcpyHostToDevice,
+                       s) != hipSuccess ||
+        hipMemcpyAsync(e->cur_rope, cr.data(), cr.size() * sizeof(float2), hipMemcpyHostToDevice,
+                       s) != hipSuccess)
+        return launch_status(fn);
+    for (int i = 0; i < n_new; ++i)
+        if (hipGraphLaunch(e->exec, s) != hipSuccess) return launch_status(fn);
+    if (hipMemcpyAsync(hs.data(), e->st, hs.size() * sizeof(EngineState), hipMemcpyDeviceToHost,
+                       s) != hipSuccess ||
+        hipMemcpyAsync(tok.data(), e->tokens, tok.size() * sizeof(int), hipMemcpyDeviceToHost, s) !=
+            hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return launch_status(fn);
+    for (int b = 0; b < n_seq; ++b) {
+        const int got = hs[b].generated < n_new ? hs[b].generated : n_new;
+        for (int i = 0; i < n_new; ++i)
+            out_tokens[static_cast<long>(b) * n_new + i] =
+                i < got ? tok[b * ts + prompt_lens[b] + i] : -1;
+        if (n_generated) n_generated[b] = got;
+    }
+    return 0;
+}
+
+extern "C" int spb_batch_engine_decode_steps(spb_batch_engine* e, int steps) {
+    clear_error();
+    if (!e) return invalid("spb_batch_engine_decode_steps: null engine");
+    if (steps < 0) return invalid("spb_batch_engine_decode_steps: steps < 0");
+    for (int i = 0; i < steps; ++i)
+        if (hipGraphLaunch(e->exec, e->stream) != hipSuccess)
+            return launch_status("spb_batch_engine_decode_steps");
+    return 0;
+}
+
+extern "C" int spb_batch_engine_buffers(const spb_batch_engine* e, const float** logits,
+                                        const int** tokens) {
+    clear_error();
+    if (!e) return invalid("spb_batch_engine_buffers: null engine");
+    if (logits) *logits = e->logits;
+    if (tokens) *tokens = e->tokens;
+    return 0;
 }

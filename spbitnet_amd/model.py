@@ -486,3 +486,53 @@ class InferenceEngine:
         """Enqueue `steps` more greedy steps (no host synchronisation)."""
         _lib.check(self._L.spb_engine_decode_steps(self._h, int(steps)),
                    "spb_engine_decode_steps")
+
+
+class BatchInferenceEngine:
+    """Greedy decode of several independent sequences per step on the HIP
+    batched engine (spb_batch_engine_*).  No reference counterpart: the
+    reference's InferenceEngine decodes one sequence; each sequence's tokens
+    here equal InferenceEngine.generate on that sequence alone."""
+
+    def __init__(self, model, max_seq: int, batch: int, stream=None):
+        self.model = model
+        self.max_seq = int(max_seq)
+        self.batch = int(batch)
+        self._L = _lib.load()
+        cfg, layers, embed, lm, final = model.engine_args()
+        self._cfg, self._layers = cfg, layers
+        h = ctypes.c_void_p()
+        _lib.check(self._L.spb_batch_engine_create(ctypes.byref(cfg), layers, embed, lm, final,
+                                                   self.max_seq, self.batch, ctypes.byref(h)),
+                   "spb_batch_engine_create")
+        self._h = h
+        self._stream = stream if stream is not None else torch.cuda.current_stream()
+        _lib.check(self._L.spb_batch_engine_set_stream(self._h, self._stream.cuda_stream or None),
+                   "spb_batch_engine_set_stream")
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._L.spb_batch_engine_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def generate(self, prompts: Sequence[Sequence[int]], n_new: int,
+                 stop_at_eos: bool = True) -> List[List[int]]:
+        """Greedy generation of len(prompts) <= batch sequences at once; one
+        token list per sequence (src/main.cpp:133-155 per sequence)."""
+        flat = [int(t) for p in prompts for t in p]
+        lens = (ctypes.c_int * len(prompts))(*[len(p) for p in prompts])
+        fp = (ctypes.c_int * max(1, len(flat)))(*flat)
+        out = (ctypes.c_int * max(1, len(prompts) * n_new))()
+        got = (ctypes.c_int * len(prompts))()
+        _lib.check(self._L.spb_batch_engine_generate(self._h, fp, lens, len(prompts), int(n_new),
+                                                     1 if stop_at_eos else 0, out, got),
+                   "spb_batch_engine_generate")
+        return [list(out[b * n_new: b * n_new + got[b]]) for b in range(len(prompts))]
+
+    def decode_steps(self, steps: int) -> None:
+        """Enqueue `steps` more batched steps (no host synchronisation)."""
+        _lib.check(self._L.spb_batch_engine_decode_steps(self._h, int(steps)),
+                   "spb_batch_engine_decode_steps")

@@ -1,0 +1,118 @@
+"""GPU parity of the batched decode engine (spb_batch_engine_*, BASELINE
+config 4 at batch 8 and 32): every sequence of a batch, with distinct ragged
+prompts, produces exactly the greedy tokens the CPU oracle's single-sequence
+generate (src/main.cpp:133-155 per sequence, oracle/spb_engine_oracle.c)
+produces for it, and those of the bs=1 engine."""
+import concurrent.futures
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _cfg(**kw):
+    from spbitnet_amd.model import ModelConfig
+    base = dict(hidden_size=512, num_hidden_layers=2, num_attention_heads=8,
+                num_key_value_heads=2, intermediate_size=1536, vocab_size=4096,
+                max_position_embeddings=4096, head_dim=64, rms_norm_eps=1e-5,
+                rope_theta=500000.0, bos_token_id=1, eos_token_id=2)
+    base.update(kw)
+    return ModelConfig(**base)
+
+
+def _prompts(n, vocab, lo, hi, seed):
+    rng = np.random.default_rng(seed)
+    return [[int(t) for t in rng.integers(0, vocab, int(rng.integers(lo, hi + 1)))]
+            for _ in range(n)]
+
+
+def _oracle_tokens(host, max_seq, prompts, n_new, eos=-1):
+    """The oracle's single-sequence generate for each prompt (host threads,
+    one oracle engine per sequence)."""
+    def one(p):
+        return O.EngineOracle(host, max_seq).generate(p, n_new, eos)
+    workers = min(16, os.cpu_count() or 1, len(prompts))
+    with concurrent.futures.ThreadPoolExecutor(workers) as pool:
+        return list(pool.map(one, prompts))
+
+
+@pytest.mark.parametrize("batch", [8, 32])
+def test_batch_decode_matches_oracle(gpu, batch):
+    """Ragged prompts of 260-700 tokens (5-11 of the 64-position attention
+    splits) in a 4096-position cache, 16 greedy steps per sequence."""
+    from spbitnet_amd.model import BatchInferenceEngine, InferenceEngine, Model
+    cfg = _cfg()
+    model = Model.random(cfg, seed=101 + batch)
+    torch.cuda.synchronize()
+    prompts = _prompts(batch, cfg.vocab_size, 260, 700, seed=batch)
+    print(f"batch {batch}: batched generate", flush=True)
+    eng = BatchInferenceEngine(model, max_seq=4096, batch=batch)
+    got = eng.generate(prompts, 16, stop_at_eos=False)
+    assert [len(g) for g in got] == [16] * batch
+    print(f"batch {batch}: oracle", flush=True)
+    want = _oracle_tokens(model.to_host(), 4096, prompts, 16)
+    for b in range(batch):
+        assert got[b] == want[b], f"sequence {b} (prompt {len(prompts[b])})"
+    # a second generation on the same engine with fewer sequences than slots
+    print(f"batch {batch}: partial batch", flush=True)
+    again = eng.generate(prompts[: batch // 2], 8, stop_at_eos=False)
+    assert again == [w[:8] for w in want[: batch // 2]]
+    eng.close()
+    # the bs=1 engine agrees on a few sequences
+    one = InferenceEngine(model, max_seq=4096)
+    for b in (0, batch - 1):
+        assert one.generate(prompts[b], 16, stop_at_eos=False) == want[b]
+    one.close()
+
+
+def test_batch_decode_gqa_variants_and_eos(gpu):
+    """GQA groups 1, 4 and 8 with head_dim 64 and 128, models without
+    sub-norms, short prompts (one-token prompts included), and EOS stops
+    that end some sequences before others."""
+    from spbitnet_amd.model import BatchInferenceEngine, Model
+    cases = [(dict(num_key_value_heads=8), {}), (dict(num_key_value_heads=1), {}),
+             (dict(hidden_size=512, num_attention_heads=4, num_key_value_heads=1, head_dim=128),
+              dict(sub_norms=False))]
+    for i, (ckw, mkw) in enumerate(cases):
+        cfg = _cfg(max_position_embeddings=512, **ckw)
+        print(f"batch variant {ckw} {mkw}", flush=True)
+        model = Model.random(cfg, seed=201 + i, **mkw)
+        prompts = _prompts(5, cfg.vocab_size, 1, 90, seed=7 + i)
+        prompts[0] = prompts[0][:1]
+        want = _oracle_tokens(model.to_host(), 512, prompts, 20)
+        eng = BatchInferenceEngine(model, max_seq=512, batch=6)
+        assert eng.generate(prompts, 20, stop_at_eos=False) == want
+        eng.close()
+        # EOS: the token sequence 0 generates at step 6 ends it there
+        eos = want[0][6]
+        model.config = _cfg(max_position_embeddings=512, eos_token_id=eos, **ckw)
+        eng = BatchInferenceEngine(model, max_seq=512, batch=6)
+        got = eng.generate(prompts, 20, stop_at_eos=True)
+        for b in range(5):
+            cut = want[b].index(eos) + 1 if eos in want[b] else 20
+            assert got[b] == want[b][:cut], f"sequence {b}"
+        eng.close()
+
+
+def test_batch_engine_rejects_bad_input(gpu):
+    from spbitnet_amd import _lib
+    from spbitnet_amd.model import BatchInferenceEngine, Model
+    cfg = _cfg(num_hidden_layers=1, max_position_embeddings=64)
+    model = Model.random(cfg, seed=3)
+    eng = BatchInferenceEngine(model, max_seq=64, batch=4)
+    with pytest.raises(_lib.SpbError):
+        eng.generate([[1, 2]] * 5, 4)           # more sequences than slots
+    with pytest.raises(_lib.SpbError):
+        eng.generate([[1] * 60], 8)             # exceeds max_seq
+    with pytest.raises(_lib.SpbError):
+        eng.generate([[1], []], 4)              # empty prompt
+    with pytest.raises(_lib.SpbError):
+        eng.generate([[cfg.vocab_size]], 4)     # token out of range
+    assert eng.generate([[5, 6, 7]], 4, stop_at_eos=False) == \
+        _oracle_tokens(model.to_host(), 64, [[5, 6, 7]], 4)
+    eng.close()
