@@ -301,6 +301,8 @@ def _elib():
         L.spbo_engine_reset.argtypes = [_P]
         L.spbo_engine_step.argtypes = [_P, _I, _P]
         L.spbo_engine_step.restype = _I
+        L.spbo_engine_prefill.argtypes = [_P, _I]
+        L.spbo_engine_prefill.restype = _I
         L.spbo_engine_hidden.argtypes = [_P, _P]
         L.spbo_engine_debug.argtypes = [_P, _I, _P]
         L.spbo_engine_debug.restype = _I
@@ -379,6 +381,11 @@ class EngineOracle:
             raise ValueError("oracle step: KV cache full or token id out of range")
         return int(t), logits
 
+    def prefill(self, token: int) -> None:
+        """A prompt token before the last: the step without the LM head."""
+        if _elib().spbo_engine_prefill(self._e, int(token)) < 0:
+            raise ValueError("oracle prefill: KV cache full or token id out of range")
+
     def hidden(self) -> np.ndarray:
         out = np.empty(self.hidden_size, np.float32)
         _elib().spbo_engine_hidden(self._e, _p(out))
@@ -397,7 +404,7 @@ class EngineOracle:
         """Greedy generation with the convention of src/main.cpp:133-155."""
         self.reset()
         for t in prompt[:-1]:
-            self.step(t)
+            self.prefill(t)
         tok = prompt[-1]
         out = []
         for _ in range(n_new):

@@ -270,16 +270,8 @@ static void attention(spbo_engine* e, int l) {
     float* pm = (float*)malloc(sizeof(float) * nh * S);
     float* pl = (float*)malloc(sizeof(float) * nh * S);
     float* pacc = (float*)malloc(sizeof(float) * nh * S * hd);
-    float qs[8][128];
-    float sc[8][ATTN_SPLIT];
+    /* RoPE of k and the cache writes at pos (every kv head) */
     for (int kvh = 0; kvh < nkv; ++kvh) {
-        for (int g = 0; g < G; ++g)
-            for (int i = 0; i < half; ++i) {
-                const float* qh = e->qkv + (kvh * G + g) * hd;
-                const float x0 = qh[2 * i], x1 = qh[2 * i + 1], c = rp[2 * i], s = rp[2 * i + 1];
-                qs[g][2 * i] = bfr(x0 * c - x1 * s);
-                qs[g][2 * i + 1] = bfr(x0 * s + x1 * c);
-            }
         const float* kh = e->qkv + nh * hd + kvh * hd;
         const float* vh = e->qkv + (nh + nkv) * hd + kvh * hd;
         uint16_t* kc = e->kc[l] + (size_t)kvh * e->max_seq * hd;
@@ -290,7 +282,24 @@ static void attention(spbo_engine* e, int l) {
             kc[(size_t)pos * hd + 2 * i + 1] = spbo_bf16_round(x0 * s + x1 * c);
         }
         for (int d = 0; d < hd; ++d) vc[(size_t)pos * hd + d] = spbo_bf16_round(vh[d]);
-        for (int s = 0; s < S; ++s) {
+    }
+    /* the partials of every (kv head, split): independent, so they run in
+     * parallel (OpenMP) for long contexts */
+#pragma omp parallel for schedule(dynamic) if (S * nkv >= 16)
+    for (int task = 0; task < nkv * S; ++task) {
+        const int kvh = task / S, s = task % S;
+        float qs[8][128];
+        float sc[8][ATTN_SPLIT];
+        for (int g = 0; g < G; ++g)
+            for (int i = 0; i < half; ++i) {
+                const float* qh = e->qkv + (kvh * G + g) * hd;
+                const float x0 = qh[2 * i], x1 = qh[2 * i + 1], c = rp[2 * i], sn = rp[2 * i + 1];
+                qs[g][2 * i] = bfr(x0 * c - x1 * sn);
+                qs[g][2 * i + 1] = bfr(x0 * sn + x1 * c);
+            }
+        const uint16_t* kc = e->kc[l] + (size_t)kvh * e->max_seq * hd;
+        const uint16_t* vc = e->vc[l] + (size_t)kvh * e->max_seq * hd;
+        {
             const int j0 = s * ATTN_SPLIT;
             const int jn = (pos + 1 - j0) < ATTN_SPLIT ? (pos + 1 - j0) : ATTN_SPLIT;
             for (int jj = 0; jj < jn; ++jj) {
@@ -342,10 +351,22 @@ static void attention(spbo_engine* e, int l) {
     free(pacc);
 }
 
+static int engine_step(spbo_engine* e, int token, float* logits, int with_head);
+
 /* One token: returns argmax(logits) (lowest index among maxima), or -1 when
  * the KV cache is full or the token id is out of range; logits (nullable)
  * receives the float32 logits. */
 int spbo_engine_step(spbo_engine* e, int token, float* logits) {
+    return engine_step(e, token, logits, 1);
+}
+
+/* A prompt token before the last (src/main.cpp:133-143): the same step
+ * without the LM head, whose logits the generate loop does not use; the KV
+ * cache and position are those spbo_engine_step leaves.  Returns 0, or -1
+ * as spbo_engine_step. */
+int spbo_engine_prefill(spbo_engine* e, int token) { return engine_step(e, token, NULL, 0); }
+
+static int engine_step(spbo_engine* e, int token, float* logits, int with_head) {
     if (e->pos >= e->max_seq || token < 0 || token >= e->V) return -1; /* cache full / bad id */
     const int H = e->H, I = e->I, hd = e->hd, kvd = e->nkv * hd;
     const float eps = e->eps;
@@ -404,6 +425,10 @@ int spbo_engine_step(spbo_engine* e, int token, float* logits) {
         const float a3 = bitlinear_raw(e, &L->p[6], vec, acc);
         const float dq3 = spbo_dequant_scale(L->p[6].gamma, a3);
         for (int r = 0; r < H; ++r) e->x[r] = bfr(bfr((float)acc[r] * dq3) + e->xb[r]);
+    }
+    if (!with_head) {
+        e->pos += 1;
+        return 0;
     }
     /* final norm and LM head (:268-277; half_gemv_kernel :488-531); rows are
      * independent, so they run in parallel (OpenMP) and the argmax follows */

@@ -2,6 +2,8 @@
 generator against the CPU oracle (oracle/spb_engine_oracle.c): logits bit
 for bit and greedy token ids exactly, the bar of the reference's own
 generate loop (src/main.cpp:133-155) on random-init weights."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -290,3 +292,56 @@ def test_engine_rejects_short_strides(gpu):
         InferenceEngine(model, max_seq=16)
     d.values_stride = keep
     InferenceEngine(model, max_seq=16).close()
+
+
+GOLDEN_2B4T = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                           "decode_2b4t_tokens.json")
+
+
+def test_engine_bitnet_2b4t_greedy_128_golden(gpu):
+    """Config 3 at full shape: BOS + 32 seeded ids, then 128 greedy steps on
+    the 2.4B-parameter model, tokens equal to the oracle's (committed by
+    tests/golden/make_decode_golden.py from the same device-generated
+    weights; the first 4 are recomputed here by the oracle live)."""
+    import json
+    from spbitnet_amd.model import InferenceEngine, Model, ModelConfig
+    gold = json.load(open(GOLDEN_2B4T))
+    cfg = ModelConfig.bitnet_b158_2b4t()
+    print("generating the 2.4B-parameter random model", flush=True)
+    model = Model.random(cfg, seed=2025)
+    prompt = [cfg.bos_token_id] + _prompt(32, cfg.vocab_size, 2025)
+    eng = InferenceEngine(model, max_seq=256)
+    print("generate 128", flush=True)
+    got = eng.generate(prompt, 128, stop_at_eos=False)
+    assert got == gold["config3"]["tokens"]
+    eng.close()
+    print("oracle: 4 live steps", flush=True)
+    assert O.EngineOracle(model.to_host(), 64).generate(prompt, 4) == got[:4]
+
+
+def test_full_width_long_context(gpu):
+    """Config-4 geometry at full width (hidden 2560, 20/5 heads, FFN 6912,
+    vocab 128256) on a 2-layer model: a 2048-token prompt into a
+    4096-position cache, 24 greedy steps, on the bs=1 engine and, for that
+    prompt and a 1500-token one together, on the batched engine; tokens
+    equal to the oracle's."""
+    from spbitnet_amd.model import BatchInferenceEngine, InferenceEngine, Model, ModelConfig
+    cfg = ModelConfig.bitnet_b158_2b4t()
+    cfg.num_hidden_layers = 2
+    print("generating the 2-layer full-width model", flush=True)
+    model = Model.random(cfg, seed=77)
+    p0 = [cfg.bos_token_id] + _prompt(2047, cfg.vocab_size, 5)
+    p1 = [cfg.bos_token_id] + _prompt(1499, cfg.vocab_size, 6)
+    eng = InferenceEngine(model, max_seq=4096)
+    got0 = eng.generate(p0, 24, stop_at_eos=False)
+    eng.close()
+    beng = BatchInferenceEngine(model, max_seq=4096, batch=2)
+    got = beng.generate([p0, p1], 24, stop_at_eos=False)
+    beng.close()
+    print("oracle (2 sequences)", flush=True)
+    host = model.to_host()
+    import concurrent.futures
+    with concurrent.futures.ThreadPoolExecutor(2) as pool:
+        want = list(pool.map(lambda p: O.EngineOracle(host, 4096).generate(p, 24), [p0, p1]))
+    assert got0 == want[0]
+    assert got == want
