@@ -46,6 +46,7 @@ namespace {
 
 constexpr int kAttnSplit = 64;    // positions per attention split (one per lane)
 constexpr int kAttnThreads = 256;
+constexpr int kAttnBucketSplits = 8;  // splits per position bucket of the decode graphs
 constexpr int kPrefillChunk = 1024;      // prompt tokens per batched-prefill pass (at most)
 constexpr long kPrefillPartialBytes = 1L << 30;  // split partials of one pass (at most)
 constexpr int kPrefillMinDefault = 16;   // prompt tokens before the last that switch to it
@@ -2178,13 +2179,16 @@ void launch_prefill_sink(const Sink& sink, long stride, const float* amax, const
                        sink, stride, amax, y0, y1, y2, end0, end1, rows, ld0, ld1, ld2);
 }
 
-void launch_attention(int hd, int G, int S, int nkv, hipStream_t s, const uint16_t* qkv,
-                      const uint16_t* kc, const uint16_t* vc, float* pm, float* pl, float* pacc,
-                      const EngineState* st, int max_seq, float scale) {
+// The first `splits` splits of S (the partials' stride stays S).
+void launch_attention(int hd, int G, int S, int splits, int nkv, hipStream_t s,
+                      const uint16_t* qkv, const uint16_t* kc, const uint16_t* vc, float* pm,
+                      float* pl, float* pacc, const EngineState* st, int max_seq, float scale) {
     if (hd == 64)
-        launch_attention_hd<64>(G, dim3(S, nkv), s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
+        launch_attention_hd<64>(G, dim3(splits, nkv), s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S,
+                                scale);
     else
-        launch_attention_hd<128>(G, dim3(S, nkv), s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
+        launch_attention_hd<128>(G, dim3(splits, nkv), s, qkv, kc, vc, pm, pl, pacc, st, max_seq,
+                                 S, scale);
 }
 
 // A projection of the decode step: the span kernel (every weight load issued
@@ -2353,8 +2357,16 @@ struct spb_engine {
     EngineState* st = nullptr;
     hipStream_t stream = nullptr;      // where graphs are launched (null = legacy stream)
     hipStream_t cap_stream = nullptr;  // capture stream
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // One token-step graph per bucket of positions: graph k launches the
+    // attention kernel on the splits of positions below (k + 1) * bucket_pos
+    // only (the blocks of splits past the position would load their K and V
+    // for nothing).  The host replays the graph of pos_hint, an upper bound
+    // of the device position (the device advances at most one position per
+    // step; a done state stops it), so the grid always covers the position.
+    std::vector<hipGraph_t> graphs;
+    std::vector<hipGraphExec_t> execs;
+    int bucket_pos = 0;  // positions per bucket (a multiple of the split)
+    int pos_hint = 0;
     int seq_len = 0;
     // The device state is in generate mode (prompt_len, stop_eos, done as
     // spb_engine_generate left them) or advanced by spb_engine_decode_steps
@@ -2368,14 +2380,25 @@ struct spb_engine {
     PrefillBufs pf;
 
     ~spb_engine() {
-        if (exec) (void)hipGraphExecDestroy(exec);
-        if (graph) (void)hipGraphDestroy(graph);
+        for (hipGraphExec_t x : execs) (void)hipGraphExecDestroy(x);
+        for (hipGraph_t g : graphs) (void)hipGraphDestroy(g);
         if (cap_stream) (void)hipStreamDestroy(cap_stream);
         for (void* p : owned) (void)hipFree(p);
     }
 
-    // The kernels of one token step, in order, on stream s.
-    void enqueue_step(hipStream_t s) const {
+    // Replays the token-step graph for the position bound pos_hint, then
+    // advances the bound.
+    hipError_t launch_step() {
+        int k = pos_hint / bucket_pos;
+        k = k < static_cast<int>(execs.size()) ? k : static_cast<int>(execs.size()) - 1;
+        const hipError_t err = hipGraphLaunch(execs[k], stream);
+        pos_hint = pos_hint < max_seq ? pos_hint + 1 : max_seq;
+        return err;
+    }
+
+    // The kernels of one token step, in order, on stream s; the attention
+    // kernel runs on the first `splits` splits (positions below 64 * splits).
+    void enqueue_step(hipStream_t s, int splits) const {
         const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
         const int nkv = cfg.num_key_value_heads;
         const float eps = cfg.rms_norm_eps;
@@ -2402,8 +2425,8 @@ struct spb_engine {
                 launch_projection(seg_weights(&L.q_proj, &L.k_proj, &L.v_proj),
                                 p, st, sink, s);
             }
-            launch_attention(hd, nh / nkv, S, nkv, s, qkv, kcache[l], vcache[l], pm, pl, pacc, st,
-                             max_seq, scale);
+            launch_attention(hd, nh / nkv, S, splits, nkv, s, qkv, kcache[l], vcache[l], pm, pl,
+                             pacc, st, max_seq, scale);
             {
                 static_assert(kAttnSplit == 64, "the combine's split index is pos >> 6");
                 AttnCombine p{pm, pl, pacc, hd, S, nh * hd, hd == 64 ? 6 : 7};
@@ -2533,6 +2556,7 @@ int set_state(spb_engine* e, int pos, int prompt_len, int stop_eos) {
     // Synchronous with respect to the host: h lives on this stack frame.
     const int half = e->cfg.head_dim / 2;
     const int rp = pos < e->max_seq ? pos : e->max_seq - 1;
+    e->pos_hint = pos;
     if (hipMemcpyAsync(e->st, &h, sizeof(h), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
         hipMemcpyAsync(e->cur_rope, e->rope + static_cast<long>(rp) * half,
                        sizeof(float2) * half, hipMemcpyDeviceToDevice, e->stream) != hipSuccess ||
@@ -2626,13 +2650,27 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
         delete e;
         return launch_status(fn);
     }
-    // Capture one token step.
-    err = hipStreamBeginCapture(e->cap_stream, hipStreamCaptureModeThreadLocal);
-    if (err == hipSuccess) {
-        e->enqueue_step(e->cap_stream);
-        err = hipStreamEndCapture(e->cap_stream, &e->graph);
+    // Capture the token step once per position bucket: buckets of 8 splits
+    // (512 positions), or of S/8 splits past 64 splits (at most 8 graphs).
+    {
+        const int per = e->S <= 64 ? kAttnBucketSplits : (e->S + 7) / 8;
+        e->bucket_pos = per * kAttnSplit;
+        for (int s0 = 0; s0 < e->S && err == hipSuccess; s0 += per) {
+            const int splits = s0 + per < e->S ? s0 + per : e->S;
+            hipGraph_t g = nullptr;
+            hipGraphExec_t x = nullptr;
+            err = hipStreamBeginCapture(e->cap_stream, hipStreamCaptureModeThreadLocal);
+            if (err == hipSuccess) {
+                e->enqueue_step(e->cap_stream, splits);
+                err = hipStreamEndCapture(e->cap_stream, &g);
+            }
+            if (err == hipSuccess) {
+                e->graphs.push_back(g);
+                err = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+            }
+            if (err == hipSuccess) e->execs.push_back(x);
+        }
     }
-    if (err == hipSuccess) err = hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0);
     if (err != hipSuccess) {
         set_error("%s: graph capture failed: %s", fn, hipGetErrorString(err));
         delete e;
@@ -2704,7 +2742,8 @@ extern "C" int spb_engine_forward(spb_engine* e, int token_id, const float** d_l
         return launch_status(fn);
     // The host copy above is pageable: wait until it has been consumed.
     if (hipStreamSynchronize(e->stream) != hipSuccess) return launch_status(fn);
-    if (hipGraphLaunch(e->exec, e->stream) != hipSuccess) return launch_status(fn);
+    e->pos_hint = pos;
+    if (e->launch_step() != hipSuccess) return launch_status(fn);
     e->seq_len = pos + 1;
     if (d_logits) *d_logits = e->logits;
     return 0;
@@ -2743,7 +2782,7 @@ extern "C" int spb_engine_generate(spb_engine* e, const int* prompt, int n_promp
     }
     const int steps = n_prompt - 1 - start + n_new;
     for (int i = 0; i < steps; ++i)
-        if (hipGraphLaunch(e->exec, e->stream) != hipSuccess) return launch_status(fn);
+        if (e->launch_step() != hipSuccess) return launch_status(fn);
     EngineState h{};
     if (hipMemcpyAsync(&h, e->st, sizeof(h), hipMemcpyDeviceToHost, e->stream) != hipSuccess)
         return launch_status(fn);
@@ -2772,8 +2811,7 @@ extern "C" int spb_engine_decode_steps(spb_engine* e, int steps) {
     if (!e) return invalid("spb_engine_decode_steps: null engine");
     if (steps < 0) return invalid("spb_engine_decode_steps: steps < 0");
     for (int i = 0; i < steps; ++i)
-        if (hipGraphLaunch(e->exec, e->stream) != hipSuccess)
-            return launch_status("spb_engine_decode_steps");
+        if (e->launch_step() != hipSuccess) return launch_status("spb_engine_decode_steps");
     // the device advanced pos (unless the state is done): seq_len and forward
     // read it back when next asked
     if (steps > 0) e->pos_stale = true;
