@@ -32,6 +32,18 @@ int device_cu_count();
 // LDS bytes per compute unit of the current device (cached per device).
 int device_lds_per_cu();
 
+}  // namespace spb
+
+struct spb_sparse_linear;
+
+namespace spb {
+
+// Up to three stacked projections with equal columns and strides in one
+// matrix-core GEMM launch (gemm.hip); 1 = not possible (nothing launched),
+// 2 = launch error, 0 = launched.  Y is [n][sum of rows].
+int gemm_stacked(const spb_sparse_linear* const* segs, int nseg, const int8_t* X, int32_t* Y,
+                 int n, hipStream_t st);
+
 // ---- 16-bit float conversions (bit patterns in uint16_t) --------------------
 
 struct F16 {

@@ -1725,18 +1725,28 @@ LmKernel lm_head_for(int H) {
 }
 
 // Batched decode: the LM head for a group of gn <= kLmGroup sequences
-// (g0 .. g0 + gn - 1) of a batch.  Every row is computed exactly as
-// lm_head_kernel computes it (final RMSNorm in the unit order of kLmBlock
-// threads; lane l takes the 8-element chunks l, l + 64, ... of the row with
-// fma in element order; the 64-lane tree), once per sequence of the group,
-// so each sequence's logits equal those of a bs=1 step bit for bit.  The
-// normalised vectors of the group sit in LDS as float [gn][H]; a row's
-// weights are unpacked once and used for every sequence.  Per-sequence
-// argmax (lowest index among maxima) and decode-state update by the last
-// block to finish (ticket of the group's first sequence), as in the bs=1
-// kernel; sequences whose state is done are not updated.
+// (g0 .. g0 + gn - 1) of a batch.  Every logit is computed with exactly the
+// operations of lm_head_kernel: the final RMSNorm in the unit order of
+// kLmBlock threads, then, for each of 64 "virtual lanes" v, the fma chain
+// over the row's 8-element chunks v, v + 64, ... (element order), then the
+// balanced pairwise tree over the 64 virtual lanes.  Here eight real lanes
+// share a row and lane j of the eight carries virtual lanes 8j .. 8j + 7:
+// the tree's first three levels are adds inside the lane, the last three
+// DPP steps across the eight lanes (pair, quad, half-row mirror), so each
+// sequence's logits equal a bs=1 step's bit for bit.  A lane's eight chunks
+// of one 64-chunk step are contiguous (128 bytes of the row), and every
+// lane of the same j reads the same x chunks from LDS (a broadcast); the
+// normalised vectors sit in LDS as float with 16 bytes of padding per 8
+// chunks, so the eight j of a read fall in different banks.  A wave handles
+// 8 rows at a time; the row's weights are unpacked once and used for every
+// sequence.  Per-sequence argmax (lowest index among maxima) and
+// decode-state update by the last block to finish (ticket of the group's
+// first sequence), as in the bs=1 kernel; done sequences are not updated.
 constexpr int kLmGroup = 8;          // sequences per batched LM-head launch (at most)
 constexpr int kLmBatchMaxRows = 512;  // rows per block (grid >= vocab / 512)
+
+// float index of chunk c's first element in the padded LDS vector
+__device__ __forceinline__ int lm_xpad(int c) { return 8 * c + 4 * (c >> 3); }
 
 template <int NC, bool kFull>
 __global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
@@ -1748,48 +1758,47 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
     int gn) {
     constexpr int kWaves = kLmBlock / kWave;
     extern __shared__ __align__(16) float lds[];
-    float* xs = lds;                                          // [gn][H]
-    float* lg = lds + static_cast<long>(kLmGroup) * H;        // [gn][kLmBatchMaxRows]
+    const int nch = H >> 3;
+    const int xstride = lm_xpad(NC * kWave);          // floats per padded vector
+    float* xs = lds;                                   // [gn][xstride]
+    float* lg = lds + static_cast<long>(kLmGroup) * xstride;  // [gn][kLmBatchMaxRows]
     __shared__ float red[kLmGroup][kWaves];
     __shared__ float wv[kWaves];
     __shared__ int wi[kWaves];
     __shared__ int last;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int nch = H >> 3;
+    const int j = lane & 7, rg = lane >> 3;  // virtual lanes 8j .. 8j+7 of row group rg
     const int blk = blockIdx.x;
     const long b0 = static_cast<long>(blk) * rbase + (blk < rrem ? blk : rrem);
     const long b1 = b0 + rbase + (blk < rrem ? 1 : 0);
-    const long n = (b1 - b0 - wave + kWaves - 1) / kWaves;
-    const long i_last = n > 0 ? n - 1 : 0;
-    auto row_of = [&](long i) { return b0 + wave + (i <= i_last ? i : i_last) * kWaves; };
-    auto load_row = [&](long i, uint4 (&w)[NC]) {
-        const long r = row_of(i);
-        const uint4* wr = reinterpret_cast<const uint4*>(W + (r < V ? r : V - 1) * H);
-#pragma unroll
-        for (int k = 0; k < NC; ++k) {
-            const int c = lane + k * kWave;
-            if (kFull)
-                w[k] = nt_load(wr + c);
-            else
-                w[k] = c < nch ? nt_load(wr + c) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    uint4 wa[NC], wb[NC];
-    load_row(0, wa);
-    // final RMSNorm of each sequence of the group (lm_head_kernel's order)
+    const long noct = (b1 - b0 + 7) >> 3;  // row octets of the block
+    // final RMSNorm of each sequence of the group (lm_head_kernel's order),
+    // stored with the chunk padding
     constexpr bool kOne = NC * kWave <= kUnits * kLmBlock;
+    float* tmp = lg;  // the norm's unpadded vector (the staging area is free until the rows)
     for (int g = 0; g < gn; ++g) {
         const uint16_t* xg = x + static_cast<long>(g0 + g) * H;
         HeldWeights<kLmBlock> hw;
         HeldUnits<kLmBlock> hx;
         hx.load(xg, H >> 3, tid);
         hw.load(wn, H >> 3, tid);
-        const float ss = load_bf16_sumsq<kLmBlock, kOne>(xg, xs + static_cast<long>(g) * H, H >> 3,
-                                                         tid, nullptr, hx);
+        const float ss = load_bf16_sumsq<kLmBlock, kOne>(xg, tmp, H >> 3, tid, nullptr, hx);
         const float inv = inv_rms(block_sum<kLmBlock>(ss, red[g]), H, eps);
-        hw.template apply<kOne>(xs + static_cast<long>(g) * H, wn, inv, H >> 3, tid);
+        hw.template apply<kOne>(tmp, wn, inv, H >> 3, tid);
+        __syncthreads();
+        float* dst = xs + static_cast<long>(g) * xstride;
+        for (int c = tid; c < NC * kWave; c += kLmBlock) {
+            float f[8];
+            if (c < nch) {
+                load_f8(tmp + 8 * c, f);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) f[e] = 0.0f;
+            }
+            store_f8(dst + lm_xpad(c), f);
+        }
+        __syncthreads();  // tmp is rewritten by the next sequence
     }
-    __syncthreads();
 
     float best[kLmGroup];
     int best_i[kLmGroup];
@@ -1798,68 +1807,105 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
         best[g] = -INFINITY;
         best_i[g] = 0x7FFFFFFF;
     }
-    auto reduce_row = [&](long i, const uint4 (&w)[NC]) {
-        float wf[NC][8];
+    auto load_step = [&](long row, int k, uint4 (&w)[8]) {
+        const uint4* wr = reinterpret_cast<const uint4*>(W + (row < V ? row : V - 1) * H);
 #pragma unroll
-        for (int k = 0; k < NC; ++k) unpack_bf16x8(w[k], wf[k]);
-        const long r = row_of(i);
+        for (int i = 0; i < 8; ++i) {
+            const int c = k * kWave + 8 * j + i;
+            if (kFull)
+                w[i] = nt_load(wr + c);
+            else
+                w[i] = c < nch ? nt_load(wr + c) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    for (long o = wave; o < noct; o += kWaves) {
+        const long row = b0 + 8 * o + rg;
+        float acc[kLmGroup][8];
 #pragma unroll
-        for (int g = 0; g < kLmGroup; ++g) {
-            if (g < gn) {
-                const float* xg = xs + static_cast<long>(g) * H;
-                float acc = 0.0f;
+        for (int g = 0; g < kLmGroup; ++g)
 #pragma unroll
-                for (int k = 0; k < NC; ++k) {
-                    const int c = lane + k * kWave;
-                    if (kFull || c < nch) {
-                        float xv[8];
-                        load_f8(xg + 8 * c, xv);
+            for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+        uint4 wa[8], wb[8];
+        load_step(row, 0, wa);
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(wf[k][e], xv[e], acc);
+        for (int k = 0; k < NC; ++k) {
+            uint4 (&cur)[8] = (k & 1) ? wb : wa;
+            uint4 (&nxt)[8] = (k & 1) ? wa : wb;
+            if (k + 1 < NC) load_step(row, k + 1, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            float wf[8][8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) unpack_bf16x8(cur[i], wf[i]);
+#pragma unroll
+            for (int g = 0; g < kLmGroup; ++g) {
+                if (g < gn) {
+                    const float* xg = xs + static_cast<long>(g) * xstride;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        if (kFull || k * kWave + 8 * j + i < nch) {  // lm_head_kernel's chunks only
+                            float xv[8];
+                            load_f8(xg + lm_xpad(k * kWave + 8 * j + i), xv);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e)
+                                acc[g][i] = __builtin_fmaf(wf[i][e], xv[e], acc[g][i]);
+                        }
                     }
-                }
-                acc = wave_sum_tree(acc);
-                if (lane == 0) lg[g * kLmBatchMaxRows + (r - b0)] = acc;
-                if (acc > best[g]) {  // rows ascend within a wave: the first maximum stays
-                    best[g] = acc;
-                    best_i[g] = static_cast<int>(r);
                 }
             }
         }
-    };
-    long i = 0;
-    for (long p = 0; p < n / 2; ++p, i += 2) {
-        load_row(i + 1, wb);
-        __builtin_amdgcn_sched_barrier(0);
-        reduce_row(i, wa);
-        load_row(i + 2, wa);
-        __builtin_amdgcn_sched_barrier(0);
-        reduce_row(i + 1, wb);
+#pragma unroll
+        for (int g = 0; g < kLmGroup; ++g) {
+            if (g < gn) {
+                // the 64-virtual-lane tree: three levels in the lane, three across
+                float t = ((acc[g][0] + acc[g][1]) + (acc[g][2] + acc[g][3])) +
+                          ((acc[g][4] + acc[g][5]) + (acc[g][6] + acc[g][7]));
+                t += dpp_f<0xB1>(t);   // quad_perm [1,0,3,2]: 16 virtual lanes
+                t += dpp_f<0x4E>(t);   // quad_perm [2,3,0,1]: 32
+                t += dpp_f<0x141>(t);  // row_half_mirror: 64
+                if (j == 0 && row < b1) {
+                    lg[g * kLmBatchMaxRows + (row - b0)] = t;
+                    if (t > best[g]) {  // a lane's rows ascend: strict > keeps the first maximum
+                        best[g] = t;
+                        best_i[g] = static_cast<int>(row);
+                    }
+                }
+            }
+        }
     }
-    if (n > 0 && (n & 1)) reduce_row(i, wa);
     __syncthreads();
     for (int g = 0; g < gn; ++g)
-        for (long j = tid; j < b1 - b0; j += kLmBlock)
-            logits[static_cast<long>(g0 + g) * V + b0 + j] = lg[g * kLmBatchMaxRows + j];
-    // per-sequence block maxima
+        for (long jj = tid; jj < b1 - b0; jj += kLmBlock)
+            logits[static_cast<long>(g0 + g) * V + b0 + jj] = lg[g * kLmBatchMaxRows + jj];
+    // per-sequence block maxima: the eight row groups of each wave, then the waves
 #pragma unroll
     for (int g = 0; g < kLmGroup; ++g) {
         if (g < gn) {
+            float bv = best[g];
+            int bi = best_i[g];
+#pragma unroll
+            for (int off = 8; off < kWave; off <<= 1) {
+                const float ov = __shfl_xor(bv, off, kWave);
+                const int oi = __shfl_xor(bi, off, kWave);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
             if (lane == 0) {
-                wv[wave] = best[g];
-                wi[wave] = best_i[g];
+                wv[wave] = bv;
+                wi[wave] = bi;
             }
             __syncthreads();
             if (tid == 0) {
-                float bv = wv[0];
-                int bi = wi[0];
+                float b = wv[0];
+                int bb = wi[0];
                 for (int w = 1; w < kWaves; ++w)
-                    if (wv[w] > bv || (wv[w] == bv && wi[w] < bi)) {
-                        bv = wv[w];
-                        bi = wi[w];
+                    if (wv[w] > b || (wv[w] == b && wi[w] < bb)) {
+                        b = wv[w];
+                        bb = wi[w];
                     }
-                part_v[static_cast<long>(g0 + g) * gridDim.x + blockIdx.x] = bv;
-                part_i[static_cast<long>(g0 + g) * gridDim.x + blockIdx.x] = bi;
+                part_v[static_cast<long>(g0 + g) * gridDim.x + blockIdx.x] = b;
+                part_i[static_cast<long>(g0 + g) * gridDim.x + blockIdx.x] = bb;
             }
             __syncthreads();
         }
@@ -1956,8 +2002,10 @@ LmBatchKernel lm_head_batch_for(int H) {
 }
 
 size_t lm_head_batch_lds(int H) {
-    return (static_cast<size_t>(kLmGroup) * H + static_cast<size_t>(kLmGroup) * kLmBatchMaxRows) *
-           sizeof(float);
+    const int nc = (H / 8 + kWave - 1) / kWave;
+    const size_t xstride = 8 * (nc * kWave) + 4 * ((nc * kWave) >> 3);  // lm_xpad(nc * 64)
+    return (static_cast<size_t>(kLmGroup) * xstride +
+            static_cast<size_t>(kLmGroup) * kLmBatchMaxRows) * sizeof(float);
 }
 
 // ---- random-init weights (model generation on the device) ------------------------
@@ -2083,9 +2131,11 @@ bool alloc_prefill(PrefillBufs& pf, const spb_model_config& cfg, int S, std::vec
     pf.chunk = static_cast<int>(c > 0 ? c : 1);
     const size_t C = static_cast<size_t>(pf.chunk);
     const size_t xmax = static_cast<size_t>(std::max(std::max(H, I), nh * hd));
+    // y[0] also holds the stacked q|k|v and gate|up products
     const size_t ymax = static_cast<size_t>(std::max(std::max(nh * hd, kvdim), std::max(H, I)));
+    const size_t ystack = std::max(ymax, static_cast<size_t>(std::max(nh * hd + 2 * kvdim, 2 * I)));
     return (pf.x = dev_alloc<int8_t>(C * xmax, own)) && (pf.amax = dev_alloc<float>(C, own)) &&
-           (pf.y[0] = dev_alloc<int32_t>(C * ymax, own)) &&
+           (pf.y[0] = dev_alloc<int32_t>(C * ystack, own)) &&
            (pf.y[1] = dev_alloc<int32_t>(C * ymax, own)) &&
            (pf.y[2] = dev_alloc<int32_t>(C * ymax, own)) &&
            (pf.qkv = dev_alloc<uint16_t>(C * (nh * hd + 2 * kvdim), own)) &&
@@ -2224,6 +2274,36 @@ struct PrefillTarget {
     const int* tokens;
 };
 
+// The int32 products of up to three projections of the same int8 input X
+// ([n][cols]): one stacked matrix-core launch when gemm_stacked takes them
+// (equal columns and strides), else one launch each into y[0..nw).  out[i]
+// and ld[i]: where projection i's rows are and their row stride.
+hipError_t gemm_group(const spb_sparse_linear* const* w, int nw, const int8_t* X,
+                      int32_t* const* y, int n, hipStream_t s, const int32_t** out, int* ld) {
+    if (gemm_stacked(w, nw, X, y[0], n, s) == 0) {
+        int rows = 0;
+        for (int i = 0; i < nw; ++i) rows += w[i]->rows;
+        int off = 0;
+        for (int i = 0; i < 3; ++i) {
+            const int k = i < nw ? i : nw - 1;
+            out[i] = y[0] + (i < nw ? off : off - w[k]->rows);
+            ld[i] = rows;
+            if (i < nw) off += w[i]->rows;
+        }
+        return hipSuccess;
+    }
+    for (int i = 0; i < 3; ++i) {
+        const int k = i < nw ? i : nw - 1;
+        if (i < nw && spb_sparse_ternary_gemm(w[i]->meta, w[i]->values, X, y[i], w[i]->rows,
+                                              w[i]->cols, n, w[i]->meta_stride,
+                                              w[i]->values_stride, s))
+            return hipErrorLaunchFailure;
+        out[i] = y[k];
+        ld[i] = w[k]->rows;
+    }
+    return hipSuccess;
+}
+
 // Positions pos0 .. pos0 + c - 1 of one sequence (t.tokens holds their ids)
 // through every layer, c <= pf.chunk: the KV cache of those positions as c
 // decode steps would write it.  Returns a HIP error or hipSuccess.
@@ -2264,7 +2344,10 @@ auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
                         H};
             launch_prefill_producer(p, H, pf.st, H, c, pf.x, pf.amax, s);
         }
-        if (gemm(L.q_proj, pf.y[0]) || gemm(L.k_proj, pf.y[1]) || gemm(L.v_proj, pf.y[2]))
+        const spb_sparse_linear* qkv3[3] = {&L.q_proj, &L.k_proj, &L.v_proj};
+        const int32_t* yq[3];
+        int ldq[3];
+        if (gemm_group(qkv3, 3, pf.x, pf.y, c, s, yq, ldq) != hipSuccess)
             return hipErrorLaunchFailure;
         {
             QkvRopeSink sink{};
@@ -2282,9 +2365,8 @@ auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
             sink.max_seq = max_seq;
             sink.rope_tab = rope;
             sink.rope_pos0 = pos0;
-            launch_prefill_sink(sink, qrows + 2 * kvdim, pf.amax, pf.y[0], pf.y[1], pf.y[2],
-                                qrows, qrows + kvdim, qrows + 2 * kvdim, qrows, kvdim, kvdim,
-                                c, s);
+            launch_prefill_sink(sink, qrows + 2 * kvdim, pf.amax, yq[0], yq[1], yq[2], qrows,
+                                qrows + kvdim, qrows + 2 * kvdim, ldq[0], ldq[1], ldq[2], c, s);
         }
         // splits that some token of the pass reaches
         const int sp = (pos0 + c - 1) / kAttnSplit + 1 < S ? (pos0 + c - 1) / kAttnSplit + 1 : S;
@@ -2312,13 +2394,16 @@ auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
                                   L.post_attention_layernorm, eps, H};
             launch_prefill_producer(p, H, pf.st, H, c, pf.x, pf.amax, s);
         }
-        if (gemm(L.gate_proj, pf.y[0]) || gemm(L.up_proj, pf.y[1]))
+        const spb_sparse_linear* gu2[2] = {&L.gate_proj, &L.up_proj};
+        const int32_t* yg[3];
+        int ldg[3];
+        if (gemm_group(gu2, 2, pf.x, pf.y, c, s, yg, ldg) != hipSuccess)
             return hipErrorLaunchFailure;
         {
             SegBf16Sink sink{pf.gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
                              I, 2 * I, 0.f, 0.f, 0.f};
-            launch_prefill_sink(sink, 2 * I, pf.amax, pf.y[0], pf.y[1], pf.y[1], I, 2 * I,
-                                2 * I, I, I, I, c, s);
+            launch_prefill_sink(sink, 2 * I, pf.amax, yg[0], yg[1], yg[2], I, 2 * I, 2 * I,
+                                ldg[0], ldg[1], ldg[2], c, s);
         }
         {
             Relu2Norm p{pf.gu, pf.gu + I, L.ffn_sub_norm,
@@ -2960,8 +3045,10 @@ struct spb_batch_engine {
                 p.tok_stride = tok_stride();
                 launch_prefill_producer(p, H, st, H, B, step.x, step.amax, s);
             }
-            if (gemm(L.q_proj, step.y[0]) || gemm(L.k_proj, step.y[1]) ||
-                gemm(L.v_proj, step.y[2]))
+            const spb_sparse_linear* qkv3[3] = {&L.q_proj, &L.k_proj, &L.v_proj};
+            const int32_t* yq[3];
+            int ldq[3];
+            if (gemm_group(qkv3, 3, step.x, step.y, B, s, yq, ldq) != hipSuccess)
                 return hipErrorLaunchFailure;
             {
                 QkvRopeSink sink{};
@@ -2980,9 +3067,9 @@ struct spb_batch_engine {
                 sink.max_seq = max_seq;
                 sink.rope_tab = nullptr;  // each sequence's own RoPE row (cur_rope)
                 sink.kv_stride = kv_seq;
-                launch_prefill_sink(sink, qrows + 2 * kvdim, step.amax, step.y[0], step.y[1],
-                                    step.y[2], qrows, qrows + kvdim, qrows + 2 * kvdim, qrows,
-                                    kvdim, kvdim, B, s);
+                launch_prefill_sink(sink, qrows + 2 * kvdim, step.amax, yq[0], yq[1], yq[2],
+                                    qrows, qrows + kvdim, qrows + 2 * kvdim, ldq[0], ldq[1],
+                                    ldq[2], B, s);
             }
             launch_attention_batch(hd, nh / nkv, S, nkv, B, s, step.qkv, kcache[l], vcache[l],
                                    step.pm, step.pl, step.pacc, st, max_seq, scale,
@@ -3003,13 +3090,16 @@ struct spb_batch_engine {
                                       L.post_attention_layernorm, eps, H};
                 launch_prefill_producer(p, H, st, H, B, step.x, step.amax, s);
             }
-            if (gemm(L.gate_proj, step.y[0]) || gemm(L.up_proj, step.y[1]))
+            const spb_sparse_linear* gu2[2] = {&L.gate_proj, &L.up_proj};
+            const int32_t* yg[3];
+            int ldg[3];
+            if (gemm_group(gu2, 2, step.x, step.y, B, s, yg, ldg) != hipSuccess)
                 return hipErrorLaunchFailure;
             {
                 SegBf16Sink sink{step.gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
                                  I, 2 * I, 0.f, 0.f, 0.f};
-                launch_prefill_sink(sink, 2 * I, step.amax, step.y[0], step.y[1], step.y[1], I,
-                                    2 * I, 2 * I, I, I, I, B, s);
+                launch_prefill_sink(sink, 2 * I, step.amax, yg[0], yg[1], yg[2], I, 2 * I, 2 * I,
+                                    ldg[0], ldg[1], ldg[2], B, s);
             }
             {
                 Relu2Norm p{step.gu, step.gu + I, L.ffn_sub_norm,

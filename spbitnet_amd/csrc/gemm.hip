@@ -39,6 +39,16 @@
 namespace spb {
 namespace {
 
+// Up to three matrices stacked along the rows (q | k | v, gate | up), with
+// equal columns and strides: rows [0, end0) are the first, [end0, end1) the
+// second (words at meta + om1 for global row r, i.e. om1 = offset of the
+// second matrix - end0 * ms), [end1, rows) the third.  One matrix: end0 =
+// end1 = rows.
+struct GemmSegs {
+    long om1, om2, ov1, ov2;
+    int end0, end1;
+};
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -83,13 +93,20 @@ template <int kStrips, int kTiles, int kWaves>
 __global__ __launch_bounds__(kWaves * kWave) void gemm_smfmac_kernel(
     const uint32_t* __restrict__ meta, const uint32_t* __restrict__ values,
     const int8_t* __restrict__ X, int32_t* __restrict__ Y, int rows, int cols, int n, int ms,
-    int vs) {
+    int vs, GemmSegs segs) {
     constexpr int kBlock = kWaves * kWave;
     constexpr int kAcc = kStrips * kTiles * 4;  // int32 accumulators per lane
     __shared__ int red[kAcc * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const long r0 = static_cast<long>(blockIdx.x) * (kStrips * 16);
+    // stacked matrices: the block's rows lie in one segment, whose words sit
+    // at a fixed offset from the row's index in the first (uniform selects)
+    if (r0 >= segs.end0) {
+        const bool last = r0 >= segs.end1;
+        meta += last ? segs.om2 : segs.om1;
+        values += last ? segs.ov2 : segs.ov1;
+    }
     const int tok0 = blockIdx.y * (kTiles * 16);
     const int q = lane >> 4;   // lane group
     const int li = lane & 15;  // A row / B,C token within a tile
@@ -194,10 +211,44 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 template <int kStrips, int kTiles, int kWaves>
 void launch_smfmac(const uint32_t* meta, const uint32_t* values, const int8_t* X, int32_t* Y,
-                   int rows, int cols, int n, int ms, int vs, hipStream_t st) {
+                   int rows, int cols, int n, int ms, int vs, hipStream_t st,
+                   const GemmSegs* segs = nullptr) {
     const dim3 grid((rows + kStrips * 16 - 1) / (kStrips * 16), (n + kTiles * 16 - 1) / (kTiles * 16));
+    const GemmSegs one{0, 0, 0, 0, rows, rows};
     hipLaunchKernelGGL((gemm_smfmac_kernel<kStrips, kTiles, kWaves>), grid, dim3(kWaves * kWave),
-                       0, st, meta, values, X, Y, rows, cols, n, ms, vs);
+                       0, st, meta, values, X, Y, rows, cols, n, ms, vs, segs ? *segs : one);
+}
+
+// The tile shape spb_sparse_ternary_gemm takes for n tokens over `rows`
+// rows: strips (16-row strips per block), tiles (16-token tiles per pass).
+void smfmac_tiles(int rows, int n, int* strips, int* tiles) {
+    if (n <= 16) {
+        *strips = 2, *tiles = 1;
+    } else if (n <= 64) {
+        *strips = 2, *tiles = 4;
+    } else {
+        const long cus = device_cu_count();
+        const long tl = (n + 63) / 64;
+        auto blocks = [&](int st) { return (rows + 16L * st - 1) / (16L * st) * tl; };
+        *tiles = 4;
+        *strips = blocks(8) * 5 >= cus * 3 ? 8 : (blocks(4) * 5 >= cus * 3 ? 4 : 2);
+    }
+}
+
+int launch_smfmac_for(const uint32_t* meta, const uint32_t* values, const int8_t* X, int32_t* Y,
+                      int rows, int cols, int n, int ms, int vs, hipStream_t st,
+                      const GemmSegs* segs) {
+    int strips = 0, tiles = 0;
+    smfmac_tiles(rows, n, &strips, &tiles);
+    if (strips == 2 && tiles == 1)
+        launch_smfmac<2, 1, 4>(meta, values, X, Y, rows, cols, n, ms, vs, st, segs);
+    else if (strips == 2)
+        launch_smfmac<2, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st, segs);
+    else if (strips == 4)
+        launch_smfmac<4, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st, segs);
+    else
+        launch_smfmac<8, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st, segs);
+    return 0;
 }
 
 }  // namespace
@@ -233,28 +284,14 @@ extern "C" int spb_sparse_ternary_gemm(const uint32_t* meta, const uint32_t* val
         // Rows per block (16 * strips), tokens per pass (16 * tiles) and waves
         // per block, chosen by measurement at 6912x2560: larger tiles as the
         // batch grows, so each activation tile read from L2 feeds more
-        // matrix-core operations.
-        if (n <= 16) {
-            launch_smfmac<2, 1, 4>(meta, values, X, Y, rows, cols, n, ms, vs, st);
-        } else if (n <= 64) {
-            launch_smfmac<2, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
-        } else {
-            if ((n + 63) / 64 > 65535) return invalid("%s: batch %d too large", fn, n);
-            // The deepest row tile whose grid still gives ~0.6 blocks per CU:
-            // on MI355X, 6912x2560 ran 21 us at n=256 with 8 strips (216
-            // blocks) against 25 with 4; 2560x2560-class and 640-row shapes,
-            // whose 8-strip grids leave most CUs idle, ran up to 2x faster
-            // with 4 or 2 strips (640x2560, n=256: 19.3 -> 9.5 us).
-            const long cus = device_cu_count();
-            const long tiles = (n + 63) / 64;
-            auto blocks = [&](int strips) { return (rows + 16L * strips - 1) / (16L * strips) * tiles; };
-            if (blocks(8) * 5 >= cus * 3)
-                launch_smfmac<8, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
-            else if (blocks(4) * 5 >= cus * 3)
-                launch_smfmac<4, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
-            else
-                launch_smfmac<2, 4, 8>(meta, values, X, Y, rows, cols, n, ms, vs, st);
-        }
+        // matrix-core operations.  Above 64 tokens, the deepest row tile
+        // whose grid still gives ~0.6 blocks per CU: on MI355X, 6912x2560 ran
+        // 21 us at n=256 with 8 strips (216 blocks) against 25 with 4;
+        // 2560x2560-class and 640-row shapes, whose 8-strip grids leave most
+        // CUs idle, ran up to 2x faster with 4 or 2 strips (640x2560, n=256:
+        // 19.3 -> 9.5 us).
+        if ((n + 15) / 16 > 65535) return invalid("%s: batch %d too large", fn, n);
+        launch_smfmac_for(meta, values, X, Y, rows, cols, n, ms, vs, st, nullptr);
     } else {
         if (n > 65535) return invalid("%s: batch %d exceeds 65535", fn, n);
         hipLaunchKernelGGL(gemm_general_kernel, dim3((rows + 3) / 4, n), dim3(256), 0, st, meta,
@@ -262,3 +299,54 @@ extern "C" int spb_sparse_ternary_gemm(const uint32_t* meta, const uint32_t* val
     }
     return launch_status(fn);
 }
+
+namespace spb {
+
+// Y [n][sum of rows] = (A | B | C) X for up to three stacked projections
+// (the engines' q | k | v and gate | up) in one matrix-core launch.
+// Returns 1 (nothing launched) when the shapes do not allow it: columns or
+// strides differ, the matrix-core conditions fail, or a segment boundary
+// falls inside a block's row tile; the caller then launches them apart.
+int gemm_stacked(const spb_sparse_linear* const* segs, int nseg, const int8_t* X, int32_t* Y,
+                 int n, hipStream_t st) {
+    if (nseg < 1 || nseg > 3 || n <= 0) return 1;
+    const spb_sparse_linear& a = *segs[0];
+    int rows = 0, ends[3] = {0, 0, 0};
+    for (int i = 0; i < nseg; ++i) {
+        const spb_sparse_linear& l = *segs[i];
+        if (l.cols != a.cols || l.meta_stride != a.meta_stride ||
+            l.values_stride != a.values_stride || !l.meta || !l.values)
+            return 1;
+        rows += l.rows;
+        ends[i] = rows;
+    }
+    if (!spb_sparse_ternary_gemm_kernel_id(a.meta, a.values, X, rows, a.cols, n, a.meta_stride,
+                                           a.values_stride) ||
+        (n + 15) / 16 > 65535)
+        return 1;
+    int strips = 0, tiles = 0;
+    smfmac_tiles(rows, n, &strips, &tiles);
+    GemmSegs g{0, 0, 0, 0, ends[0], nseg > 1 ? ends[1] : ends[0]};
+    if (nseg == 1) g.end0 = g.end1 = rows;
+    for (int i = 1; i < nseg; ++i) {
+        if (ends[i - 1] % (16 * strips)) return 1;
+        const long om = (segs[i]->meta - a.meta) - static_cast<long>(ends[i - 1]) * a.meta_stride;
+        const long ov = (segs[i]->values - a.values) -
+                        static_cast<long>(ends[i - 1]) * a.values_stride;
+        if (i == 1) {
+            g.om1 = om;
+            g.ov1 = ov;
+            g.om2 = om;  // two segments: rows past end1 do not exist
+            g.ov2 = ov;
+        } else {
+            g.om2 = om;
+            g.ov2 = ov;
+        }
+    }
+    if (nseg == 2) g.end1 = rows;
+    launch_smfmac_for(a.meta, a.values, X, Y, rows, a.cols, n, a.meta_stride, a.values_stride,
+                      st, &g);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // namespace spb
