@@ -44,6 +44,11 @@ namespace spb {
 int gemm_stacked(const spb_sparse_linear* const* segs, int nseg, const int8_t* X, int32_t* Y,
                  int n, hipStream_t st);
 
+// Raises the LDS limit of the matrix-core GEMM kernels that need more than
+// 64 KB on the current device (idempotent; 0 = done).  Engines call it before
+// capturing graphs, so no attribute change happens inside a capture.
+int gemm_prepare();
+
 // ---- 16-bit float conversions (bit patterns in uint16_t) --------------------
 
 struct F16 {

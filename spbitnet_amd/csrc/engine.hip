@@ -2673,6 +2673,7 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
         return invalid("%s: null argument", fn);
     *out = nullptr;
     if (int rc = check_model(fn, cfg, layers, embed_tokens, lm_head, max_seq)) return rc;
+    if (gemm_prepare() != 0) return launch_status(fn);  // before any graph capture
     const int H = cfg->hidden_size, nh = cfg->num_attention_heads, nkv = cfg->num_key_value_heads;
     const int hd = cfg->head_dim, I = cfg->intermediate_size, V = cfg->vocab_size;
     const int kvdim = nkv * hd;
@@ -3191,7 +3192,8 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
     // exceed 64 KB (96 KB at hidden 2560)
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(e->lm_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(lm_head_batch_lds(H))) != hipSuccess) {
+                            static_cast<int>(lm_head_batch_lds(H))) != hipSuccess ||
+        gemm_prepare() != 0) {
         delete e;
         return launch_status(fn);
     }

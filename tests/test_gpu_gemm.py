@@ -80,3 +80,34 @@ def test_gemm_addsub_comparator(gpu, n):
     L = W.random_layer(rows, cols, W.seed_for("addsub", n))
     X = activations(n, cols, 77)
     assert (run(L, X, gpu, kernel="addsub") == expected(L, X)).all()
+
+
+@pytest.mark.parametrize("rows,cols,n", [(2560, 6912, 64), (2560, 6912, 256), (96, 768, 33),
+                                         (48, 2816, 16), (200, 512, 70), (64, 256, 64)])
+def test_gemm_partial_chunks_and_tiles(gpu, rows, cols, n):
+    """Column counts whose last staged chunk is partial (6912 = 27 column
+    pairs, 2816 = 11, 768 = 3), row counts that end inside a row block and
+    batches that end inside a token tile."""
+    L = W.random_layer(rows, cols, W.seed_for("gemm-chunks", rows, cols, n))
+    X = np.random.default_rng(rows * 7 + cols + n).integers(-128, 128, (n, cols)).astype(np.int8)
+    assert (run(L, X, gpu) == expected(L, X)).all()
+
+
+@pytest.mark.parametrize("pad_m,pad_v", [(4, 4), (8, 0), (1, 0), (0, 2), (3, 5)])
+@pytest.mark.parametrize("n", [16, 64, 200])
+def test_gemm_padded_strides(gpu, pad_m, pad_v, n):
+    """Row strides past the format's minimum: multiples of 4 words keep the
+    staged matrix-core kernel, others take the direct one; both exact, and the
+    padding words (all ones, invalid bitmaps) change nothing."""
+    rows, cols = 160, 2560
+    L = W.random_layer(rows, cols, W.seed_for("gemm-pad", pad_m, pad_v, n))
+    meta = np.full((rows, L.meta_stride + pad_m), 0xFFFFFFFF, np.uint32)
+    values = np.full((rows, L.values_stride + pad_v), 0xFFFFFFFF, np.uint32)
+    meta[:, :L.meta_stride] = L.meta
+    values[:, :L.values_stride] = L.values
+    X = activations(n, cols, 500 + pad_m + pad_v)
+    Y = torch.full((n, rows), -7, dtype=torch.int32, device=gpu)
+    K.sparse_ternary_gemm_gpu(dev_u32(meta, gpu), dev_u32(values, gpu), dev(X, gpu), Y, rows,
+                              cols, n, meta.shape[1], values.shape[1])
+    torch.cuda.synchronize()
+    assert (Y.cpu().numpy() == expected(L, X)).all()
