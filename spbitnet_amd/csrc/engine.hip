@@ -636,6 +636,73 @@ struct AttnCombine {
     }
 };
 
+// The o projection's input when attn_combine_kernel has already folded the
+// splits (long contexts): the nh * hd floats it wrote, which are exactly the
+// values AttnCombine computes (same operations in the same order), so the
+// quantised input and the outputs are unchanged.
+struct CombinedAttn {
+    static constexpr int kAux = 0;
+    const float* v;  // [nh * hd], bf16-rounded
+    int n;
+    __device__ void at(int, long) {}
+    struct Regs {
+        float4 a[kUnits], b[kUnits];
+    };
+    template <int KU>
+    __device__ void issue(int tid, const EngineState*, Regs& r) const {
+        const int units = n >> 3;
+#pragma unroll
+        for (int k = 0; k < KU; ++k) {
+            const int u = tid + k * kBlock < units ? tid + k * kBlock : units - 1;
+            r.a[k] = reinterpret_cast<const float4*>(v)[2 * u];
+            r.b[k] = reinterpret_cast<const float4*>(v)[2 * u + 1];
+        }
+    }
+    int units_per_thread() const {
+        const int u = n >> 3;
+        return u <= kBlock ? 1 : (u <= kUnits * kBlock ? 2 : 0);
+    }
+    template <int KU>
+    __device__ float fill_one(float (&vv)[kUnits][8], int tid, float*, const EngineState*,
+                              Regs& r) const {
+        const int units = n >> 3;
+        float mx = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KU; ++k) {
+            if (tid + k * kBlock < units) {
+                const float f[8] = {r.a[k].x, r.a[k].y, r.a[k].z, r.a[k].w,
+                                    r.b[k].x, r.b[k].y, r.b[k].z, r.b[k].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    vv[k][e] = f[e];
+                    mx = __builtin_fmaxf(mx, __builtin_fabsf(f[e]));
+                }
+            }
+        }
+        return mx;
+    }
+    template <bool kOne>
+    __device__ float fill(float* vec, float*, int, int tid, float*, const EngineState*,
+                          Regs& r) const {
+        const int units = n >> 3;
+        float mx = 0.0f;
+        for (int u = tid, k = 0; u < units; u += kBlock, ++k) {
+            float f[8];
+            if (k < kUnits) {
+                const float4 a = r.a[k < kUnits ? k : 0], b = r.b[k < kUnits ? k : 0];
+                f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w;
+                f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
+            } else {
+                load_f8(v + 8 * u, f);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = __builtin_fmaxf(mx, __builtin_fabsf(f[e]));
+            store_f8(vec + 8 * u, f);
+        }
+        return mx;
+    }
+};
+
 // gate/up input: o = RMSNorm(o; attn_sub_norm) (skipped when absent),
 // x = bf16(o + r) (block 0 stores it as the new residual), then
 // RMSNorm(x; post_attention_layernorm).  Reference inference.cu:205-230.
@@ -1171,6 +1238,68 @@ __device__ __forceinline__ void attention_split(const uint4 (&kq)[G][HD / 32], f
             pl[h * S + s] = hsum[g];
         }
     }
+}
+
+// Split combine of one decode step, once per head (long contexts): block h
+// folds head h's splits 0 .. ns - 1 (those holding positions 0 .. pos) with
+// AttnCombine::combine's operations in its order: M = max of the split
+// maxima, w_s = exp(m_s - M) (computed once per split here, by one thread,
+// and shared through LDS), then l and each element's sum accumulated split
+// by split; thread d writes bf16r(sum_d / l).  The element's partials of the
+// first kCombineBatch splits are loaded before anything else.
+constexpr int kCombineBatch = 64;
+// Token-step graphs whose attention reaches at most this many splits keep the
+// combine in the o projection's prologue; longer ones launch attn_combine_kernel.
+constexpr int kFusedCombineSplits = 8;
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ pm,
+                                                          const float* __restrict__ pl,
+                                                          const float* __restrict__ pacc,
+                                                          float* __restrict__ out,
+                                                          const EngineState* __restrict__ st,
+                                                          int S) {
+    extern __shared__ float wl[];  // [2][S]: w_s, l_s
+    __shared__ float red[HD / kWave];
+    const int h = blockIdx.x, d = threadIdx.x, lane = d & (kWave - 1), wave = d / kWave;
+    const int pos = state_pos(st);
+    int ns = (pos >> 6) + 1;
+    ns = ns < S ? ns : S;
+    const float* mh = pm + static_cast<long>(h) * S;
+    const float* lh = pl + static_cast<long>(h) * S;
+    const float* ph = pacc + static_cast<long>(h) * S * HD + d;
+    float pv[kCombineBatch];
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) pv[k] = ph[static_cast<long>(k < ns ? k : ns - 1) * HD];
+    float M = -INFINITY;
+    for (int s = d; s < ns; s += HD) M = __builtin_fmaxf(M, mh[s]);
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) M = __builtin_fmaxf(M, __shfl_xor(M, off, kWave));
+    if (lane == 0) red[wave] = M;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < HD / kWave; ++w) M = __builtin_fmaxf(M, red[w]);
+    for (int s = d; s < ns; s += HD) {
+        wl[s] = exp_neg(mh[s] - M);
+        wl[S + s] = lh[s];
+    }
+    __syncthreads();
+    float l = 0.0f, a = 0.0f;
+    for (int s0 = 0; s0 < ns; s0 += kCombineBatch) {
+        if (s0) {
+#pragma unroll
+            for (int k = 0; k < kCombineBatch; ++k)
+                pv[k] = ph[static_cast<long>(s0 + k < ns ? s0 + k : ns - 1) * HD];
+        }
+#pragma unroll
+        for (int k = 0; k < kCombineBatch; ++k) {
+            if (s0 + k < ns) {
+                const float w = wl[s0 + k];
+                l = __builtin_fmaf(w, wl[S + s0 + k], l);
+                a = __builtin_fmaf(w, pv[k], a);
+            }
+        }
+    }
+    out[h * HD + d] = bf16r(a / l);
 }
 
 template <int HD, int G>
@@ -2435,6 +2564,7 @@ struct spb_engine {
     std::vector<uint16_t*> kcache, vcache;
     uint16_t *xa = nullptr, *xb = nullptr, *qkv = nullptr, *obuf = nullptr, *gu = nullptr;
     float *pm = nullptr, *pl = nullptr, *pacc = nullptr, *logits = nullptr, *part_v = nullptr;
+    float* comb = nullptr;  // combined attention output (steps past kFusedCombineSplits splits)
     int* part_i = nullptr;
     int* tokens = nullptr;
     float2* rope = nullptr;
@@ -2514,10 +2644,24 @@ struct spb_engine {
                              pacc, st, max_seq, scale);
             {
                 static_assert(kAttnSplit == 64, "the combine's split index is pos >> 6");
-                AttnCombine p{pm, pl, pacc, hd, S, nh * hd, hd == 64 ? 6 : 7};
                 SegBf16Sink sink{obuf, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma,
                                  L.o_proj.rows, L.o_proj.rows, 0.f, 0.f, 0.f};
-                launch_projection(single_weights(L.o_proj), p, st, sink, s);
+                if (splits <= kFusedCombineSplits) {
+                    // every block of the o projection folds the splits itself
+                    AttnCombine p{pm, pl, pacc, hd, S, nh * hd, hd == 64 ? 6 : 7};
+                    launch_projection(single_weights(L.o_proj), p, st, sink, s);
+                } else {
+                    // long contexts: fold once per head, then read the result
+                    const size_t lds = 2 * static_cast<size_t>(S) * sizeof(float);
+                    if (hd == 64)
+                        hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(nh), dim3(64), lds, s,
+                                           pm, pl, pacc, comb, st, S);
+                    else
+                        hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(nh), dim3(128), lds, s,
+                                           pm, pl, pacc, comb, st, S);
+                    CombinedAttn p{comb, nh * hd};
+                    launch_projection(single_weights(L.o_proj), p, st, sink, s);
+                }
             }
             {
                 SubNormResidualNorm p{obuf, xa, xb, L.attn_sub_norm, L.post_attention_layernorm,
@@ -2712,6 +2856,7 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
          (e->pm = dev_alloc<float>(static_cast<size_t>(nh) * e->S, own)) &&
          (e->pl = dev_alloc<float>(static_cast<size_t>(nh) * e->S, own)) &&
          (e->pacc = dev_alloc<float>(static_cast<size_t>(nh) * e->S * hd, own)) &&
+         (e->comb = dev_alloc<float>(static_cast<size_t>(nh) * hd, own)) &&
          (e->logits = dev_alloc<float>(V, own)) &&
          (e->part_v = dev_alloc<float>(e->lm_grid, own)) &&
          (e->part_i = dev_alloc<int>(e->lm_grid, own)) &&
