@@ -200,6 +200,9 @@ def main() -> int:
                     help="config 4: skip timing the prefill as one decode step per token")
     ap.add_argument("--only-batch-decode", action="store_true",
                     help="profiling: run only the config-4 batched decode (no JSON line)")
+    ap.add_argument("--only-mall-resident", action="store_true",
+                    help="profiling: run only the Infinity-Cache-resident GEMV protocol "
+                         "(for a rocprofv3 FETCH_SIZE pass) and print its timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB once (known bytes, for scaling rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE) and exit")
@@ -260,6 +263,10 @@ def main() -> int:
         return (dense @ xx.astype(np.int64)).astype(np.int32)
 
     want = {"gate": exact(base["gate"], x_h), "down": exact(base["down"], x_i)}
+
+    if args.only_mall_resident:
+        print(json.dumps(mall_resident(B, base, dev_base, d_x, want)), flush=True)
+        return 0
 
     # ---- the timed step: streamed, one launch per shape over stacked copies
     launches = []
@@ -882,6 +889,22 @@ def pmc_summary(d):
     out["algorithmic_bytes_per_launch_avg"] = sum(alg) // 2
     out["traffic_over_algorithmic"] = round(out["traffic_bytes_per_launch_avg"] /
                                             out["algorithmic_bytes_per_launch_avg"], 4)
+    # Infinity-Cache-resident protocol (48 copies re-streamed), when its
+    # FETCH_SIZE pass (d/mall) is present.  FETCH_SIZE counts the bytes the L2
+    # fetches from the fabric, whether the Infinity Cache or HBM serves them:
+    # it shows that each launch moves its algorithmic bytes once; the
+    # residency itself shows in the launch time.
+    if glob.glob(os.path.join(d, "mall", "**", "*.db"), recursive=True):
+        mall = per_kernel("mall", "FETCH_SIZE", "gemv_stream_kernel")
+        out["mall_resident"] = {
+            "command": "rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_stream/mall -o m -- python3 "
+                       "-u bench.py --only-mall-resident",
+            "algorithmic_bytes": {"6912x2560x48": gemv_bytes(6912 * 48, 2560),
+                                  "2560x6912x48": gemv_bytes(2560 * 48, 6912)},
+            "per_launch": {f"lds{lds}": {"dispatches": len(v),
+                                          "fetch_bytes": int(sum(v) / len(v) * fs * 1024)}
+                           for lds, v in sorted(mall.items())}}
+        out["commands"].insert(4, out["mall_resident"]["command"])
     with open(PMC_JSON, "w") as fh:
         json.dump(out, fh, indent=1)
     print(json.dumps(out, indent=1))
