@@ -201,21 +201,20 @@ __global__ __launch_bounds__(kWaves * kWave) void gemm_smfmac_direct_kernel(
 // (4p + q, half i).  The B operand follows: lane (token, q) of step i holds
 // columns 64(q >> 1) + 32i + 16(q & 1) + [0, 16) and the same + 128 (the
 // k-th byte of its two 16-byte halves pairs with the k-th compressed value
-// of A lane group q >> 1 and 2 + (q >> 1)).  Staging permutes each token's
-// 16-byte units of a pair so that a lane's 32 bytes of step i are adjacent.
+// of A lane group q >> 1 and 2 + (q >> 1)).  Staging stores each lane
+// group's 32 bytes of step i adjacent in LDS.
 //
-// LDS layout per buffer (bank-conflict-free reads, measured with
-// SQ_LDS_BANK_CONFLICT on gfx950: 64 banks, a 16-lane group per ds_read_b128
-// pass):
+// LDS layout per buffer (bank-conflict free for the operand reads and the
+// staging writes, as measured with SQ_LDS_BANK_CONFLICT on gfx950 for these
+// access patterns):
 //   meta   [8 KCP words][RBM rows]   (transposed; RBM = 8 or 24 mod 32)
 //   values [4 KCP words][RBV rows]   (transposed; RBV = 16 or 48 mod 64)
-//   B      [TB tokens][16 KCP units], unit u of token t at u ^ (t & 15)
+//   B      [4 lane groups q][KCP pairs][TB tokens][4 units]: units 2i, 2i+1
+//          of (q, pair, token t) are lane group q's step-i bytes, unit c
+//          stored at c ^ ((t >> 2) & 3); the q-parts are 4 mod 8 units apart
 // Block: WS x KW waves.  Wave (ws, kw) owns strips ws*S .. ws*S + S - 1 and
 // all T token tiles, and takes the chunk's steps kw, kw + KW, ...; the KW
 // partial sums of a tile meet in LDS after the last chunk.
-__device__ __forceinline__ int pair_slot(int u) {  // 16-byte unit of a pair: (h,a,i,b) -> (a,b,i,h)
-    return (((u >> 2) & 1) << 3) | ((u & 1) << 2) | (((u >> 1) & 1) << 1) | (u >> 3);
-}
 constexpr int low_pow2(int x) { return x & -x; }
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
@@ -230,17 +229,21 @@ struct StagedTile {
     static constexpr int NT = WS * KW * kWave;
     static constexpr int RB = WS * S * 16, TB = T * 16;
     static constexpr int RBM = pitch_mod(RB, 32, 8, 24), RBV = pitch_mod(RB, 64, 16, 48);
-    static constexpr int BU = 16 * KCP;  // 16-byte units per token row and chunk
+    // B: lane group q of a step reads 32 bytes of its token (units c = 2i, 2i+1
+    // of its q-part); the chunk is stored as 4 q-parts of [pair][token][4 units]
+    // (unit c of token t at c ^ ((t >> 2) & 3)), the q-parts QS units apart
+    static constexpr int QS = KCP * TB * 4 + 4;
     // staging maps: a thread owns unit column j < G of rows tr, tr + NT/G, ...
     static constexpr int GM = cmin(low_pow2(2 * KCP), 16);
     static constexpr int RMK = NT / GM, KRM = (RB + RMK - 1) / RMK, KJM = 2 * KCP / GM;
     static constexpr int GV = cmin(low_pow2(KCP), 16);
     static constexpr int RVK = NT / GV, KRV = (RB + RVK - 1) / RVK, KJV = KCP / GV;
-    static constexpr int GB = cmax(16, cmin(low_pow2(BU), NT / 16));
-    static constexpr int TBK = NT / GB, KRB = (TB + TBK - 1) / TBK, KJB = BU / GB;
-    static_assert(TBK % 16 == 0, "a thread's tokens must share the swizzle");
+    // B staging: 16 threads move one token's 256-byte pair; G16 such groups
+    // take items (token t, pair p) = g + G16 r, t fastest
+    static constexpr int G16 = NT / 16, KIB = (TB * KCP + G16 - 1) / G16;
+    static_assert((TB & (TB - 1)) == 0 && (G16 & (G16 - 1)) == 0, "power-of-two staging maps");
     static constexpr int kABytes = (8 * KCP * RBM + 4 * KCP * RBV) * 4;
-    static constexpr int kBufBytes = kABytes + TB * BU * 16;
+    static constexpr int kBufBytes = kABytes + 4 * QS * 16;
     static constexpr int NSW = 2 * KCP / KW;  // steps per wave and chunk
     static_assert((2 * KCP) % KW == 0, "KW must divide a chunk's steps");
     static constexpr int kRedBytes = KW * WS * S * T * kWave * 16;
@@ -285,14 +288,17 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
         btoks * cols, kRawBufferFlags);
     const int jm = tid % P::GM, trm = tid / P::GM;
     const int jv = tid % P::GV, trv = tid / P::GV;
-    const int jb = tid % P::GB, trb = tid / P::GB;
-    const int gm0 = (trm * ms + 4 * jm) * 4, gv0 = (trv * vs + 4 * jv) * 4, gb0 = trb * cols + 16 * jb;
+    const int gm0 = (trm * ms + 4 * jm) * 4, gv0 = (trv * vs + 4 * jv) * 4;
+    // B: thread k of a 16-group loads unit src(k) of the 256-byte pair (the
+    // group's 16 loads cover it) and stores it as (q, c) = (k >> 2, k & 3):
+    // each 8-thread half then writes 8 distinct bank groups (q-parts 4 mod 8
+    // units apart), and the reads of a 16-lane group hit 16.
+    const int gk = tid >> 4, kq = (tid & 15) >> 2, kc = tid & 3;
+    const int src16 = 16 * ((kq >> 1) * 4 + 2 * (kc >> 1) + (kq & 1) + 8 * (kc & 1));
     const int lm0 = (4 * jm * P::RBM + trm) * 4;
     const int lv0 = (8 * KCP * P::RBM + 4 * jv * P::RBV + trv) * 4;
-    const int slotb = (jb & ~15) + pair_slot(jb & 15);
-    const int lb0 = P::kABytes + (trb * P::BU + (slotb ^ (trb & 15))) * 16;
 
-    u32x4v sm[P::KRM][P::KJM], sv[P::KRV][P::KJV], sb[P::KRB][P::KJB];
+    u32x4v sm[P::KRM][P::KJM], sv[P::KRV][P::KJV], sb[P::KIB];
     auto load_chunk = [&](int c) {
         const int cm = c * 32 * KCP, cv = c * 16 * KCP, cb = c * 256 * KCP;
 #pragma unroll
@@ -310,12 +316,11 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
                     sv[kr][kj] = __builtin_amdgcn_raw_buffer_load_b128(
                         rv, gv0 + kr * P::RVK * vs * 4 + kj * P::GV * 16, cv, 0);
 #pragma unroll
-        for (int kr = 0; kr < P::KRB; ++kr)
-#pragma unroll
-            for (int kj = 0; kj < P::KJB; ++kj)
-                if (P::TBK * (kr + 1) <= P::TB || trb + kr * P::TBK < P::TB)
-                    sb[kr][kj] = __builtin_amdgcn_raw_buffer_load_b128(
-                        rx, gb0 + kr * P::TBK * cols + kj * P::GB * 16, cb, 0);
+        for (int r = 0; r < P::KIB; ++r) {
+            const int item = gk + r * P::G16, t = item & (P::TB - 1), pr = item / P::TB;
+            if ((P::TB * KCP) % P::G16 == 0 || item < P::TB * KCP)
+                sb[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, t * cols + pr * 256 + src16, cb, 0);
+        }
     };
     auto store_chunk = [&](int buf) {
         uint8_t* base = smem + buf * P::kBufBytes;
@@ -340,12 +345,13 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
                     for (int e = 0; e < 4; ++e) d[e * P::RBV] = sv[kr][kj][e];
                 }
 #pragma unroll
-        for (int kr = 0; kr < P::KRB; ++kr)
-#pragma unroll
-            for (int kj = 0; kj < P::KJB; ++kj)
-                if (P::TBK * (kr + 1) <= P::TB || trb + kr * P::TBK < P::TB)
-                    *reinterpret_cast<u32x4v*>(base + lb0 + (kr * P::TBK * P::BU + kj * P::GB) * 16) =
-                        sb[kr][kj];
+        for (int r = 0; r < P::KIB; ++r) {
+            const int item = gk + r * P::G16, t = item & (P::TB - 1), pr = item / P::TB;
+            if ((P::TB * KCP) % P::G16 == 0 || item < P::TB * KCP)
+                *reinterpret_cast<u32x4v*>(
+                    base + P::kABytes +
+                    (kq * P::QS + (pr * P::TB + t) * 4 + (kc ^ ((t >> 2) & 3))) * 16) = sb[r];
+        }
     };
 
     v4i acc[S][T];
@@ -379,10 +385,10 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
             }
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                const int tr = t * 16 + li;
-                const int u0 = pp * 16 + 4 * q + 2 * i;
-                blo[j][t] = bb[tr * P::BU + (u0 ^ li)];
-                bhi[j][t] = bb[tr * P::BU + ((u0 + 1) ^ li)];
+                const int tr = t * 16 + li, sw = (tr >> 2) & 3;
+                const u32x4v* row = bb + q * P::QS + (pp * P::TB + tr) * 4;
+                blo[j][t] = row[(2 * i) ^ sw];
+                bhi[j][t] = row[(2 * i + 1) ^ sw];
             }
         }
         __builtin_amdgcn_sched_barrier(0);
