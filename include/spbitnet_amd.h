@@ -161,8 +161,11 @@ int spb_sparse_ternary_gemm_addsub(const uint32_t* meta, const uint32_t* values,
                                    int meta_row_stride, int values_row_stride,
                                    spb_stream_t stream);
 
-/* 1 if spb_sparse_ternary_gemm would use the matrix-core kernel, else 0.
- * Host-only query; no reference counterpart. */
+/* Which kernel spb_sparse_ternary_gemm would run: 2 the staged matrix-core
+ * kernel (cols % 256 == 0, both row strides multiples of 4 words, meta,
+ * values and X 16-byte aligned), 1 the direct matrix-core kernel (cols % 128
+ * == 0, X 16-byte aligned), 0 the general kernel.  Host-only query; no
+ * reference counterpart. */
 int spb_sparse_ternary_gemm_kernel_id(const uint32_t* meta, const uint32_t* values,
                                       const int8_t* X, int rows, int cols, int n,
                                       int meta_row_stride, int values_row_stride);

@@ -608,13 +608,10 @@ using namespace spb;
 extern "C" int spb_sparse_ternary_gemm_kernel_id(const uint32_t* meta, const uint32_t* values,
                                                  const int8_t* X, int rows, int cols, int n,
                                                  int ms, int vs) {
-    (void)meta;
-    (void)values;
     (void)rows;
     (void)n;
-    (void)ms;
-    (void)vs;
-    return (cols > 0 && cols % 128 == 0 && aligned(X, 16)) ? 1 : 0;
+    if (cols <= 0 || cols % 128 != 0 || !aligned(X, 16)) return 0;
+    return staged_ok(meta, values, X, cols, ms, vs) ? 2 : 1;
 }
 
 extern "C" int spb_sparse_ternary_gemm(const uint32_t* meta, const uint32_t* values,
@@ -630,15 +627,8 @@ extern "C" int spb_sparse_ternary_gemm(const uint32_t* meta, const uint32_t* val
     if (!meta || !values || !X || !Y) return invalid("%s: null pointer", fn);
     hipStream_t st = as_stream(stream);
     if (spb_sparse_ternary_gemm_kernel_id(meta, values, X, rows, cols, n, ms, vs)) {
-        // Rows per block (16 * strips), tokens per pass (16 * tiles) and waves
-        // per block, chosen by measurement at 6912x2560: larger tiles as the
-        // batch grows, so each activation tile read from L2 feeds more
-        // matrix-core operations.  Above 64 tokens, the deepest row tile
-        // whose grid still gives ~0.6 blocks per CU: on MI355X, 6912x2560 ran
-        // 21 us at n=256 with 8 strips (216 blocks) against 25 with 4;
-        // 2560x2560-class and 640-row shapes, whose 8-strip grids leave most
-        // CUs idle, ran up to 2x faster with 4 or 2 strips (640x2560, n=256:
-        // 19.3 -> 9.5 us).
+        // The staged kernel when the strides and pointers allow it, else the
+        // direct one (launch_smfmac_for picks the tile for the batch).
         if ((n + 15) / 16 > 65535) return invalid("%s: batch %d too large", fn, n);
         const int rc = launch_smfmac_for(meta, values, X, Y, rows, cols, n, ms, vs, st, nullptr);
         if (rc) return rc;
@@ -652,11 +642,9 @@ extern "C" int spb_sparse_ternary_gemm(const uint32_t* meta, const uint32_t* val
 
 namespace spb {
 
-// Y [n][sum of rows] = (A | B | C) X for up to three stacked projections
-// (the engines' q | k | v and gate | up) in one matrix-core launch.
-// Returns 1 (nothing launched) when the shapes do not allow it: columns or
-// strides differ, the matrix-core conditions fail, or a segment boundary
-// falls inside a block's row tile; the caller then launches them apart.
+// Raises the LDS limit of the staged kernels above 64 KB on the current
+// device (once per device); 0 on success.  Engines call it at create, so no
+// attribute call happens during graph capture.
 int gemm_prepare() {
     return allow_lds(staged_fn<1, 1, 2, 4, 10>()) && allow_lds(staged_fn<2, 2, 2, 4, 2>()) &&
                    allow_lds(staged_fn<2, 4, 2, 4, 2>())
@@ -664,6 +652,11 @@ int gemm_prepare() {
                : 1;
 }
 
+// Y [n][sum of rows] = (A | B | C) X for up to three stacked projections
+// (the engines' q | k | v and gate | up) in one matrix-core launch.
+// Returns 1 (nothing launched) when the shapes do not allow it: columns or
+// strides differ, the matrix-core conditions fail, or a segment boundary
+// falls inside a block's row tile; the caller then launches them apart.
 int gemm_stacked(const spb_sparse_linear* const* segs, int nseg, const int8_t* X, int32_t* Y,
                  int n, hipStream_t st) {
     if (nseg < 1 || nseg > 3 || n <= 0) return 1;

@@ -148,7 +148,9 @@ def sparse_ternary_gemm_gpu(meta, values, X, Y, rows, cols, n, meta_row_stride,
 
 
 def gemm_kernel_id(meta, values, X, rows, cols, n, meta_row_stride, values_row_stride) -> int:
-    """1 if the matrix-core GEMM kernel would run for these arguments, else 0."""
+    """Kernel spb_sparse_ternary_gemm would run for these arguments: 2 the
+    staged matrix-core kernel, 1 the direct matrix-core kernel, 0 the general
+    kernel."""
     return _lib.load().spb_sparse_ternary_gemm_kernel_id(
         meta.data_ptr(), values.data_ptr(), X.data_ptr(), rows, cols, n, meta_row_stride,
         values_row_stride)

@@ -103,6 +103,19 @@ def test_gemv_kernel_selection(lib):
     assert kid(a16, a16, 4, 65536, 2048, 1024) == 0  # beyond the bit-plane column limit
 
 
+def test_gemm_kernel_selection(lib):
+    kid = lib.spb_sparse_ternary_gemm_kernel_id
+    a16, a4 = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x10004)
+    assert kid(a16, a16, a16, 6912, 2560, 64, 80, 40) == 2       # staged
+    assert kid(a16, a16, a16, 2560, 6912, 16, 216, 108) == 2
+    assert kid(a16, a16, a16, 64, 384, 16, 12, 6) == 1           # cols % 256 != 0: direct
+    assert kid(a16, a16, a16, 64, 2560, 16, 81, 40) == 1         # meta stride % 4 != 0
+    assert kid(a16, a16, a16, 64, 2560, 16, 80, 42) == 1         # values stride % 4 != 0
+    assert kid(a4, a16, a16, 64, 2560, 16, 80, 40) == 1          # meta base not 16-byte aligned
+    assert kid(a16, a16, a4, 64, 2560, 16, 80, 40) == 0          # X not 16-byte aligned: general
+    assert kid(a16, a16, a16, 64, 100, 16, 4, 2) == 0            # cols % 128 != 0: general
+
+
 def test_cpp_mirror_header_compiles_links_and_runs_noops(tmp_path):
     """include/spbitnet/sparse_ternary_kernels.h (the reference's C++ names
     over the C ABI) builds into a host program (ROCm clang, as hipcc uses for host code) and

@@ -51,7 +51,7 @@ def test_gemm_config2(gpu, n):
     X = activations(n, cols, 1000 + n)
     X_dev = dev(X, gpu)
     assert K.gemm_kernel_id(dev_u32(L.meta, gpu), dev_u32(L.values, gpu), X_dev, rows, cols, n,
-                            L.meta_stride, L.values_stride) == 1
+                            L.meta_stride, L.values_stride) == 2
     assert (run(L, X, gpu) == expected(L, X)).all()
 
 
@@ -106,8 +106,12 @@ def test_gemm_padded_strides(gpu, pad_m, pad_v, n):
     meta[:, :L.meta_stride] = L.meta
     values[:, :L.values_stride] = L.values
     X = activations(n, cols, 500 + pad_m + pad_v)
+    m_dev, v_dev, X_dev = dev_u32(meta, gpu), dev_u32(values, gpu), dev(X, gpu)
+    staged = meta.shape[1] % 4 == 0 and values.shape[1] % 4 == 0
+    assert K.gemm_kernel_id(m_dev, v_dev, X_dev, rows, cols, n, meta.shape[1],
+                            values.shape[1]) == (2 if staged else 1)
     Y = torch.full((n, rows), -7, dtype=torch.int32, device=gpu)
-    K.sparse_ternary_gemm_gpu(dev_u32(meta, gpu), dev_u32(values, gpu), dev(X, gpu), Y, rows,
-                              cols, n, meta.shape[1], values.shape[1])
+    K.sparse_ternary_gemm_gpu(m_dev, v_dev, X_dev, Y, rows, cols, n, meta.shape[1],
+                              values.shape[1])
     torch.cuda.synchronize()
     assert (Y.cpu().numpy() == expected(L, X)).all()
