@@ -1138,15 +1138,13 @@ struct SinkPairs<QkvRopeSink> {
 // holds k and v at pos (both written by the qkv projection's epilogue), so
 // every load is issued at kernel start; rows past pos are loaded too (the
 // cache is allocated to max_seq) and masked.
-//   * scores: thread t takes quarter qq = t % 4 of the head dim of q head
-//     g = (t / 4) / (64 / G) and the G positions ((t / 4) % (64 / G)) * G + i,
-//     so it reads one quarter of one q head from LDS (LDS return bandwidth is
-//     what bounds a full head per thread) and G quarter K rows from global;
-//     the 4 quarter sums of a (head, position) meet in the 4 lanes of a quad
-//     (two DPP adds).
-//   * V rows of the split stay bf16 in LDS; a PV thread owns dims (d, d+1)
-//     of one head and reads both with one 32-bit LDS load, and 4 positions'
-//     weights with one 16-byte load.
+//   * scores: thread t takes quarter qq = t % 4 of K row t / 4 (one global
+//     read of each K element per block, unpacked once) and the quarter of
+//     every q head of the group from LDS; the 4 quarter sums of a (head,
+//     position) meet in the 4 lanes of a quad (two DPP adds).
+//   * V rows of the split stay bf16 in LDS; a PV thread owns element d of
+//     NH heads, unpacks each V element once for them, and reads 4 positions'
+//     weights of a head with one 16-byte load.
 //   score_j = ((a0 + a1) + (a2 + a3)) * scale, a_k = fma over the d of
 //     quarter k (ascending) of q[d] * k_j[d]
 //   per head: m = max_j score_j, e_j = exp(score_j - m),
@@ -1155,49 +1153,54 @@ struct SinkPairs<QkvRopeSink> {
 // Reference: attention_scores, softmax, attention_output
 // (inference_kernels.cu:241-371), GQA kv = h * nkv / nh.
 
-// The per-split work of one query (the decode kernel and the prefill kernel
+// The per-split work of one query (the decode kernels and the prefill kernel
 // share it): once its q (qs, float) and the split's V rows (vs, bf16) are in
-// LDS behind a barrier and the thread holds its quarter K rows (kq), the
-// scores, the split's softmax and the weighted V sum, stored as the split's
-// partials of heads kvh * G .. kvh * G + G - 1.  jn: positions of the split
-// holding positions 0..pos.  A caller that writes qs again barriers first.
+// LDS behind a barrier and the thread holds its quarter of K row p = tid / 4
+// (kq; quarter tid % 4), the scores, the split's softmax and the weighted V
+// sum, stored as the split's partials of heads kvh * G .. kvh * G + G - 1.
+// Scores: the thread unpacks its K quarter once and runs the quarter's fma
+// chain for every head of the group; the four quarters of a position are the
+// four lanes of a quad and combine through DPP.  V sums: thread t takes
+// element t % HD of NH heads (NH = G * HD / 256, at least 1), unpacking each
+// V element once for them.  jn: positions of the split holding positions
+// 0..pos.  A caller that writes qs again barriers first.
 template <int HD, int G>
-__device__ __forceinline__ void attention_split(const uint4 (&kq)[G][HD / 32], float (&qs)[G][HD],
+__device__ __forceinline__ void attention_split(const uint4 (&kq)[HD / 32], float (&qs)[G][HD],
                                                 uint32_t (&vs)[kAttnSplit][HD / 2 + 1],
                                                 float (&sc)[G][kAttnSplit], float (&hmax)[G],
                                                 float (&hsum)[G], int jn, float scale, int s,
                                                 int kvh, int S, float* __restrict__ pm,
                                                 float* __restrict__ pl, float* __restrict__ pacc) {
-    constexpr int kQU = HD / 32;
-    constexpr int kPG = kAttnSplit / G;
+    constexpr int kQU = HD / 32;  // 16-byte units per quarter row
+    constexpr int kQD = HD / 4;   // elements per quarter row
+    constexpr int kVRow = HD / 2 + 1;
+    static_assert(kAttnThreads == 4 * kAttnSplit, "4 quarters x 64 positions");
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int qq = tid & 3, slot = tid >> 2;
-    const int sg = slot / kPG, pb = (slot - sg * kPG) * G;
+    const int qq = tid & 3, p = tid >> 2;
     // scores (every lane active: the quads combine through DPP)
     {
-        float qv[HD / 4];
+        float kf[kQD];
 #pragma unroll
-        for (int u = 0; u < HD / 16; ++u) {
-            const float4 t = *reinterpret_cast<const float4*>(&qs[sg][qq * (HD / 4) + 4 * u]);
-            qv[4 * u] = t.x;
-            qv[4 * u + 1] = t.y;
-            qv[4 * u + 2] = t.z;
-            qv[4 * u + 3] = t.w;
+        for (int u = 0; u < kQU; ++u) {
+            float f[8];
+            unpack_bf16x8(kq[u], f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kf[8 * u + e] = f[e];
         }
 #pragma unroll
-        for (int i = 0; i < G; ++i) {
+        for (int g = 0; g < G; ++g) {
             float a = 0.0f;
 #pragma unroll
-            for (int u = 0; u < kQU; ++u) {
-                float f[8];
-                unpack_bf16x8(kq[i][u], f);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) a = __builtin_fmaf(qv[8 * u + e], f[e], a);
+            for (int u = 0; u < kQD / 4; ++u) {
+                const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][qq * kQD + 4 * u]);
+                a = __builtin_fmaf(q4.x, kf[4 * u], a);
+                a = __builtin_fmaf(q4.y, kf[4 * u + 1], a);
+                a = __builtin_fmaf(q4.z, kf[4 * u + 2], a);
+                a = __builtin_fmaf(q4.w, kf[4 * u + 3], a);
             }
             a += dpp_f<0xB1>(a);  // quad_perm [1,0,3,2]: a0 + a1, a2 + a3
             a += dpp_f<0x4E>(a);  // quad_perm [2,3,0,1]: (a0 + a1) + (a2 + a3)
-            const int p = pb + i;
-            if (qq == 0 && p < jn) sc[sg][p] = a * scale;
+            if (qq == 0 && p < jn) sc[g][p] = a * scale;
         }
     }
     __syncthreads();
@@ -1213,29 +1216,53 @@ __device__ __forceinline__ void attention_split(const uint4 (&kq)[G][HD / 32], f
         }
     }
     __syncthreads();
-    for (int o = tid; o < G * (HD / 2); o += kAttnThreads) {
-        const int g = o / (HD / 2), dp = o - g * (HD / 2);
-        float a0 = 0.0f, a1 = 0.0f;
-        auto step = [&](int jj, float e) {
-            const uint32_t w = vs[jj][dp];
-            a0 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w & 0xFFFFu)), a0);
-            a1 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w >> 16)), a1);
+    constexpr int kOut = G * HD;
+    constexpr int NH = kOut > kAttnThreads ? kOut / kAttnThreads : 1;  // heads per thread
+    if (tid < kOut / NH) {
+        const int d = tid % HD, g0 = (tid / HD) * NH;
+        const uint16_t* vcol = reinterpret_cast<const uint16_t*>(&vs[0][0]) + d;
+        float a[NH];
+#pragma unroll
+        for (int h = 0; h < NH; ++h) a[h] = 0.0f;
+        auto step = [&](int jj, const float (&e)[NH]) {
+            const float v = __builtin_bit_cast(
+                float, static_cast<uint32_t>(vcol[jj * 2 * kVRow]) << 16);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) a[h] = __builtin_fmaf(e[h], v, a[h]);
         };
         const int n4 = jn >> 2;
         for (int q = 0; q < n4; ++q) {
-            const float4 e = *reinterpret_cast<const float4*>(&sc[g][4 * q]);
-            step(4 * q, e.x);
-            step(4 * q + 1, e.y);
-            step(4 * q + 2, e.z);
-            step(4 * q + 3, e.w);
+            float4 e4[NH];
+#pragma unroll
+            for (int h = 0; h < NH; ++h) e4[h] = *reinterpret_cast<const float4*>(&sc[g0 + h][4 * q]);
+            float e[NH];
+#pragma unroll
+            for (int h = 0; h < NH; ++h) e[h] = e4[h].x;
+            step(4 * q, e);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) e[h] = e4[h].y;
+            step(4 * q + 1, e);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) e[h] = e4[h].z;
+            step(4 * q + 2, e);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) e[h] = e4[h].w;
+            step(4 * q + 3, e);
         }
-        for (int jj = 4 * n4; jj < jn; ++jj) step(jj, sc[g][jj]);
-        const int h = kvh * G + g;
-        float* out = pacc + (static_cast<long>(h) * S + s) * HD + 2 * dp;
-        *reinterpret_cast<float2*>(out) = make_float2(a0, a1);
-        if (dp == 0) {
-            pm[h * S + s] = hmax[g];
-            pl[h * S + s] = hsum[g];
+        for (int jj = 4 * n4; jj < jn; ++jj) {
+            float e[NH];
+#pragma unroll
+            for (int h = 0; h < NH; ++h) e[h] = sc[g0 + h][jj];
+            step(jj, e);
+        }
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const int hh = kvh * G + g0 + h;
+            pacc[(static_cast<long>(hh) * S + s) * HD + d] = a[h];
+            if (d == 0) {
+                pm[hh * S + s] = hmax[g0 + h];
+                pl[hh * S + s] = hsum[g0 + h];
+            }
         }
     }
 }
@@ -1246,7 +1273,9 @@ __device__ __forceinline__ void attention_split(const uint4 (&kq)[G][HD / 32], f
 // maxima, w_s = exp(m_s - M) (computed once per split here, by one thread,
 // and shared through LDS), then l and each element's sum accumulated split
 // by split; thread d writes bf16r(sum_d / l).  The element's partials of the
-// first kCombineBatch splits are loaded before anything else.
+// first kCombineBatch splits and the split maxima and sums are loaded
+// together, right after the position (loads of splits past it, whose
+// partials are old and cold, would hold up the live ones).
 constexpr int kCombineBatch = 64;
 // Token-step graphs whose attention reaches at most this many splits keep the
 // combine in the o projection's prologue; longer ones launch attn_combine_kernel.
@@ -1270,15 +1299,21 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
     float pv[kCombineBatch];
 #pragma unroll
     for (int k = 0; k < kCombineBatch; ++k) pv[k] = ph[static_cast<long>(k < ns ? k : ns - 1) * HD];
-    float M = -INFINITY;
-    for (int s = d; s < ns; s += HD) M = __builtin_fmaxf(M, mh[s]);
+    const float m0 = d < ns ? mh[d] : -INFINITY;
+    const float l0 = d < ns ? lh[d] : 0.0f;
+    float M = m0;
+    for (int s = d + HD; s < ns; s += HD) M = __builtin_fmaxf(M, mh[s]);
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) M = __builtin_fmaxf(M, __shfl_xor(M, off, kWave));
     if (lane == 0) red[wave] = M;
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < HD / kWave; ++w) M = __builtin_fmaxf(M, red[w]);
-    for (int s = d; s < ns; s += HD) {
+    if (d < ns) {
+        wl[d] = exp_neg(m0 - M);
+        wl[S + d] = l0;
+    }
+    for (int s = d + HD; s < ns; s += HD) {
         wl[s] = exp_neg(mh[s] - M);
         wl[S + s] = lh[s];
     }
@@ -1310,9 +1345,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     float scale) {
     constexpr int kU = HD / 8;       // 16-byte units per row
     constexpr int kQU = kU / 4;      // units per quarter row
-    constexpr int kPG = kAttnSplit / G;  // position groups per head
     constexpr int kVRow = HD / 2 + 1;  // 32-bit words per bf16 V row in LDS (+1: no bank conflicts)
-    static_assert(kAttnThreads == 4 * kAttnSplit && kAttnSplit % G == 0, "4 quarters x 64 slots");
     __shared__ __align__(16) float qs[G][HD];
     __shared__ uint32_t vs[kAttnSplit][kVRow];
     __shared__ __align__(16) float sc[G][kAttnSplit];
@@ -1322,17 +1355,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     const int tid = threadIdx.x;
     const long cache0 = static_cast<long>(kvh) * max_seq * HD;
     const int jmax = max_seq - 1;
-    // the thread's quarter K rows (positions clamped to the cache)
-    const int qq = tid & 3, slot = tid >> 2;
-    const int sg = slot / kPG, pb = (slot - sg * kPG) * G;
-    uint4 kq[G][kQU];
+    // the thread's quarter of K row j0 + tid / 4 (clamped to the cache)
+    uint4 kq[kQU];
+    {
+        const int j = j0 + (tid >> 2) <= jmax ? j0 + (tid >> 2) : jmax;
+        const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) +
+                          (tid & 3) * kQU;
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-        const int j = j0 + pb + i <= jmax ? j0 + pb + i : jmax;
-        const uint4* kr =
-            reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) + qq * kQU;
-#pragma unroll
-        for (int u = 0; u < kQU; ++u) kq[i][u] = kr[u];
+        for (int u = 0; u < kQU; ++u) kq[u] = kr[u];
     }
     // V rows of the split: kVPer 16-byte units per thread, all loads issued
     // before the first LDS store
@@ -1386,7 +1416,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
     int qkv_stride) {
     constexpr int kU = HD / 8;
     constexpr int kQU = kU / 4;
-    constexpr int kPG = kAttnSplit / G;
     constexpr int kVRow = HD / 2 + 1;
     __shared__ __align__(16) float qs[G][HD];
     __shared__ uint32_t vs[kAttnSplit][kVRow];
@@ -1400,16 +1429,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
     const int tid = threadIdx.x;
     const long cache0 = static_cast<long>(kvh) * max_seq * HD;
     const int jmax = max_seq - 1;
-    const int qq = tid & 3, slot = tid >> 2;
-    const int sg = slot / kPG, pb = (slot - sg * kPG) * G;
-    uint4 kq[G][kQU];
+    // the thread's quarter of K row j0 + tid / 4 (clamped to the cache)
+    uint4 kq[kQU];
+    {
+        const int j = j0 + (tid >> 2) <= jmax ? j0 + (tid >> 2) : jmax;
+        const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) +
+                          (tid & 3) * kQU;
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-        const int j = j0 + pb + i <= jmax ? j0 + pb + i : jmax;
-        const uint4* kr =
-            reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) + qq * kQU;
-#pragma unroll
-        for (int u = 0; u < kQU; ++u) kq[i][u] = kr[u];
+        for (int u = 0; u < kQU; ++u) kq[u] = kr[u];
     }
     constexpr int kVPer = kAttnSplit * kU / kAttnThreads;
     uint4 vraw[kVPer];
@@ -1471,7 +1498,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_batch_kernel(
     float scale, int qkv_stride, long kv_stride) {
     constexpr int kU = HD / 8;
     constexpr int kQU = kU / 4;
-    constexpr int kPG = kAttnSplit / G;
     constexpr int kVRow = HD / 2 + 1;
     __shared__ __align__(16) float qs[G][HD];
     __shared__ uint32_t vs[kAttnSplit][kVRow];
@@ -1492,16 +1518,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_batch_kernel(
     pacc += b * hs * HD;
     const long cache0 = static_cast<long>(kvh) * max_seq * HD;
     const int jmax = max_seq - 1;
-    const int qq = tid & 3, slot = tid >> 2;
-    const int sg = slot / kPG, pb = (slot - sg * kPG) * G;
-    uint4 kq[G][kQU];
+    // the thread's quarter of K row j0 + tid / 4 (clamped to the cache)
+    uint4 kq[kQU];
+    {
+        const int j = j0 + (tid >> 2) <= jmax ? j0 + (tid >> 2) : jmax;
+        const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) +
+                          (tid & 3) * kQU;
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-        const int j = j0 + pb + i <= jmax ? j0 + pb + i : jmax;
-        const uint4* kr =
-            reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) + qq * kQU;
-#pragma unroll
-        for (int u = 0; u < kQU; ++u) kq[i][u] = kr[u];
+        for (int u = 0; u < kQU; ++u) kq[u] = kr[u];
     }
     constexpr int kVPer = kAttnSplit * kU / kAttnThreads;
     uint4 vraw[kVPer];
@@ -1858,76 +1882,100 @@ LmKernel lm_head_for(int H) {
 // operations of lm_head_kernel: the final RMSNorm in the unit order of
 // kLmBlock threads, then, for each of 64 "virtual lanes" v, the fma chain
 // over the row's 8-element chunks v, v + 64, ... (element order), then the
-// balanced pairwise tree over the 64 virtual lanes.  Here eight real lanes
-// share a row and lane j of the eight carries virtual lanes 8j .. 8j + 7:
-// the tree's first three levels are adds inside the lane, the last three
-// DPP steps across the eight lanes (pair, quad, half-row mirror), so each
-// sequence's logits equal a bs=1 step's bit for bit.  A lane's eight chunks
-// of one 64-chunk step are contiguous (128 bytes of the row), and every
-// lane of the same j reads the same x chunks from LDS (a broadcast); the
-// normalised vectors sit in LDS as float with 16 bytes of padding per 8
-// chunks, so the eight j of a read fall in different banks.  A wave handles
-// 8 rows at a time; the row's weights are unpacked once and used for every
-// sequence.  Per-sequence argmax (lowest index among maxima) and
-// decode-state update by the last block to finish (ticket of the group's
-// first sequence), as in the bs=1 kernel; done sequences are not updated.
-constexpr int kLmGroup = 8;          // sequences per batched LM-head launch (at most)
-constexpr int kLmBatchMaxRows = 512;  // rows per block (grid >= vocab / 512)
+// balanced pairwise tree over the 64 virtual lanes.  Here a row belongs to
+// 32 real lanes: lane j carries virtual lanes j (A) and j + 32 (B).  The
+// tree's first four levels are DPP steps inside each 16-lane row, applied to
+// A and B alike (A's rows then hold lm_head_kernel's row sums r0, r1, B's r2,
+// r3), the fifth is a lane swap across the two rows (r0 + r1, r2 + r3), the
+// last the in-lane A + B, so each sequence's logits equal a bs=1 step's bit
+// for bit.  Each half of a wave takes 4 rows at once: every x chunk read
+// from LDS feeds 4 rows x 8 fma (the matrix multiply-adds, not the LDS, bound
+// the kernel), the weight loads of a 64-chunk step are 512 contiguous bytes
+// per row and instruction, and the next step's loads are in flight while one
+// step is reduced.  The normalised vectors sit in LDS as float with 16 bytes
+// of padding per 8 chunks, so the 16 lanes of a read fall in distinct banks.
+// Per-sequence argmax (lowest index among maxima) and decode-state update by
+// the last block to finish (ticket of the group's first sequence), as in the
+// bs=1 kernel; done sequences are not updated.
+constexpr int kLmGroup = 8;          // sequences per batched LM-head block (at most)
+constexpr int kLmBatchMaxRows = 512;  // rows per block (blocks per group >= vocab / 512)
+constexpr int kLmRows = 4;            // rows per half wave at once
+constexpr int kLmBatchBlock = 512;    // threads per batched LM-head block
+// The batched LM head holds a group's normalised vectors in LDS, so it
+// takes hidden sizes up to kLmBatchMaxH (NC <= 8 chunks per lane).
+constexpr int kLmBatchMaxH = 4096;
 
 // float index of chunk c's first element in the padded LDS vector
 __device__ __forceinline__ int lm_xpad(int c) { return 8 * c + 4 * (c >> 3); }
 
+// Batched decode: the final RMSNorm of sequence blockIdx.x with
+// lm_head_kernel's prologue (same threads, same order), written padded for
+// lm_head_batch_kernel: xn[b][lm_xpad(c) ..] = chunk c of the normalised
+// vector (bf16-rounded floats), zeros for chunks c >= H / 8 up to nc64.
+template <bool kOne>
+__global__ __launch_bounds__(kLmBlock) void final_norm_batch_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ wn, float eps,
+    float* __restrict__ xn, int H, int nc64, int xstride) {
+    __shared__ __align__(16) float xs[kLmBatchMaxH];
+    __shared__ float red[kLmBlock / kWave];
+    const int tid = threadIdx.x, nch = H >> 3;
+    const uint16_t* xg = x + static_cast<long>(blockIdx.x) * H;
+    HeldWeights<kLmBlock> hw;
+    HeldUnits<kLmBlock> hx;
+    hx.load(xg, nch, tid);
+    hw.load(wn, nch, tid);
+    const float ss = load_bf16_sumsq<kLmBlock, kOne>(xg, xs, nch, tid, nullptr, hx);
+    const float inv = inv_rms(block_sum<kLmBlock>(ss, red), H, eps);
+    hw.template apply<kOne>(xs, wn, inv, nch, tid);
+    __syncthreads();
+    float* dst = xn + static_cast<long>(blockIdx.x) * xstride;
+    for (int c = tid; c < nc64; c += kLmBlock) {
+        float f[8];
+        if (c < nch) {
+            load_f8(xs + 8 * c, f);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = 0.0f;
+        }
+        store_f8(dst + lm_xpad(c), f);
+    }
+}
+
+// One launch covers every group of kLmGroup sequences: nblk row blocks per
+// group, block x -> (row block, group) such that the groups' blocks of one
+// row block are dispatched together to the same XCD (x % 8), so the table's
+// rows come from HBM once and from that XCD's L2 for the other groups.
 template <int NC, bool kFull>
-__global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
-    const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
-    const float* __restrict__ wn, float eps, float* __restrict__ logits,
+__global__ __launch_bounds__(kLmBatchBlock) void lm_head_batch_kernel(
+    const uint16_t* __restrict__ W, const float* __restrict__ xn, float* __restrict__ logits,
     float* __restrict__ part_v, int* __restrict__ part_i, EngineState* __restrict__ st,
     int* __restrict__ tokens, long tok_stride, int V, int H, const float2* __restrict__ rope,
-    float2* __restrict__ cur_rope, int half_hd, int max_seq, int rbase, int rrem, int g0,
-    int gn) {
-    constexpr int kWaves = kLmBlock / kWave;
+    float2* __restrict__ cur_rope, int half_hd, int max_seq, int rbase, int rrem, int nblk,
+    int B) {
+    constexpr int kWaves = kLmBatchBlock / kWave;
     extern __shared__ __align__(16) float lds[];
     const int nch = H >> 3;
     const int xstride = lm_xpad(NC * kWave);          // floats per padded vector
     float* xs = lds;                                   // [gn][xstride]
     float* lg = lds + static_cast<long>(kLmGroup) * xstride;  // [gn][kLmBatchMaxRows]
-    __shared__ float red[kLmGroup][kWaves];
     __shared__ float wv[kWaves];
     __shared__ int wi[kWaves];
     __shared__ int last;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int j = lane & 7, rg = lane >> 3;  // virtual lanes 8j .. 8j+7 of row group rg
-    const int blk = blockIdx.x;
+    const int j = lane & 31, hg = lane >> 5;  // virtual lanes j, j + 32 of the half's rows
+    const int ng = (B + kLmGroup - 1) / kLmGroup;
+    const int bq = blockIdx.x >> 3, grp = bq % ng;
+    const int blk = (bq / ng) * 8 + (blockIdx.x & 7);  // nblk % 8 == 0
+    const int g0 = grp * kLmGroup, gn = B - g0 < kLmGroup ? B - g0 : kLmGroup;
     const long b0 = static_cast<long>(blk) * rbase + (blk < rrem ? blk : rrem);
     const long b1 = b0 + rbase + (blk < rrem ? 1 : 0);
     const long noct = (b1 - b0 + 7) >> 3;  // row octets of the block
-    // final RMSNorm of each sequence of the group (lm_head_kernel's order),
-    // stored with the chunk padding
-    constexpr bool kOne = NC * kWave <= kUnits * kLmBlock;
-    float* tmp = lg;  // the norm's unpadded vector (the staging area is free until the rows)
-    for (int g = 0; g < gn; ++g) {
-        const uint16_t* xg = x + static_cast<long>(g0 + g) * H;
-        HeldWeights<kLmBlock> hw;
-        HeldUnits<kLmBlock> hx;
-        hx.load(xg, H >> 3, tid);
-        hw.load(wn, H >> 3, tid);
-        const float ss = load_bf16_sumsq<kLmBlock, kOne>(xg, tmp, H >> 3, tid, nullptr, hx);
-        const float inv = inv_rms(block_sum<kLmBlock>(ss, red[g]), H, eps);
-        hw.template apply<kOne>(tmp, wn, inv, H >> 3, tid);
-        __syncthreads();
-        float* dst = xs + static_cast<long>(g) * xstride;
-        for (int c = tid; c < NC * kWave; c += kLmBlock) {
-            float f[8];
-            if (c < nch) {
-                load_f8(tmp + 8 * c, f);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) f[e] = 0.0f;
-            }
-            store_f8(dst + lm_xpad(c), f);
-        }
-        __syncthreads();  // tmp is rewritten by the next sequence
+    {
+        const uint4* src = reinterpret_cast<const uint4*>(xn + static_cast<long>(g0) * xstride);
+        uint4* dst = reinterpret_cast<uint4*>(xs);
+        for (int i = tid; i < gn * (xstride >> 2); i += kLmBatchBlock) dst[i] = src[i];
     }
+    __syncthreads();
 
     float best[kLmGroup];
     int best_i[kLmGroup];
@@ -1936,47 +1984,54 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
         best[g] = -INFINITY;
         best_i[g] = 0x7FFFFFFF;
     }
-    auto load_step = [&](long row, int k, uint4 (&w)[8]) {
-        const uint4* wr = reinterpret_cast<const uint4*>(W + (row < V ? row : V - 1) * H);
+    // step k of the 4 rows from rb: chunks k * 64 + j (A) and k * 64 + 32 + j (B)
+    auto load_step = [&](long rb, int k, uint4 (&w)[kLmRows][2]) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = k * kWave + 8 * j + i;
-            if (kFull)
-                w[i] = nt_load(wr + c);
-            else
-                w[i] = c < nch ? nt_load(wr + c) : make_uint4(0, 0, 0, 0);
+        for (int r = 0; r < kLmRows; ++r) {
+            const long row = rb + r;
+            const uint4* wr = reinterpret_cast<const uint4*>(W + (row < V ? row : V - 1) * H);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int c = k * kWave + 32 * i + j;
+                if (kFull)
+                    w[r][i] = nt_load(wr + c);
+                else
+                    w[r][i] = c < nch ? nt_load(wr + c) : make_uint4(0, 0, 0, 0);
+            }
         }
     };
     for (long o = wave; o < noct; o += kWaves) {
-        const long row = b0 + 8 * o + rg;
-        float acc[kLmGroup][8];
+        const long rb = b0 + 8 * o + kLmRows * hg;
+        float acc[kLmGroup][kLmRows][2];
 #pragma unroll
         for (int g = 0; g < kLmGroup; ++g)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
-        uint4 wa[8], wb[8];
-        load_step(row, 0, wa);
+            for (int r = 0; r < kLmRows; ++r) acc[g][r][0] = acc[g][r][1] = 0.0f;
+        uint4 wa[kLmRows][2], wb[kLmRows][2];
+        load_step(rb, 0, wa);
 #pragma unroll
         for (int k = 0; k < NC; ++k) {
-            uint4 (&cur)[8] = (k & 1) ? wb : wa;
-            uint4 (&nxt)[8] = (k & 1) ? wa : wb;
-            if (k + 1 < NC) load_step(row, k + 1, nxt);
+            uint4 (&cur)[kLmRows][2] = (k & 1) ? wb : wa;
+            uint4 (&nxt)[kLmRows][2] = (k & 1) ? wa : wb;
+            if (k + 1 < NC) load_step(rb, k + 1, nxt);
             __builtin_amdgcn_sched_barrier(0);
-            float wf[8][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) unpack_bf16x8(cur[i], wf[i]);
+            for (int i = 0; i < 2; ++i) {
+                const int c = k * kWave + 32 * i + j;
+                if (kFull || c < nch) {  // lm_head_kernel's chunks only
+                    float wf[kLmRows][8];
 #pragma unroll
-            for (int g = 0; g < kLmGroup; ++g) {
-                if (g < gn) {
-                    const float* xg = xs + static_cast<long>(g) * xstride;
+                    for (int r = 0; r < kLmRows; ++r) unpack_bf16x8(cur[r][i], wf[r]);
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        if (kFull || k * kWave + 8 * j + i < nch) {  // lm_head_kernel's chunks only
+                    for (int g = 0; g < kLmGroup; ++g) {
+                        if (g < gn) {
                             float xv[8];
-                            load_f8(xg + lm_xpad(k * kWave + 8 * j + i), xv);
+                            load_f8(xs + static_cast<long>(g) * xstride + lm_xpad(c), xv);
 #pragma unroll
-                            for (int e = 0; e < 8; ++e)
-                                acc[g][i] = __builtin_fmaf(wf[i][e], xv[e], acc[g][i]);
+                            for (int r = 0; r < kLmRows; ++r)
+#pragma unroll
+                                for (int e = 0; e < 8; ++e)
+                                    acc[g][r][i] = __builtin_fmaf(wf[r][e], xv[e], acc[g][r][i]);
                         }
                     }
                 }
@@ -1985,17 +2040,27 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
 #pragma unroll
         for (int g = 0; g < kLmGroup; ++g) {
             if (g < gn) {
-                // the 64-virtual-lane tree: three levels in the lane, three across
-                float t = ((acc[g][0] + acc[g][1]) + (acc[g][2] + acc[g][3])) +
-                          ((acc[g][4] + acc[g][5]) + (acc[g][6] + acc[g][7]));
-                t += dpp_f<0xB1>(t);   // quad_perm [1,0,3,2]: 16 virtual lanes
-                t += dpp_f<0x4E>(t);   // quad_perm [2,3,0,1]: 32
-                t += dpp_f<0x141>(t);  // row_half_mirror: 64
-                if (j == 0 && row < b1) {
-                    lg[g * kLmBatchMaxRows + (row - b0)] = t;
-                    if (t > best[g]) {  // a lane's rows ascend: strict > keeps the first maximum
-                        best[g] = t;
-                        best_i[g] = static_cast<int>(row);
+#pragma unroll
+                for (int r = 0; r < kLmRows; ++r) {
+                    float a = acc[g][r][0], b = acc[g][r][1];
+                    a += dpp_f<0xB1>(a);   // quad_perm [1,0,3,2]
+                    b += dpp_f<0xB1>(b);
+                    a += dpp_f<0x4E>(a);   // quad_perm [2,3,0,1]
+                    b += dpp_f<0x4E>(b);
+                    a += dpp_f<0x141>(a);  // row_half_mirror
+                    b += dpp_f<0x141>(b);
+                    a += dpp_f<0x140>(a);  // row_mirror: r0 | r1 (A), r2 | r3 (B)
+                    b += dpp_f<0x140>(b);
+                    a += __shfl_xor(a, 16, kWave);  // r0 + r1
+                    b += __shfl_xor(b, 16, kWave);  // r2 + r3
+                    const float t = a + b;
+                    const long row = rb + r;
+                    if (j == 0 && row < b1) {
+                        lg[g * kLmBatchMaxRows + (row - b0)] = t;
+                        if (t > best[g]) {  // a lane's rows ascend: strict > keeps the first maximum
+                            best[g] = t;
+                            best_i[g] = static_cast<int>(row);
+                        }
                     }
                 }
             }
@@ -2003,16 +2068,16 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
     }
     __syncthreads();
     for (int g = 0; g < gn; ++g)
-        for (long jj = tid; jj < b1 - b0; jj += kLmBlock)
+        for (long jj = tid; jj < b1 - b0; jj += kLmBatchBlock)
             logits[static_cast<long>(g0 + g) * V + b0 + jj] = lg[g * kLmBatchMaxRows + jj];
-    // per-sequence block maxima: the eight row groups of each wave, then the waves
+    // per-sequence block maxima: the two halves of each wave, then the waves
 #pragma unroll
     for (int g = 0; g < kLmGroup; ++g) {
         if (g < gn) {
             float bv = best[g];
             int bi = best_i[g];
 #pragma unroll
-            for (int off = 8; off < kWave; off <<= 1) {
+            for (int off = 32; off < kWave; off <<= 1) {  // lanes 0 and 32 hold the rows
                 const float ov = __shfl_xor(bv, off, kWave);
                 const int oi = __shfl_xor(bi, off, kWave);
                 if (ov > bv || (ov == bv && oi < bi)) {
@@ -2033,27 +2098,27 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
                         b = wv[w];
                         bb = wi[w];
                     }
-                part_v[static_cast<long>(g0 + g) * gridDim.x + blockIdx.x] = b;
-                part_i[static_cast<long>(g0 + g) * gridDim.x + blockIdx.x] = bb;
+                part_v[static_cast<long>(g0 + g) * nblk + blk] = b;
+                part_i[static_cast<long>(g0 + g) * nblk + blk] = bb;
             }
             __syncthreads();
         }
     }
     if (tid == 0) {
         __threadfence();
-        const unsigned t = atomicAdd(&st[g0].ticket, 1u);
-        last = t == gridDim.x - 1;
+        const unsigned tk = atomicAdd(&st[g0].ticket, 1u);
+        last = tk == static_cast<unsigned>(nblk) - 1;
     }
     __syncthreads();
     if (!last) return;
     __threadfence();
     for (int g = 0; g < gn; ++g) {
         EngineState* sg = st + g0 + g;
-        const float* pv = part_v + static_cast<long>(g0 + g) * gridDim.x;
-        const int* pi = part_i + static_cast<long>(g0 + g) * gridDim.x;
+        const float* pv = part_v + static_cast<long>(g0 + g) * nblk;
+        const int* pi = part_i + static_cast<long>(g0 + g) * nblk;
         float bv = -INFINITY;
         int bi = 0x7FFFFFFF;
-        for (int k = tid; k < static_cast<int>(gridDim.x); k += kLmBlock) {
+        for (int k = tid; k < nblk; k += kLmBatchBlock) {
             const float v = __hip_atomic_load(&pv[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const int ii = __hip_atomic_load(&pi[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (v > bv || (v == bv && ii < bi)) {
@@ -2097,15 +2162,16 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_batch_kernel(
         }
         const int p = pos_old + 1 < max_seq ? pos_old + 1 : max_seq - 1;
         float2* cr = cur_rope + static_cast<long>(g0 + g) * half_hd;
-        for (int k = tid; k < half_hd; k += kLmBlock) cr[k] = rope[static_cast<long>(p) * half_hd + k];
+        for (int k = tid; k < half_hd; k += kLmBatchBlock)
+            cr[k] = rope[static_cast<long>(p) * half_hd + k];
         __syncthreads();  // wv / wi are reused by the next sequence
     }
     if (tid == 0) st[g0].ticket = 0u;
 }
 
-typedef void (*LmBatchKernel)(const uint16_t*, const uint16_t*, const float*, float, float*,
-                              float*, int*, EngineState*, int*, long, int, int, const float2*,
-                              float2*, int, int, int, int, int, int);
+typedef void (*LmBatchKernel)(const uint16_t*, const float*, float*, float*, int*,
+                              EngineState*, int*, long, int, int, const float2*, float2*, int,
+                              int, int, int, int, int);
 
 template <bool kFull>
 LmBatchKernel lm_head_batch_for_nc(int nc) {
@@ -2121,19 +2187,19 @@ LmBatchKernel lm_head_batch_for_nc(int nc) {
     }
 }
 
-// The batched LM head holds the group's normalised vectors in LDS, so it
-// takes hidden sizes up to kLmBatchMaxH (NC <= 8 chunks per lane).
-constexpr int kLmBatchMaxH = 4096;
-
 LmBatchKernel lm_head_batch_for(int H) {
     const int nc = (H / 8 + kWave - 1) / kWave;
     return (H % 512 == 0) ? lm_head_batch_for_nc<true>(nc) : lm_head_batch_for_nc<false>(nc);
 }
 
-size_t lm_head_batch_lds(int H) {
+// floats per padded normalised vector: lm_xpad(nc * 64), nc = ceil(H / 512)
+int lm_head_batch_xstride(int H) {
     const int nc = (H / 8 + kWave - 1) / kWave;
-    const size_t xstride = 8 * (nc * kWave) + 4 * ((nc * kWave) >> 3);  // lm_xpad(nc * 64)
-    return (static_cast<size_t>(kLmGroup) * xstride +
+    return 8 * (nc * kWave) + 4 * ((nc * kWave) >> 3);
+}
+
+size_t lm_head_batch_lds(int H) {
+    return (static_cast<size_t>(kLmGroup) * lm_head_batch_xstride(H) +
             static_cast<size_t>(kLmGroup) * kLmBatchMaxRows) * sizeof(float);
 }
 
@@ -3148,6 +3214,7 @@ struct spb_batch_engine {
     PrefillBufs step;  // the decode step's per-token buffers (batch tokens)
     PrefillBufs pf;    // the prompt prefill's buffers
     float* logits = nullptr;              // [batch][vocab]
+    float* xn = nullptr;                  // [batch][padded hidden]: final-normed vectors
     float* part_v = nullptr;              // [batch][lm_grid]
     int* part_i = nullptr;                // [batch][lm_grid]
     int* tokens = nullptr;                // [batch][max_seq + 1]
@@ -3171,7 +3238,8 @@ struct spb_batch_engine {
 
     // One decode step of every sequence: per layer the producer, GEMM(s)
     // and sink of each projection over the batch's tokens and the batched
-    // attention; then the LM head in groups of kLmGroup sequences.
+    // attention; then the final norm and the LM head (groups of kLmGroup
+    // sequences in one launch).
     hipError_t enqueue_step(hipStream_t s) const {
         const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
         const int nkv = cfg.num_key_value_heads, H = cfg.hidden_size;
@@ -3261,14 +3329,15 @@ struct spb_batch_engine {
                                     H, H, H, B, s);
             }
         }
-        const int V = cfg.vocab_size;
-        for (int g0 = 0; g0 < B; g0 += kLmGroup) {
-            const int gn = B - g0 < kLmGroup ? B - g0 : kLmGroup;
-            hipLaunchKernelGGL(lm_kernel, dim3(lm_grid), dim3(kLmBlock), lm_head_batch_lds(H), s,
-                               lm_head, step.r, final_norm, eps, logits, part_v, part_i, st,
-                               tokens, tok_stride(), V, H, rope, cur_rope, hd / 2, max_seq,
-                               V / lm_grid, V % lm_grid, g0, gn);
-        }
+        const int V = cfg.vocab_size, xstride = lm_head_batch_xstride(H);
+        const int nc64 = (H / 8 + kWave - 1) / kWave * kWave;
+        const int ng = (B + kLmGroup - 1) / kLmGroup;
+        hipLaunchKernelGGL(final_norm_batch_kernel<true>, dim3(B), dim3(kLmBlock), 0, s, step.r,
+                           final_norm, eps, xn, H, nc64, xstride);
+        hipLaunchKernelGGL(lm_kernel, dim3(lm_grid * ng), dim3(kLmBatchBlock),
+                           lm_head_batch_lds(H), s, lm_head, xn, logits, part_v, part_i, st,
+                           tokens, tok_stride(), V, H, rope, cur_rope, hd / 2, max_seq,
+                           V / lm_grid, V % lm_grid, lm_grid, B);
         return hipGetLastError();
     }
 };
@@ -3302,13 +3371,15 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
     e->S = (max_seq + kAttnSplit - 1) / kAttnSplit;
     e->kv_seq = static_cast<long>(nkv) * max_seq * hd;
     e->lm_kernel = lm_head_batch_for(H);
-    // one block per CU, at least vocab / kLmBatchMaxRows blocks (the rows of
-    // a block are staged in LDS)
-    const long lm_need = (static_cast<long>(V) + kLmBlock / kWave - 1) / (kLmBlock / kWave);
+    // blocks per group: one per CU, at least vocab / kLmBatchMaxRows (the
+    // rows of a block are staged in LDS), a multiple of 8 (one per XCD)
+    const long lm_need = (static_cast<long>(V) + 8 * kLmBatchBlock / kWave - 1) /
+                         (8 * kLmBatchBlock / kWave);  // an octet of rows per wave
     const long lm_min = (static_cast<long>(V) + kLmBatchMaxRows - 1) / kLmBatchMaxRows;
     long lm_grid = device_cu_count();
     if (lm_grid > lm_need) lm_grid = lm_need;
-    e->lm_grid = static_cast<int>(lm_grid > lm_min ? lm_grid : lm_min);
+    lm_grid = lm_grid > lm_min ? lm_grid : lm_min;
+    e->lm_grid = static_cast<int>((lm_grid + 7) / 8 * 8);
 
     auto& own = e->owned;
     const size_t kv = static_cast<size_t>(batch) * e->kv_seq;
@@ -3322,6 +3393,7 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
     ok = ok && alloc_prefill(e->step, *cfg, e->S, own, batch) &&
          alloc_prefill(e->pf, *cfg, e->S, own) &&
          (e->logits = dev_alloc<float>(B * V, own)) &&
+         (e->xn = dev_alloc<float>(B * lm_head_batch_xstride(H), own)) &&
          (e->part_v = dev_alloc<float>(B * e->lm_grid, own)) &&
          (e->part_i = dev_alloc<int>(B * e->lm_grid, own)) &&
          (e->tokens = dev_alloc<int>(B * (max_seq + 1), own)) &&
