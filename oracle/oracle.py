@@ -391,7 +391,7 @@ class EngineOracle:
         _elib().spbo_engine_hidden(self._e, _p(out))
         return out
 
-    DEBUG = {"qkv": 0, "attn": 1, "o": 2, "x_mid": 3, "gate_up": 4, "h": 5, "m": 6}
+    DEBUG = {"qkv": 0, "attn": 1, "o": 2, "x_mid": 3, "gate_up": 4, "h": 5, "m": 6, "xn": 7}
 
     def debug(self, name: str) -> np.ndarray:
         """An internal vector of the last step's last layer (see

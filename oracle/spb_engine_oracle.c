@@ -466,7 +466,8 @@ void spbo_engine_hidden(const spbo_engine* e, float* out) { memcpy(out, e->x, si
 /* Internal vectors of the last step's last layer, for checking the checker
  * itself: 0 = q|k|v (pre-RoPE), 1 = attention output, 2 = o (after the
  * sub-norm), 3 = mid-layer residual, 4 = gate|up, 5 = normalised layer input,
- * 6 = normalised down-projection input. */
+ * 6 = normalised down-projection input, 7 = final-normed hidden state (after
+ * a step with the LM head). */
 int spbo_engine_debug(const spbo_engine* e, int which, float* out) {
     const int H = e->H, kvd = e->nkv * e->hd, I = e->I;
     switch (which) {
@@ -477,6 +478,7 @@ int spbo_engine_debug(const spbo_engine* e, int which, float* out) {
         case 4: memcpy(out, e->gu, sizeof(float) * 2 * I); return 2 * I;
         case 5: memcpy(out, e->h_in, sizeof(float) * H); return H;
         case 6: memcpy(out, e->m_in, sizeof(float) * I); return I;
+        case 7: memcpy(out, e->vec, sizeof(float) * H); return H;
         default: return 0;
     }
 }

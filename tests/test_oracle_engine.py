@@ -74,18 +74,20 @@ def _rope64(v, pos, cfg):
                           x0 * np.sin(ang) + x1 * np.cos(ang)], -1).reshape(-1))
 
 
-@pytest.mark.parametrize("nkv,sub_norms", [(2, True), (4, True), (1, False)])
-def test_engine_oracle_teacher_forced(nkv, sub_norms):
+@pytest.mark.parametrize("nkv,sub_norms,max_seq,n_pos", [
+    (2, True, 128, 70), (4, True, 128, 70), (1, False, 128, 70),
+    (2, True, 512, 300)])  # five 64-position splits
+def test_engine_oracle_teacher_forced(nkv, sub_norms, max_seq, n_pos):
     cfg = _cfg(num_key_value_heads=nkv)
     H, I, hd, nh = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim, cfg.num_attention_heads
     kvd = nkv * hd
     host = host_model(cfg, seed=nkv, qk_gamma=0.02, sub_norms=sub_norms, norm_jitter=0.1)
     L = host["layers"][0]
     n_in, n_post, n_sub, n_ffn = L["norms"]
-    e = O.EngineOracle(host, 128)
+    e = O.EngineOracle(host, max_seq)
     emb = (np.asarray(host["embed"], np.uint32) << 16).view(np.float32).astype(np.float64)
     ks, vs = [], []
-    toks = [int(t) for t in np.random.default_rng(nkv).integers(0, cfg.vocab_size, 70)]
+    toks = [int(t) for t in np.random.default_rng(nkv).integers(0, cfg.vocab_size, n_pos)]
     for pos, tok in enumerate(toks):
         argmax, logits = e.step(tok)
         x_in = emb[tok]
@@ -126,8 +128,9 @@ def test_engine_oracle_teacher_forced(nkv, sub_norms):
         x_out = e.hidden()
         _close(x_out, bf16(bf16(_bitlinear64(m, L["down_proj"], raw=True)) + x_mid),
                f"down + residual @{pos}")
-        xn = _rms64(x_out, host["final_norm"], cfg.rms_norm_eps)
-        lg = emb @ xn
+        xn = e.debug("xn")
+        _close(xn, _rms64(x_out, host["final_norm"], cfg.rms_norm_eps), f"final norm @{pos}")
+        lg = emb @ np.asarray(xn, np.float64)
         assert np.abs(logits - lg).max() <= 1e-5 * np.abs(lg).max() + 1e-6, f"logits @{pos}"
         top2 = np.sort(lg)[-2:]
         if top2[1] - top2[0] > 1e-4 * np.abs(lg).max():
