@@ -1142,9 +1142,9 @@ struct SinkPairs<QkvRopeSink> {
 //     read of each K element per block, unpacked once) and the quarter of
 //     every q head of the group from LDS; the 4 quarter sums of a (head,
 //     position) meet in the 4 lanes of a quad (two DPP adds).
-//   * V rows of the split stay bf16 in LDS; a PV thread owns element d of
-//     NH heads, unpacks each V element once for them, and reads 4 positions'
-//     weights of a head with one 16-byte load.
+//   * V rows of the split stay bf16 in LDS; a PV thread owns dims (d, d+1)
+//     of one head, reads both with one 32-bit load, and reads 4 positions'
+//     weights with one 16-byte load.
 //   score_j = ((a0 + a1) + (a2 + a3)) * scale, a_k = fma over the d of
 //     quarter k (ascending) of q[d] * k_j[d]
 //   per head: m = max_j score_j, e_j = exp(score_j - m),
@@ -1160,10 +1160,11 @@ struct SinkPairs<QkvRopeSink> {
 // sum, stored as the split's partials of heads kvh * G .. kvh * G + G - 1.
 // Scores: the thread unpacks its K quarter once and runs the quarter's fma
 // chain for every head of the group; the four quarters of a position are the
-// four lanes of a quad and combine through DPP.  V sums: thread t takes
-// element t % HD of NH heads (NH = G * HD / 256, at least 1), unpacking each
-// V element once for them.  jn: positions of the split holding positions
-// 0..pos.  A caller that writes qs again barriers first.
+// four lanes of a quad and combine through DPP.  V sums: a thread owns a
+// pair of elements of one head (one 32-bit V read per position, one 16-byte
+// weight read per 4 positions: the V phase's LDS reads are what its time is
+// made of).  jn: positions of the split holding positions 0..pos.  A caller
+// that writes qs again barriers first.
 template <int HD, int G>
 __device__ __forceinline__ void attention_split(const uint4 (&kq)[HD / 32], float (&qs)[G][HD],
                                                 uint32_t (&vs)[kAttnSplit][HD / 2 + 1],
@@ -1216,53 +1217,30 @@ __device__ __forceinline__ void attention_split(const uint4 (&kq)[HD / 32], floa
         }
     }
     __syncthreads();
-    constexpr int kOut = G * HD;
-    constexpr int NH = kOut > kAttnThreads ? kOut / kAttnThreads : 1;  // heads per thread
-    if (tid < kOut / NH) {
-        const int d = tid % HD, g0 = (tid / HD) * NH;
-        const uint16_t* vcol = reinterpret_cast<const uint16_t*>(&vs[0][0]) + d;
-        float a[NH];
-#pragma unroll
-        for (int h = 0; h < NH; ++h) a[h] = 0.0f;
-        auto step = [&](int jj, const float (&e)[NH]) {
-            const float v = __builtin_bit_cast(
-                float, static_cast<uint32_t>(vcol[jj * 2 * kVRow]) << 16);
-#pragma unroll
-            for (int h = 0; h < NH; ++h) a[h] = __builtin_fmaf(e[h], v, a[h]);
+    // weighted V sums: thread o owns elements (2dp, 2dp+1) of head o / (HD/2)
+    for (int o = tid; o < G * (HD / 2); o += kAttnThreads) {
+        const int g = o / (HD / 2), dp = o - g * (HD / 2);
+        float a0 = 0.0f, a1 = 0.0f;
+        auto step = [&](int jj, float e) {
+            const uint32_t w = vs[jj][dp];
+            a0 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w & 0xFFFFu)), a0);
+            a1 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w >> 16)), a1);
         };
         const int n4 = jn >> 2;
         for (int q = 0; q < n4; ++q) {
-            float4 e4[NH];
-#pragma unroll
-            for (int h = 0; h < NH; ++h) e4[h] = *reinterpret_cast<const float4*>(&sc[g0 + h][4 * q]);
-            float e[NH];
-#pragma unroll
-            for (int h = 0; h < NH; ++h) e[h] = e4[h].x;
-            step(4 * q, e);
-#pragma unroll
-            for (int h = 0; h < NH; ++h) e[h] = e4[h].y;
-            step(4 * q + 1, e);
-#pragma unroll
-            for (int h = 0; h < NH; ++h) e[h] = e4[h].z;
-            step(4 * q + 2, e);
-#pragma unroll
-            for (int h = 0; h < NH; ++h) e[h] = e4[h].w;
-            step(4 * q + 3, e);
+            const float4 e = *reinterpret_cast<const float4*>(&sc[g][4 * q]);
+            step(4 * q, e.x);
+            step(4 * q + 1, e.y);
+            step(4 * q + 2, e.z);
+            step(4 * q + 3, e.w);
         }
-        for (int jj = 4 * n4; jj < jn; ++jj) {
-            float e[NH];
-#pragma unroll
-            for (int h = 0; h < NH; ++h) e[h] = sc[g0 + h][jj];
-            step(jj, e);
-        }
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            const int hh = kvh * G + g0 + h;
-            pacc[(static_cast<long>(hh) * S + s) * HD + d] = a[h];
-            if (d == 0) {
-                pm[hh * S + s] = hmax[g0 + h];
-                pl[hh * S + s] = hsum[g0 + h];
-            }
+        for (int jj = 4 * n4; jj < jn; ++jj) step(jj, sc[g][jj]);
+        const int h = kvh * G + g;
+        float* out = pacc + (static_cast<long>(h) * S + s) * HD + 2 * dp;
+        *reinterpret_cast<float2*>(out) = make_float2(a0, a1);
+        if (dp == 0) {
+            pm[h * S + s] = hmax[g];
+            pl[h * S + s] = hsum[g];
         }
     }
 }
