@@ -116,3 +116,25 @@ def test_batch_engine_rejects_bad_input(gpu):
     assert eng.generate([[5, 6, 7]], 4, stop_at_eos=False) == \
         _oracle_tokens(model.to_host(), 64, [[5, 6, 7]], 4)
     eng.close()
+
+
+def test_batch_decode_odd_shapes(gpu):
+    """Shapes off the 2B model's multiples: hidden 640 (the LM heads' partial
+    last 512-element step), vocabulary 4093 (blocks and row octets that end
+    inside a row group), GQA group 2, and 12 sequences (a last group of 4 in
+    the batched LM head); tokens equal to the oracle's single-sequence
+    generate on the batched and the bs=1 engine."""
+    from spbitnet_amd.model import BatchInferenceEngine, InferenceEngine, Model
+    cfg = _cfg(hidden_size=640, num_attention_heads=10, num_key_value_heads=5,
+               intermediate_size=1664, vocab_size=4093, max_position_embeddings=512)
+    model = Model.random(cfg, seed=311)
+    prompts = _prompts(12, cfg.vocab_size, 1, 300, seed=19)
+    print("oracle", flush=True)
+    want = _oracle_tokens(model.to_host(), 512, prompts, 12)
+    eng = BatchInferenceEngine(model, max_seq=512, batch=12)
+    assert eng.generate(prompts, 12, stop_at_eos=False) == want
+    eng.close()
+    one = InferenceEngine(model, max_seq=512)
+    for b in (0, 7):
+        assert one.generate(prompts[b], 12, stop_at_eos=False) == want[b]
+    one.close()
