@@ -1153,6 +1153,65 @@ struct SinkPairs<QkvRopeSink> {
 // Reference: attention_scores, softmax, attention_output
 // (inference_kernels.cu:241-371), GQA kv = h * nkv / nh.
 
+// The split's softmax over its jn live positions, per head (wave g % 4 takes
+// head g, lane = position): m = the wave maximum, e = exp(score - m) stored
+// to sc, l = the wave tree sum of e.  score(g, lane) reads the head's score
+// of the lane's position; after a barrier that orders the scores.
+template <int G, class Score>
+__device__ __forceinline__ void split_softmax(float (&sc)[G][kAttnSplit], float (&hmax)[G],
+                                              float (&hsum)[G], int jn, Score score) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    for (int g = wave; g < G; g += kAttnThreads / kWave) {
+        const float v = lane < jn ? score(g, lane) : -INFINITY;
+        const float m = wave_max_tree(v);
+        const float e = lane < jn ? exp_neg(v - m) : 0.0f;
+        const float l = wave_sum_tree(e);
+        sc[g][lane] = e;
+        if (lane == 0) {
+            hmax[g] = m;
+            hsum[g] = l;
+        }
+    }
+}
+
+// The split's weighted V sums and partials: thread o owns elements (2dp,
+// 2dp+1) of head o / (HD/2) (one 32-bit V read per position, one 16-byte
+// weight read per 4 positions), j ascending with fma.  After a barrier that
+// orders the softmax.
+template <int HD, int G>
+__device__ __forceinline__ void split_weighted_v(const uint32_t (&vs)[kAttnSplit][HD / 2 + 1],
+                                                 const float (&sc)[G][kAttnSplit],
+                                                 const float (&hmax)[G], const float (&hsum)[G],
+                                                 int jn, int s, int kvh, int S,
+                                                 float* __restrict__ pm, float* __restrict__ pl,
+                                                 float* __restrict__ pacc) {
+    for (int o = threadIdx.x; o < G * (HD / 2); o += kAttnThreads) {
+        const int g = o / (HD / 2), dp = o - g * (HD / 2);
+        float a0 = 0.0f, a1 = 0.0f;
+        auto step = [&](int jj, float e) {
+            const uint32_t w = vs[jj][dp];
+            a0 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w & 0xFFFFu)), a0);
+            a1 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w >> 16)), a1);
+        };
+        const int n4 = jn >> 2;
+        for (int q = 0; q < n4; ++q) {
+            const float4 e = *reinterpret_cast<const float4*>(&sc[g][4 * q]);
+            step(4 * q, e.x);
+            step(4 * q + 1, e.y);
+            step(4 * q + 2, e.z);
+            step(4 * q + 3, e.w);
+        }
+        for (int jj = 4 * n4; jj < jn; ++jj) step(jj, sc[g][jj]);
+        const int h = kvh * G + g;
+        float* out = pacc + (static_cast<long>(h) * S + s) * HD + 2 * dp;
+        *reinterpret_cast<float2*>(out) = make_float2(a0, a1);
+        if (dp == 0) {
+            pm[h * S + s] = hmax[g];
+            pl[h * S + s] = hsum[g];
+        }
+    }
+}
+
 // The per-split work of one query (the decode kernels and the prefill kernel
 // share it): once its q (qs, float) and the split's V rows (vs, bf16) are in
 // LDS behind a barrier and the thread holds its quarter of K row p = tid / 4
@@ -1205,44 +1264,9 @@ __device__ __forceinline__ void attention_split(const uint4 (&kq)[HD / 32], floa
         }
     }
     __syncthreads();
-    for (int g = wave; g < G; g += kAttnThreads / kWave) {
-        const float v = lane < jn ? sc[g][lane] : -INFINITY;
-        const float m = wave_max_tree(v);
-        const float e = lane < jn ? exp_neg(v - m) : 0.0f;
-        const float l = wave_sum_tree(e);
-        sc[g][lane] = e;
-        if (lane == 0) {
-            hmax[g] = m;
-            hsum[g] = l;
-        }
-    }
+    split_softmax<G>(sc, hmax, hsum, jn, [&](int g, int p) { return sc[g][p]; });
     __syncthreads();
-    // weighted V sums: thread o owns elements (2dp, 2dp+1) of head o / (HD/2)
-    for (int o = tid; o < G * (HD / 2); o += kAttnThreads) {
-        const int g = o / (HD / 2), dp = o - g * (HD / 2);
-        float a0 = 0.0f, a1 = 0.0f;
-        auto step = [&](int jj, float e) {
-            const uint32_t w = vs[jj][dp];
-            a0 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w & 0xFFFFu)), a0);
-            a1 = __builtin_fmaf(e, BF16::to_float(static_cast<uint16_t>(w >> 16)), a1);
-        };
-        const int n4 = jn >> 2;
-        for (int q = 0; q < n4; ++q) {
-            const float4 e = *reinterpret_cast<const float4*>(&sc[g][4 * q]);
-            step(4 * q, e.x);
-            step(4 * q + 1, e.y);
-            step(4 * q + 2, e.z);
-            step(4 * q + 3, e.w);
-        }
-        for (int jj = 4 * n4; jj < jn; ++jj) step(jj, sc[g][jj]);
-        const int h = kvh * G + g;
-        float* out = pacc + (static_cast<long>(h) * S + s) * HD + 2 * dp;
-        *reinterpret_cast<float2*>(out) = make_float2(a0, a1);
-        if (dp == 0) {
-            pm[h * S + s] = hmax[g];
-            pl[h * S + s] = hsum[g];
-        }
-    }
+    split_weighted_v<HD, G>(vs, sc, hmax, hsum, jn, s, kvh, S, pm, pl, pacc);
 }
 
 // Split combine of one decode step, once per head (long contexts): block h
@@ -1383,9 +1407,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
 // Prefill form: the queries of the tokens of a batch (token t at position
 // pos0 + t, its q at qkv + t * qkv_stride, its partials after those of
 // t - 1).  A block (split s, kv head, kQ consecutive tokens) loads the
-// split's K and V once and runs attention_split for each of its tokens whose
-// position reaches the split, the next token's q loaded while the current
-// one is processed.
+// split's K and V once and keeps both in registers for all of its tokens:
+//   * wave w holds quarter w of the head dims of K row j0 + lane, unpacked
+//     (kf), and reads each token's q quarters with scalar loads (the
+//     address is the same for the whole wave), so a score costs no LDS
+//     reads; the four quarter sums meet in LDS (red).
+//   * a V thread holds the element pair dp = tid % (HD/2) of all 64 rows of
+//     the split (vcol, bf16 pairs) and reads only the softmax weights from
+//     LDS.
+// The arithmetic is attention_split's, operation for operation, so a
+// prefilled token's partials equal those of its decode step:
+//   score = ((a0 + a1) + (a2 + a3)) * scale, a_w = fma chain over quarter w,
+//   the softmax of split_softmax, and acc = fma over j ascending of e_j v_j.
 template <int HD, int G, int kQ>
 __global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
@@ -1393,10 +1426,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
     float* __restrict__ pacc, int max_seq, int S, float scale, int pos0, int nt,
     int qkv_stride) {
     constexpr int kU = HD / 8;
-    constexpr int kQU = kU / 4;
-    constexpr int kVRow = HD / 2 + 1;
-    __shared__ __align__(16) float qs[G][HD];
+    constexpr int kQU = kU / 4;       // 16-byte units per quarter row
+    constexpr int kQD = HD / 4;       // elements per quarter row
+    constexpr int kVP = HD / 2;       // element pairs per row
+    constexpr int kVRow = kVP + 1;
+    static_assert(kAttnThreads == 4 * kWave && kAttnSplit == kWave, "4 waves, lane = position");
+    static_assert(kAttnThreads % kVP == 0, "a thread's V pair is the same for all its heads");
     __shared__ uint32_t vs[kAttnSplit][kVRow];
+    __shared__ float red[4][G][kAttnSplit];
     __shared__ __align__(16) float sc[G][kAttnSplit];
     __shared__ float hmax[G], hsum[G];
     const int s = blockIdx.x, kvh = blockIdx.y;
@@ -1404,33 +1441,29 @@ __global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
     const int t0 = blockIdx.z * kQ;
     const int t1 = t0 + kQ < nt ? t0 + kQ : nt;
     if (j0 > pos0 + t1 - 1) return;  // no token of the block reaches the split
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wq = __builtin_amdgcn_readfirstlane(tid / kWave);
     const long cache0 = static_cast<long>(kvh) * max_seq * HD;
     const int jmax = max_seq - 1;
-    // the thread's quarter of K row j0 + tid / 4 (clamped to the cache)
+    // quarter wq of K row j0 + lane (clamped to the cache) and the split's V
+    // rows (kVPer 16-byte units per thread), all loads issued together
     uint4 kq[kQU];
     {
-        const int j = j0 + (tid >> 2) <= jmax ? j0 + (tid >> 2) : jmax;
+        const int j = j0 + lane <= jmax ? j0 + lane : jmax;
         const uint4* kr = reinterpret_cast<const uint4*>(kc + cache0 + static_cast<long>(j) * HD) +
-                          (tid & 3) * kQU;
+                          wq * kQU;
 #pragma unroll
         for (int u = 0; u < kQU; ++u) kq[u] = kr[u];
     }
     constexpr int kVPer = kAttnSplit * kU / kAttnThreads;
     uint4 vraw[kVPer];
 #pragma unroll
-    for (int t = 0; t < kVPer; ++t) {
-        const int idx = tid + t * kAttnThreads;
+    for (int i = 0; i < kVPer; ++i) {
+        const int idx = tid + i * kAttnThreads;
         const int jj = idx / kU, c = idx - jj * kU;
         const int j = j0 + jj <= jmax ? j0 + jj : jmax;
-        vraw[t] = reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
+        vraw[i] = reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
     }
-    const bool has_q = tid < G * kU;
-    // the first token of the block that reaches the split
-    int t = t0;
-    if (j0 > pos0 + t) t = j0 - pos0;
-    uint4 qraw = make_uint4(0, 0, 0, 0);
-    if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + static_cast<long>(t) * qkv_stride + (kvh * G) * HD)[tid];
 #pragma unroll
     for (int i = 0; i < kVPer; ++i) {
         const int idx = tid + i * kAttnThreads;
@@ -1441,22 +1474,103 @@ __global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
         row[2] = vraw[i].z;
         row[3] = vraw[i].w;
     }
+    float kf[kQD];
+#pragma unroll
+    for (int u = 0; u < kQU; ++u) {
+        float f[8];
+        unpack_bf16x8(kq[u], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[8 * u + e] = f[e];
+    }
+    __syncthreads();
+    const int dp = tid % kVP;
+    uint32_t vcol[kAttnSplit];
+#pragma unroll
+    for (int jj = 0; jj < kAttnSplit; ++jj) vcol[jj] = vs[jj][dp];
+
+    // q element pairs of quarter wq of token t's heads (the address is the
+    // same for the whole wave: scalar loads); the next token's are loaded
+    // during the current token's softmax and V sums when they fit in SGPRs
+    constexpr int kQP = kQD / 2;
+    constexpr bool kPrefetchQ = G * kQP <= 64;
+    const uint32_t* q32 = reinterpret_cast<const uint32_t*>(qkv);
+    auto load_q = [&](int tt, uint32_t (&q)[G * kQP]) {
+        const uint32_t* qw =
+            q32 + (static_cast<long>(tt) * qkv_stride + (kvh * G) * HD + wq * kQD) / 2;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < kQP; ++i) q[g * kQP + i] = qw[g * kVP + i];
+    };
     const long hs = static_cast<long>(gridDim.y) * G * S;
+    // the first token of the block that reaches the split
+    int t = t0;
+    if (j0 > pos0 + t) t = j0 - pos0;
+    uint32_t qn[G * kQP];
+    if (kPrefetchQ) load_q(t, qn);
     for (; t < t1; ++t) {
-        if (t > t0) __syncthreads();  // the previous token's reads of qs and sc are done
-        if (has_q) {
-            float f[8];
-            unpack_bf16x8(qraw, f);
-            store_f8(&qs[tid / kU][8 * (tid % kU)], f);
-        }
-        // the next token's q (clamped to the block's last token)
-        const int tn = t + 1 < t1 ? t + 1 : t;
-        if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + static_cast<long>(tn) * qkv_stride + (kvh * G) * HD)[tid];
         const int pos = pos0 + t;
         const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
+        // V stays packed (64 registers, not 128 unpacked ones): the block
+        // keeps 4 waves per SIMD
+#pragma unroll
+        for (int jj = 0; jj < kAttnSplit; ++jj) asm volatile("" : "+v"(vcol[jj]));
+        uint32_t qc[G * kQP];
+        if (kPrefetchQ) {
+#pragma unroll
+            for (int i = 0; i < G * kQP; ++i) qc[i] = qn[i];
+        } else {
+            load_q(t, qc);
+        }
+        // scores: quarter wq of every q head of the group against K row j0 + lane
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kQP; ++i) {
+                const uint32_t w = qc[g * kQP + i];
+                a = __builtin_fmaf(__uint_as_float(w << 16), kf[2 * i], a);
+                a = __builtin_fmaf(__uint_as_float(w & 0xFFFF0000u), kf[2 * i + 1], a);
+            }
+            red[wq][g][lane] = a;
+        }
+        __syncthreads();  // red complete; the previous token's reads of sc are done
+        if (kPrefetchQ && t + 1 < t1) load_q(t + 1, qn);
+        split_softmax<G>(sc, hmax, hsum, jn, [&](int g, int p) {
+            return ((red[0][g][p] + red[1][g][p]) + (red[2][g][p] + red[3][g][p])) * scale;
+        });
         __syncthreads();
-        attention_split<HD, G>(kq, qs, vs, sc, hmax, hsum, jn, scale, s, kvh, S, pm + t * hs,
-                               pl + t * hs, pacc + t * hs * HD);
+        // weighted V sums of the heads o / kVP, element pair dp (all 64
+        // positions without a bound per step in the common full split)
+        for (int o = tid; o < G * kVP; o += kAttnThreads) {
+            const int g = o / kVP;
+            float a0 = 0.0f, a1 = 0.0f;
+            auto step = [&](float e, uint32_t w) {
+                a0 = __builtin_fmaf(e, __uint_as_float(w << 16), a0);
+                a1 = __builtin_fmaf(e, __uint_as_float(w & 0xFFFF0000u), a1);
+            };
+            if (jn == kAttnSplit) {
+#pragma unroll
+                for (int q = 0; q < kAttnSplit / 4; ++q) {
+                    const float4 e = *reinterpret_cast<const float4*>(&sc[g][4 * q]);
+                    step(e.x, vcol[4 * q]);
+                    step(e.y, vcol[4 * q + 1]);
+                    step(e.z, vcol[4 * q + 2]);
+                    step(e.w, vcol[4 * q + 3]);
+                }
+            } else {
+#pragma unroll
+                for (int jj = 0; jj < kAttnSplit; ++jj)
+                    if (jj < jn) step(sc[g][jj], vcol[jj]);
+            }
+            const int h = kvh * G + g;
+            float* out = pacc + t * hs * HD + (static_cast<long>(h) * S + s) * HD + 2 * dp;
+            *reinterpret_cast<float2*>(out) = make_float2(a0, a1);
+            if (dp == 0) {
+                pm[t * hs + h * S + s] = hmax[g];
+                pl[t * hs + h * S + s] = hsum[g];
+            }
+        }
     }
 }
 

@@ -149,15 +149,17 @@ def test_engine_batched_prefill_matches_stepwise(gpu):
     GEMM, the prefill form of the attention kernel) against one decode step
     per prompt token on the same engine: the logits of the first generated
     step are bit-identical and the generated tokens equal; prompts that span
-    several prefill passes and attention splits, GQA groups 4 and 1, with and
-    without sub-norms."""
+    several prefill passes and attention splits, GQA groups 8, 4 and 1, head
+    dims 64 and 128, with and without sub-norms."""
     # 2100 tokens: three prefill passes (1024, 1024, 51 tokens) and 33 splits
-    cases = [(dict(), 2, 2200, 2100), (dict(sub_norms=False), 2, 96, 40), (dict(), 8, 320, 300),
-             (dict(), 1, 64, 17)]
-    for kw, nkv, max_seq, n_prompt in cases:
+    hd128 = dict(head_dim=128, hidden_size=1024)
+    cases = [({}, dict(), 2, 2200, 2100), ({}, dict(sub_norms=False), 2, 96, 40),
+             ({}, dict(), 8, 320, 300), ({}, dict(), 1, 64, 17), (hd128, dict(), 2, 200, 150),
+             (hd128, dict(), 1, 160, 130), (hd128, dict(), 8, 96, 70)]
+    for ckw, kw, nkv, max_seq, n_prompt in cases:
         cfg = _small_config(num_key_value_heads=nkv, max_position_embeddings=max(max_seq, 1024),
-                            num_hidden_layers=1 if n_prompt > 1000 else 2)
-        print(f"prefill {kw} nkv={nkv} max_seq={max_seq} prompt={n_prompt}", flush=True)
+                            num_hidden_layers=1 if n_prompt > 1000 else 2, **ckw)
+        print(f"prefill {ckw} {kw} nkv={nkv} max_seq={max_seq} prompt={n_prompt}", flush=True)
         model, eng, ora = _engine_pair(cfg, seed=61 + nkv + n_prompt, max_seq=max_seq, **kw)
         prompt = _prompt(n_prompt, cfg.vocab_size, 5 + nkv)
         eng.set_prefill_batch(16)
