@@ -39,6 +39,7 @@
 #include <vector>
 
 #include "bitplane.hpp"
+#include "gemm_staged.hpp"
 #include "spbitnet_amd.h"
 
 namespace spb {
@@ -996,6 +997,17 @@ struct SegBf16Sink {
         const float dq = r < end0 ? opaque(dq0) : (r < end1 ? opaque(dq1) : opaque(dq2));
         out[r] = BF16::from_float(static_cast<float>(acc) * dq);
     }
+    // rows r .. r + 3 (r % 4 == 0, out 8-byte aligned there) in one store
+    __device__ void store4(long r, const int (&acc)[4]) const {
+        uint32_t h[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const long rk = r + k;
+            const float dq = rk < end0 ? opaque(dq0) : (rk < end1 ? opaque(dq1) : opaque(dq2));
+            h[k] = BF16::from_float(static_cast<float>(acc[k]) * dq);
+        }
+        *reinterpret_cast<uint2*>(out + r) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    }
 };
 
 // down projection: x_out[r] = bf16(bf16(acc * dq) + res[r])
@@ -1028,6 +1040,20 @@ struct ResidualSink {
         const uint16_t rv = r == pre_row ? static_cast<uint16_t>(opaque(static_cast<uint32_t>(pre_res)))
                                          : res[r];
         x_out[r] = BF16::from_float(d + BF16::to_float(rv));
+    }
+    // rows r .. r + 3 (r % 4 == 0, 8-byte aligned there): one load, one store
+    __device__ void store4(long r, const int (&acc)[4]) const {
+        const uint2 rv = *reinterpret_cast<const uint2*>(res + r);
+        const uint32_t rw[2] = {rv.x, rv.y};
+        uint32_t h[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float d = bf16r(static_cast<float>(acc[k]) * dq);
+            const uint16_t e = static_cast<uint16_t>(k & 1 ? rw[k >> 1] >> 16 : rw[k >> 1] & 0xFFFFu);
+            h[k] = BF16::from_float(d + BF16::to_float(e));
+        }
+        *reinterpret_cast<uint2*>(x_out + r) =
+            make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
     }
 };
 
@@ -1127,6 +1153,21 @@ struct QkvRopeSink {
 
 template <>
 struct SinkPairs<QkvRopeSink> {
+    static constexpr bool value = true;
+};
+
+// Sinks with a four-row store (store4): the GEMM epilogue's lane holds four
+// consecutive rows of one token.
+template <class Sink>
+struct SinkQuads {
+    static constexpr bool value = false;
+};
+template <>
+struct SinkQuads<SegBf16Sink> {
+    static constexpr bool value = true;
+};
+template <>
+struct SinkQuads<ResidualSink> {
     static constexpr bool value = true;
 };
 
@@ -1233,9 +1274,8 @@ __device__ __forceinline__ void attention_split(const uint4 (&kq)[HD / 32], floa
                                                 float* __restrict__ pl, float* __restrict__ pacc) {
     constexpr int kQU = HD / 32;  // 16-byte units per quarter row
     constexpr int kQD = HD / 4;   // elements per quarter row
-    constexpr int kVRow = HD / 2 + 1;
     static_assert(kAttnThreads == 4 * kAttnSplit, "4 quarters x 64 positions");
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int tid = threadIdx.x;
     const int qq = tid & 3, p = tid >> 2;
     // scores (every lane active: the quads combine through DPP)
     {
@@ -1666,6 +1706,47 @@ __global__ __launch_bounds__(kAttnThreads) void attention_batch_kernel(
 struct AmaxOf {
     float m;
     __device__ float absmax() const { return m; }
+};
+
+// Epilogue of the staged GEMM (gemm_staged.hpp) that passes the products
+// through a per-token sink in registers: the lane holding rows row .. row+3
+// of token tok runs the sink for them with the calls and arithmetic of
+// prefill_sink_kernel, so the outputs are those of a GEMM followed by that
+// kernel, and no int32 product is stored.
+template <class Sink>
+struct SinkOut {
+    Sink sink;
+    long stride;        // per-token output stride
+    const float* amax;  // per-token absmax of the GEMM's int8 input
+    int rows;           // rows of the (stacked) product
+    __device__ void store4(int tok, int row, v4i acc) const {
+        Sink sk = sink;
+        sk.at(tok, stride);
+        sk.prepare();
+        if constexpr (SinkQuads<Sink>::value) {
+            sk.bind(AmaxOf{amax[tok]});
+            if (row + 3 < rows) {
+                const int a[4] = {acc[0], acc[1], acc[2], acc[3]};
+                sk.store4(row, a);
+            } else {
+                sk.prefetch(row, 4, 0);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (row + k < rows) sk.store(row + k, acc[k]);
+            }
+            return;
+        }
+        sk.prefetch(row, 4, 0);
+        sk.bind(AmaxOf{amax[tok]});
+        if constexpr (SinkPairs<Sink>::value) {
+            sk.store_pair(row, acc[0], acc[1]);  // rows are even, row < rows
+            if (row + 2 < rows) sk.store_pair(row + 2, acc[2], acc[3]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (row + k < rows) sk.store(row + k, acc[k]);
+        }
+    }
 };
 
 template <class P>
@@ -2591,6 +2672,58 @@ hipError_t gemm_group(const spb_sparse_linear* const* w, int nw, const int8_t* X
     return hipSuccess;
 }
 
+// Sinks fused into the GEMM at every batch size; the q/k/v sink only up to
+// kFuseTokens tokens: in a 1024-token prefill pass its epilogue (decode
+// state and RoPE row loads per lane, pair stores to the KV cache) made the
+// GEMM longer than GEMM + sink kernel (33.8 against 20.7 + 10.1 us), while
+// the bf16 and residual sinks gained (gate|up 69.4 against 61.1 + 28.0 us,
+// down 40.1 against 36.3 + 7.6 us).
+template <class Sink>
+struct SinkFusesWide {
+    static constexpr bool value = true;
+};
+template <>
+struct SinkFusesWide<QkvRopeSink> {
+    static constexpr bool value = false;
+};
+constexpr int kFuseTokens = 64;
+
+// The products of up to three stacked projections of the int8 tokens X
+// ([n][cols], absmax amax[t]) through a per-token sink (output stride
+// `stride`): one staged GEMM launch with the sink as its epilogue when
+// gemm_stacked_epi takes the shapes (and the sink fuses at n tokens), else
+// the int32 products into y (one launch per projection when they cannot be
+// stacked) and prefill_sink_kernel.
+template <class Sink>
+hipError_t gemm_sink(const spb_sparse_linear* const* w, int nw, const int8_t* X,
+                     const float* amax, const Sink& sink, long stride, int32_t* const* y, int n,
+                     hipStream_t s) {
+    int rows = 0;
+    for (int i = 0; i < nw; ++i) rows += w[i]->rows;
+    if (n <= kFuseTokens || SinkFusesWide<Sink>::value) {
+        const int rc = gemm_stacked_epi(w, nw, X, SinkOut<Sink>{sink, stride, amax, rows}, n, s);
+        if (rc == 0) return hipSuccess;
+        if (rc == 2) return hipErrorLaunchFailure;
+    }
+    const int32_t* yy[3];
+    int ld[3];
+    if (gemm_group(w, nw, X, y, n, s, yy, ld) != hipSuccess) return hipErrorLaunchFailure;
+    const int end0 = w[0]->rows, end1 = nw > 1 ? end0 + w[1]->rows : end0;
+    launch_prefill_sink(sink, stride, amax, yy[0], yy[1], yy[2], end0, end1, rows, ld[0], ld[1],
+                        ld[2], n, s);
+    return hipSuccess;
+}
+
+// Raises the LDS limit of the sink-epilogue GEMM kernels (0 = done); at
+// engine create, before any graph capture.
+int gemm_sink_prepare() {
+    return staged_prepare<SinkOut<QkvRopeSink>>() == 0 &&
+                   staged_prepare<SinkOut<SegBf16Sink>>() == 0 &&
+                   staged_prepare<SinkOut<ResidualSink>>() == 0
+               ? 0
+               : 1;
+}
+
 // Positions pos0 .. pos0 + c - 1 of one sequence (t.tokens holds their ids)
 // through every layer, c <= pf.chunk: the KV cache of those positions as c
 // decode steps would write it.  Returns a HIP error or hipSuccess.
@@ -2620,10 +2753,6 @@ auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
                                     hipMemcpyHostToDevice, s);
     if (err == hipSuccess) err = hipStreamSynchronize(s);  // hs is on this frame
     if (err != hipSuccess) return err;
-    auto gemm = [&](const spb_sparse_linear& w, int32_t* y) {
-        return spb_sparse_ternary_gemm(w.meta, w.values, pf.x, y, w.rows, w.cols, c,
-                                       w.meta_stride, w.values_stride, s);
-    };
     for (size_t l = 0; l < layers.size(); ++l) {
         const spb_transformer_layer& L = layers[l];
         {
@@ -2632,10 +2761,6 @@ auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
             launch_prefill_producer(p, H, pf.st, H, c, pf.x, pf.amax, s);
         }
         const spb_sparse_linear* qkv3[3] = {&L.q_proj, &L.k_proj, &L.v_proj};
-        const int32_t* yq[3];
-        int ldq[3];
-        if (gemm_group(qkv3, 3, pf.x, pf.y, c, s, yq, ldq) != hipSuccess)
-            return hipErrorLaunchFailure;
         {
             QkvRopeSink sink{};
             sink.out = pf.qkv;
@@ -2652,8 +2777,9 @@ auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
             sink.max_seq = max_seq;
             sink.rope_tab = rope;
             sink.rope_pos0 = pos0;
-            launch_prefill_sink(sink, qrows + 2 * kvdim, pf.amax, yq[0], yq[1], yq[2], qrows,
-                                qrows + kvdim, qrows + 2 * kvdim, ldq[0], ldq[1], ldq[2], c, s);
+            if (gemm_sink(qkv3, 3, pf.x, pf.amax, sink, qrows + 2 * kvdim, pf.y, c, s) !=
+                hipSuccess)
+                return hipErrorLaunchFailure;
         }
         // splits that some token of the pass reaches
         const int sp = (pos0 + c - 1) / kAttnSplit + 1 < S ? (pos0 + c - 1) / kAttnSplit + 1 : S;
@@ -2669,28 +2795,24 @@ auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
             AttnCombine p{pf.pm, pf.pl, pf.pacc, hd, S, qrows, hd == 64 ? 6 : 7};
             launch_prefill_producer(p, 0, pf.st, qrows, c, pf.x, pf.amax, s);
         }
-        if (gemm(L.o_proj, pf.y[0])) return hipErrorLaunchFailure;
         {
+            const spb_sparse_linear* o1[1] = {&L.o_proj};
             SegBf16Sink sink{pf.o, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma, H, H,
                              0.f, 0.f, 0.f};
-            launch_prefill_sink(sink, H, pf.amax, pf.y[0], pf.y[0], pf.y[0], H, H, H, H, H,
-                                H, c, s);
+            if (gemm_sink(o1, 1, pf.x, pf.amax, sink, H, pf.y, c, s) != hipSuccess)
+                return hipErrorLaunchFailure;
         }
         {
             SubNormResidualNorm p{pf.o, pf.r, pf.r2, L.attn_sub_norm,
                                   L.post_attention_layernorm, eps, H};
             launch_prefill_producer(p, H, pf.st, H, c, pf.x, pf.amax, s);
         }
-        const spb_sparse_linear* gu2[2] = {&L.gate_proj, &L.up_proj};
-        const int32_t* yg[3];
-        int ldg[3];
-        if (gemm_group(gu2, 2, pf.x, pf.y, c, s, yg, ldg) != hipSuccess)
-            return hipErrorLaunchFailure;
         {
+            const spb_sparse_linear* gu2[2] = {&L.gate_proj, &L.up_proj};
             SegBf16Sink sink{pf.gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
                              I, 2 * I, 0.f, 0.f, 0.f};
-            launch_prefill_sink(sink, 2 * I, pf.amax, yg[0], yg[1], yg[2], I, 2 * I, 2 * I,
-                                ldg[0], ldg[1], ldg[2], c, s);
+            if (gemm_sink(gu2, 2, pf.x, pf.amax, sink, 2 * I, pf.y, c, s) != hipSuccess)
+                return hipErrorLaunchFailure;
         }
         {
             Relu2Norm p{pf.gu, pf.gu + I, L.ffn_sub_norm,
@@ -2698,11 +2820,11 @@ auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
                         eps, I};
             launch_prefill_producer(p, 2 * I, pf.st, I, c, pf.x, pf.amax, s);
         }
-        if (gemm(L.down_proj, pf.y[0])) return hipErrorLaunchFailure;
         {
+            const spb_sparse_linear* d1[1] = {&L.down_proj};
             ResidualSink sink{pf.r, pf.r2, L.down_proj.gamma, 0.f};
-            launch_prefill_sink(sink, H, pf.amax, pf.y[0], pf.y[0], pf.y[0], H, H, H, H, H,
-                                H, c, s);
+            if (gemm_sink(d1, 1, pf.x, pf.amax, sink, H, pf.y, c, s) != hipSuccess)
+                return hipErrorLaunchFailure;
         }
     }
     return hipGetLastError();
@@ -2975,7 +3097,8 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
         return invalid("%s: null argument", fn);
     *out = nullptr;
     if (int rc = check_model(fn, cfg, layers, embed_tokens, lm_head, max_seq)) return rc;
-    if (gemm_prepare() != 0) return launch_status(fn);  // before any graph capture
+    if (gemm_prepare() != 0 || gemm_sink_prepare() != 0)  // before any graph capture
+        return launch_status(fn);
     const int H = cfg->hidden_size, nh = cfg->num_attention_heads, nkv = cfg->num_key_value_heads;
     const int hd = cfg->head_dim, I = cfg->intermediate_size, V = cfg->vocab_size;
     const int kvdim = nkv * hd;
@@ -3339,10 +3462,6 @@ struct spb_batch_engine {
         const float eps = cfg.rms_norm_eps;
         const float scale = 1.0f / sqrtf(static_cast<float>(hd));  // inference.cu:182
         const int B = batch;
-        auto gemm = [&](const spb_sparse_linear& w, int32_t* y) {
-            return spb_sparse_ternary_gemm(w.meta, w.values, step.x, y, w.rows, w.cols, B,
-                                           w.meta_stride, w.values_stride, s);
-        };
         for (size_t l = 0; l < layers.size(); ++l) {
             const spb_transformer_layer& L = layers[l];
             {
@@ -3352,10 +3471,6 @@ struct spb_batch_engine {
                 launch_prefill_producer(p, H, st, H, B, step.x, step.amax, s);
             }
             const spb_sparse_linear* qkv3[3] = {&L.q_proj, &L.k_proj, &L.v_proj};
-            const int32_t* yq[3];
-            int ldq[3];
-            if (gemm_group(qkv3, 3, step.x, step.y, B, s, yq, ldq) != hipSuccess)
-                return hipErrorLaunchFailure;
             {
                 QkvRopeSink sink{};
                 sink.out = step.qkv;
@@ -3373,9 +3488,9 @@ struct spb_batch_engine {
                 sink.max_seq = max_seq;
                 sink.rope_tab = nullptr;  // each sequence's own RoPE row (cur_rope)
                 sink.kv_stride = kv_seq;
-                launch_prefill_sink(sink, qrows + 2 * kvdim, step.amax, yq[0], yq[1], yq[2],
-                                    qrows, qrows + kvdim, qrows + 2 * kvdim, ldq[0], ldq[1],
-                                    ldq[2], B, s);
+                if (gemm_sink(qkv3, 3, step.x, step.amax, sink, qrows + 2 * kvdim, step.y, B,
+                              s) != hipSuccess)
+                    return hipErrorLaunchFailure;
             }
             launch_attention_batch(hd, nh / nkv, S, nkv, B, s, step.qkv, kcache[l], vcache[l],
                                    step.pm, step.pl, step.pacc, st, max_seq, scale,
@@ -3384,28 +3499,25 @@ struct spb_batch_engine {
                 AttnCombine p{step.pm, step.pl, step.pacc, hd, S, qrows, hd == 64 ? 6 : 7};
                 launch_prefill_producer(p, 0, st, qrows, B, step.x, step.amax, s);
             }
-            if (gemm(L.o_proj, step.y[0])) return hipErrorLaunchFailure;
             {
+                const spb_sparse_linear* o1[1] = {&L.o_proj};
                 SegBf16Sink sink{step.o, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma, H, H,
                                  0.f, 0.f, 0.f};
-                launch_prefill_sink(sink, H, step.amax, step.y[0], step.y[0], step.y[0], H, H, H,
-                                    H, H, H, B, s);
+                if (gemm_sink(o1, 1, step.x, step.amax, sink, H, step.y, B, s) != hipSuccess)
+                    return hipErrorLaunchFailure;
             }
             {
                 SubNormResidualNorm p{step.o, step.r, step.r2, L.attn_sub_norm,
                                       L.post_attention_layernorm, eps, H};
                 launch_prefill_producer(p, H, st, H, B, step.x, step.amax, s);
             }
-            const spb_sparse_linear* gu2[2] = {&L.gate_proj, &L.up_proj};
-            const int32_t* yg[3];
-            int ldg[3];
-            if (gemm_group(gu2, 2, step.x, step.y, B, s, yg, ldg) != hipSuccess)
-                return hipErrorLaunchFailure;
             {
+                const spb_sparse_linear* gu2[2] = {&L.gate_proj, &L.up_proj};
                 SegBf16Sink sink{step.gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
                                  I, 2 * I, 0.f, 0.f, 0.f};
-                launch_prefill_sink(sink, 2 * I, step.amax, yg[0], yg[1], yg[2], I, 2 * I, 2 * I,
-                                    ldg[0], ldg[1], ldg[2], B, s);
+                if (gemm_sink(gu2, 2, step.x, step.amax, sink, 2 * I, step.y, B, s) !=
+                    hipSuccess)
+                    return hipErrorLaunchFailure;
             }
             {
                 Relu2Norm p{step.gu, step.gu + I, L.ffn_sub_norm,
@@ -3414,11 +3526,11 @@ struct spb_batch_engine {
                             eps, I};
                 launch_prefill_producer(p, 2 * I, st, I, B, step.x, step.amax, s);
             }
-            if (gemm(L.down_proj, step.y[0])) return hipErrorLaunchFailure;
             {
+                const spb_sparse_linear* d1[1] = {&L.down_proj};
                 ResidualSink sink{step.r, step.r2, L.down_proj.gamma, 0.f};
-                launch_prefill_sink(sink, H, step.amax, step.y[0], step.y[0], step.y[0], H, H, H,
-                                    H, H, H, B, s);
+                if (gemm_sink(d1, 1, step.x, step.amax, sink, H, step.y, B, s) != hipSuccess)
+                    return hipErrorLaunchFailure;
             }
         }
         const int V = cfg.vocab_size, xstride = lm_head_batch_xstride(H);
@@ -3502,7 +3614,7 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(e->lm_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(lm_head_batch_lds(H))) != hipSuccess ||
-        gemm_prepare() != 0) {
+        gemm_prepare() != 0 || gemm_sink_prepare() != 0) {
         delete e;
         return launch_status(fn);
     }

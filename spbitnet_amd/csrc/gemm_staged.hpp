@@ -1,0 +1,471 @@
+// gemm_staged.hpp -- the staged 2:4 sparse-ternary GEMM kernel on the
+// int8 structured-sparse matrix cores of gfx950 (v_smfmac_i32_16x16x128_i8)
+// with an epilogue policy: the entry point spb_sparse_ternary_gemm stores the
+// int32 products (Int32Out, gemm.hip); the engines apply their per-token
+// output stages (dequantise, RoPE and KV-cache write, residual add) to the
+// products in registers (engine.hip), so no int32 buffer is written or read.
+//
+// What it computes: Y[t][r] = sum_c W[r][c] * X[t][c] (exact int32), X
+// token-major int8 [n][cols]; the reference's cuSPARSELt product D = A * B
+// (src/cusparselt_backend.cu:53-62, 83-89, 186-207) computed directly on
+// spbitnet's packed format.  The operand layouts are described in gemm.hip.
+#pragma once
+
+#include <cstdint>
+
+#include "common.hpp"
+#include "spbitnet_amd.h"
+
+namespace spb {
+
+// Raises a kernel's dynamic-LDS limit to the CU's LDS, once per device
+// (gemm.hip); false if the runtime refuses.
+bool gemm_allow_lds(const void* fn);
+
+namespace {
+
+// Up to three matrices stacked along the rows (q | k | v, gate | up), with
+// equal columns and strides: rows [0, end0) are the first, [end0, end1) the
+// second (words at meta + om1 for global row r, i.e. om1 = offset of the
+// second matrix - end0 * ms), [end1, rows) the third.  One matrix: end0 =
+// end1 = rows.
+struct GemmSegs {
+    long om1, om2, ov1, ov2;
+    int end0, end1;
+};
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+
+template <uint32_t kTable>
+__device__ __forceinline__ uint32_t gemm_bitop3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, kTable);
+}
+
+// Index word of one meta word (8 groups): nibble g = p0 | p1 << 2.
+__device__ __forceinline__ int smfmac_index(uint32_t k) {
+    const uint32_t a = k >> 1, c = k << 1;
+    const uint32_t t0 = gemm_bitop3<0x20>(a, k, 0x11111111u);  // (a & ~b) & m : ~b0 & b1
+    const uint32_t t1 = gemm_bitop3<0x02>(c, k, 0x22222222u);  // ~(a | b) & m : ~(b0 | b1)
+    const uint32_t t2 = gemm_bitop3<0xA2>(a, k, 0x44444444u);  // (a | ~b) & m : b3 | ~b2
+    const uint32_t t3 = gemm_bitop3<0xA8>(c, k, 0x88888888u);  // (a | b) & m  : b3 | b2
+    return static_cast<int>(gemm_bitop3<0xFE>(t0, t1, t2) | t3);
+}
+
+// Four compressed-value dwords (16 int8 +-1) from 16 sign bits: bit j -> byte j.
+__device__ __forceinline__ v4i smfmac_values(uint32_t s16) {
+    v4i a;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t nib = (s16 >> (4 * d)) & 0xFu;
+        const uint32_t nb = (nib * 0x00204081u) & 0x01010101u;  // bit i -> byte i (0/1)
+        // per 16-bit half: 0/1 bytes * 0xFE + 0x0101 -> 0x01 / 0xFF bytes, no carries
+        u16x2 h = __builtin_bit_cast(u16x2, nb);
+        h = h * (u16x2){0xFE, 0xFE} + (u16x2){0x0101, 0x0101};
+        a[d] = __builtin_bit_cast(int, h);
+    }
+    return a;
+}
+
+// ---------------------------------------------------------------------------
+// Staged kernel (the path for column counts that are a multiple of 256 and
+// 16-byte aligned rows).  The direct kernel above reads each lane's A words
+// and B bytes straight from memory: 4- and 16-byte pieces of 16 different
+// rows per instruction, with each K step's loads consumed at once, so its
+// time is the memory pipeline's per-request cost and latency (~20 us at
+// n=256 on 6912x2560, nearly independent of the grid size).  This kernel
+// moves whole tiles with 16-byte buffer loads of consecutive addresses into
+// LDS, double-buffered over chunks of KCP column pairs, and the waves read
+// their operands from LDS.
+//
+// Column pairs.  SMFMAC lane group q covers logical K [32q, 32q + 32) of a
+// 128-K step.  Two steps are taken over 256 columns ("a pair") such that lane
+// group q of step i reads meta word 8p + 2q + i of the pair p: the lane's two
+// steps are adjacent words, and its sign bits for both are one values word
+// (4p + q, half i).  The B operand follows: lane (token, q) of step i holds
+// columns 64(q >> 1) + 32i + 16(q & 1) + [0, 16) and the same + 128 (the
+// k-th byte of its two 16-byte halves pairs with the k-th compressed value
+// of A lane group q >> 1 and 2 + (q >> 1)).  Staging stores each lane
+// group's 32 bytes of step i adjacent in LDS.
+//
+// LDS layout per buffer (bank-conflict free for the operand reads and the
+// staging writes, as measured with SQ_LDS_BANK_CONFLICT on gfx950 for these
+// access patterns):
+//   meta   [8 KCP words][RBM rows]   (transposed; RBM = 8 or 24 mod 32)
+//   values [4 KCP words][RBV rows]   (transposed; RBV = 16 or 48 mod 64)
+//   B      [4 lane groups q][KCP pairs][TB tokens][4 units]: units 2i, 2i+1
+//          of (q, pair, token t) are lane group q's step-i bytes, unit c
+//          stored at c ^ ((t >> 2) & 3); the q-parts are 4 mod 8 units apart
+// Block: WS x KW waves.  Wave (ws, kw) owns strips ws*S .. ws*S + S - 1 and
+// all T token tiles, and takes the chunk's steps kw, kw + KW, ...; the KW
+// partial sums of a tile meet in LDS after the last chunk, and the epilogue
+// policy Epi takes each lane's four rows of one token (store4).
+constexpr int low_pow2(int x) { return x & -x; }
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int pitch_mod(int rb, int m, int r1, int r2) {  // smallest p >= rb with p % m in {r1, r2}
+    return (rb % m <= r1) ? rb - rb % m + r1 : (rb % m <= r2 ? rb - rb % m + r2 : rb - rb % m + m + r1);
+}
+constexpr int kRawBufferFlags = 0x00020000;  // gfx9 raw buffer resource word 3
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+template <int S, int T, int WS, int KW, int KCP>
+struct StagedTile {
+    static constexpr int NT = WS * KW * kWave;
+    static constexpr int RB = WS * S * 16, TB = T * 16;
+    static constexpr int RBM = pitch_mod(RB, 32, 8, 24), RBV = pitch_mod(RB, 64, 16, 48);
+    // B: lane group q of a step reads 32 bytes of its token (units c = 2i, 2i+1
+    // of its q-part); the chunk is stored as 4 q-parts of [pair][token][4 units]
+    // (unit c of token t at c ^ ((t >> 2) & 3)), the q-parts QS units apart
+    static constexpr int QS = KCP * TB * 4 + 4;
+    // staging maps: a thread owns unit column j < G of rows tr, tr + NT/G, ...
+    static constexpr int GM = cmin(low_pow2(2 * KCP), 16);
+    static constexpr int RMK = NT / GM, KRM = (RB + RMK - 1) / RMK, KJM = 2 * KCP / GM;
+    static constexpr int GV = cmin(low_pow2(KCP), 16);
+    static constexpr int RVK = NT / GV, KRV = (RB + RVK - 1) / RVK, KJV = KCP / GV;
+    // B staging: 16 threads move one token's 256-byte pair; G16 such groups
+    // take items (token t, pair p) = g + G16 r, t fastest
+    static constexpr int G16 = NT / 16, KIB = (TB * KCP + G16 - 1) / G16;
+    static_assert((TB & (TB - 1)) == 0 && (G16 & (G16 - 1)) == 0, "power-of-two staging maps");
+    static constexpr int kABytes = (8 * KCP * RBM + 4 * KCP * RBV) * 4;
+    static constexpr int kBufBytes = kABytes + 4 * QS * 16;
+    static constexpr int NSW = 2 * KCP / KW;  // steps per wave and chunk
+    static_assert((2 * KCP) % KW == 0, "KW must divide a chunk's steps");
+    static constexpr int kRedBytes = KW * WS * S * T * kWave * 16;
+    static __host__ __device__ int lds_bytes(int nch) {
+        const int b = (nch > 1 ? 2 : 1) * kBufBytes;
+        return b > kRedBytes ? b : kRedBytes;
+    }
+};
+
+template <int S, int T, int WS, int KW, int KCP, class Epi>
+__global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
+    const uint32_t* __restrict__ meta, const uint32_t* __restrict__ values,
+    const int8_t* __restrict__ X, Epi epi, int rows, int cols, int n, int ms, int vs,
+    GemmSegs segs) {
+    using P = StagedTile<S, T, WS, KW, KCP>;
+    extern __shared__ __align__(16) uint8_t gemm_smem[];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int ws = wave % WS, kw = wave / WS;
+    const int q = lane >> 4, li = lane & 15;
+    const int r0 = blockIdx.x * P::RB;
+    const int t0 = blockIdx.y * P::TB;
+    if (r0 >= segs.end0) {
+        const bool last = r0 >= segs.end1;
+        meta += last ? segs.om2 : segs.om1;
+        values += last ? segs.ov2 : segs.ov1;
+    }
+    const int npairs = cols >> 8;
+    const int nch = (npairs + KCP - 1) / KCP;
+    // Block-relative buffer resources: rows and tokens past the matrix read
+    // zeros (their results are not stored); columns past the end in the last
+    // chunk read other in-range bytes or zeros and feed only masked steps.
+    const int brows = min(rows - r0, P::RB), btoks = min(n - t0, P::TB);
+    const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(meta + static_cast<long>(r0) * ms), static_cast<short>(0),
+        brows * ms * 4, kRawBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(values + static_cast<long>(r0) * vs), static_cast<short>(0),
+        brows * vs * 4, kRawBufferFlags);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(X + static_cast<long>(t0) * cols), static_cast<short>(0),
+        btoks * cols, kRawBufferFlags);
+    const int jm = tid % P::GM, trm = tid / P::GM;
+    const int jv = tid % P::GV, trv = tid / P::GV;
+    const int gm0 = (trm * ms + 4 * jm) * 4, gv0 = (trv * vs + 4 * jv) * 4;
+    // B: thread k of a 16-group loads unit src(k) of the 256-byte pair (the
+    // group's 16 loads cover it) and stores it as (q, c) = (k >> 2, k & 3):
+    // each 8-thread half then writes 8 distinct bank groups (q-parts 4 mod 8
+    // units apart), and the reads of a 16-lane group hit 16.
+    const int gk = tid >> 4, kq = (tid & 15) >> 2, kc = tid & 3;
+    const int src16 = 16 * ((kq >> 1) * 4 + 2 * (kc >> 1) + (kq & 1) + 8 * (kc & 1));
+    const int lm0 = (4 * jm * P::RBM + trm) * 4;
+    const int lv0 = (8 * KCP * P::RBM + 4 * jv * P::RBV + trv) * 4;
+
+    u32x4v sm[P::KRM][P::KJM], sv[P::KRV][P::KJV], sb[P::KIB];
+    auto load_chunk = [&](int c) {
+        const int cm = c * 32 * KCP, cv = c * 16 * KCP, cb = c * 256 * KCP;
+#pragma unroll
+        for (int kr = 0; kr < P::KRM; ++kr)
+#pragma unroll
+            for (int kj = 0; kj < P::KJM; ++kj)
+                if (P::RMK * (kr + 1) <= P::RB || trm + kr * P::RMK < P::RB)
+                    sm[kr][kj] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rm, gm0 + kr * P::RMK * ms * 4 + kj * P::GM * 16, cm, 0);
+#pragma unroll
+        for (int kr = 0; kr < P::KRV; ++kr)
+#pragma unroll
+            for (int kj = 0; kj < P::KJV; ++kj)
+                if (P::RVK * (kr + 1) <= P::RB || trv + kr * P::RVK < P::RB)
+                    sv[kr][kj] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rv, gv0 + kr * P::RVK * vs * 4 + kj * P::GV * 16, cv, 0);
+#pragma unroll
+        for (int r = 0; r < P::KIB; ++r) {
+            const int item = gk + r * P::G16, t = item & (P::TB - 1), pr = item / P::TB;
+            if ((P::TB * KCP) % P::G16 == 0 || item < P::TB * KCP)
+                sb[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, t * cols + pr * 256 + src16, cb, 0);
+        }
+    };
+    auto store_chunk = [&](int buf) {
+        uint8_t* base = gemm_smem + buf * P::kBufBytes;
+#pragma unroll
+        for (int kr = 0; kr < P::KRM; ++kr)
+#pragma unroll
+            for (int kj = 0; kj < P::KJM; ++kj)
+                if (P::RMK * (kr + 1) <= P::RB || trm + kr * P::RMK < P::RB) {
+                    uint32_t* d = reinterpret_cast<uint32_t*>(
+                        base + lm0 + kr * P::RMK * 4 + kj * P::GM * 16 * P::RBM);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) d[e * P::RBM] = sm[kr][kj][e];
+                }
+#pragma unroll
+        for (int kr = 0; kr < P::KRV; ++kr)
+#pragma unroll
+            for (int kj = 0; kj < P::KJV; ++kj)
+                if (P::RVK * (kr + 1) <= P::RB || trv + kr * P::RVK < P::RB) {
+                    uint32_t* d = reinterpret_cast<uint32_t*>(
+                        base + lv0 + kr * P::RVK * 4 + kj * P::GV * 16 * P::RBV);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) d[e * P::RBV] = sv[kr][kj][e];
+                }
+#pragma unroll
+        for (int r = 0; r < P::KIB; ++r) {
+            const int item = gk + r * P::G16, t = item & (P::TB - 1), pr = item / P::TB;
+            if ((P::TB * KCP) % P::G16 == 0 || item < P::TB * KCP)
+                *reinterpret_cast<u32x4v*>(
+                    base + P::kABytes +
+                    (kq * P::QS + (pr * P::TB + t) * 4 + (kc ^ ((t >> 2) & 3))) * 16) = sb[r];
+        }
+    };
+
+    v4i acc[S][T];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[s][t] = (v4i){0, 0, 0, 0};
+
+    load_chunk(0);
+    store_chunk(0);
+    __syncthreads();
+    for (int c = 0; c < nch; ++c) {
+        if (c + 1 < nch) load_chunk(c + 1);  // in flight during this chunk's steps
+        const uint8_t* base = gemm_smem + (c & 1) * P::kBufBytes;
+        const uint32_t* am = reinterpret_cast<const uint32_t*>(base);
+        const uint32_t* av = am + 8 * KCP * P::RBM;
+        const u32x4v* bb = reinterpret_cast<const u32x4v*>(base + P::kABytes);
+        const int nst = 2 * min(KCP, npairs - c * KCP);  // steps in this chunk
+        uint32_t mw[P::NSW][S], vw[P::NSW][S];
+        u32x4v blo[P::NSW][T], bhi[P::NSW][T];
+        // every operand of the wave's steps is read first, then decoded and used
+#pragma unroll
+        for (int j = 0; j < P::NSW; ++j) {
+            const int stp = kw + j * KW;
+            const int pp = stp >> 1, i = stp & 1;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int r = (ws * S + s) * 16 + li;
+                mw[j][s] = am[(8 * pp + 2 * q + i) * P::RBM + r];
+                vw[j][s] = av[(4 * pp + q) * P::RBV + r];
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const int tr = t * 16 + li, sw = (tr >> 2) & 3;
+                const u32x4v* row = bb + q * P::QS + (pp * P::TB + tr) * 4;
+                blo[j][t] = row[(2 * i) ^ sw];
+                bhi[j][t] = row[(2 * i + 1) ^ sw];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < P::NSW; ++j) {
+            const int stp = kw + j * KW;
+            const bool ok = stp < nst;  // the last chunk's missing steps add zero
+            const int i = stp & 1;
+            v4i a[S];
+            int idx[S];
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                idx[s] = smfmac_index(mw[j][s]);
+                a[s] = smfmac_values(vw[j][s] >> (16 * i));
+                if (!ok) a[s] = (v4i){0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const v8i b = (v8i){(int)blo[j][t][0], (int)blo[j][t][1], (int)blo[j][t][2],
+                                    (int)blo[j][t][3], (int)bhi[j][t][0], (int)bhi[j][t][1],
+                                    (int)bhi[j][t][2], (int)bhi[j][t][3]};
+#pragma unroll
+                for (int s = 0; s < S; ++s)
+                    acc[s][t] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a[s], b, acc[s][t],
+                                                                           idx[s], 0, 0);
+            }
+        }
+        if (c + 1 < nch) store_chunk((c + 1) & 1);  // that buffer was last read a chunk ago
+        __syncthreads();
+    }
+    // split-K sum: every wave parks its partials; wave kw adds up and stores
+    // the (strip, tile) pairs e with e % KW == kw (exact integer adds)
+    if (KW > 1) {
+        v4i* red = reinterpret_cast<v4i*>(gemm_smem);
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+                red[((kw * WS + ws) * S * T + s * T + t) * kWave + lane] = acc[s][t];
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+                if ((s * T + t) % KW == kw) {
+                    v4i sum = red[(ws * S * T + s * T + t) * kWave + lane];
+#pragma unroll
+                    for (int k = 1; k < KW; ++k)
+                        sum += red[((k * WS + ws) * S * T + s * T + t) * kWave + lane];
+                    acc[s][t] = sum;
+                }
+    }
+    // lane (li, q) of tile (s, t) holds rows 16(ws S + s) + 4q .. +3 of token 16t + li
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int row = r0 + (ws * S + s) * 16 + 4 * q;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int tok = t0 + t * 16 + li;
+            if ((KW == 1 || (s * T + t) % KW == kw) && tok < n && row < rows)
+                epi.store4(tok, row, acc[s][t]);
+        }
+    }
+}
+
+bool gemm_aligned(const void* p, uintptr_t a) {
+    return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+// The staged kernel needs whole column pairs, 16-byte aligned rows and
+// 16-byte aligned base pointers.
+bool staged_ok(const void* meta, const void* values, const void* X, int cols, int ms, int vs) {
+    return cols >= 256 && cols % 256 == 0 && ms % 4 == 0 && vs % 4 == 0 &&
+           gemm_aligned(meta, 16) && gemm_aligned(values, 16) && gemm_aligned(X, 16);
+}
+
+// Staged tile per batch size (sweep on MI355X over 6912x2560, 2560x6912,
+// 2560x2560 and 640x2560 at n = 16, 32, 64, 256 against the direct kernel):
+//   n <= 16: 32 rows x 16 tokens, 8 waves splitting K 4 ways, chunks of 2560
+//            columns (a 2560-column row in one memory round trip; longer rows
+//            double-buffer 123 KB of LDS)
+//   n <= 64: 64 rows x 32 tokens, 8 waves (2 row groups x 4 K ways)
+//   n > 64 : 64 rows x 64 tokens, 8 waves (2 row groups x 4 K ways), 78 KB
+// Kernels above 64 KB of LDS need their limit raised (gemm_prepare).
+enum StagedShape { kStagedN16, kStagedN64, kStagedWide };
+StagedShape staged_shape(int n) { return n <= 16 ? kStagedN16 : (n <= 64 ? kStagedN64 : kStagedWide); }
+int staged_row_block(int n) { return n <= 16 ? 32 : 64; }
+
+template <int S, int T, int WS, int KW, int KCP, class Epi>
+const void* staged_fn() {
+    return reinterpret_cast<const void*>(&gemm_smfmac_kernel<S, T, WS, KW, KCP, Epi>);
+}
+
+template <int S, int T, int WS, int KW, int KCP, class Epi>
+int launch_staged(const uint32_t* meta, const uint32_t* values, const int8_t* X, const Epi& epi,
+                  int rows, int cols, int n, int ms, int vs, hipStream_t st, const GemmSegs& segs) {
+    using P = StagedTile<S, T, WS, KW, KCP>;
+    const int nch = (cols / 256 + KCP - 1) / KCP;
+    const int lds = P::lds_bytes(nch);
+    if (lds > 65536 &&
+        (lds > device_lds_per_cu() || !gemm_allow_lds(staged_fn<S, T, WS, KW, KCP, Epi>())))
+        return invalid("spb_sparse_ternary_gemm: %d bytes of LDS unavailable", lds);
+    const dim3 grid((rows + P::RB - 1) / P::RB, (n + P::TB - 1) / P::TB);
+    hipLaunchKernelGGL((gemm_smfmac_kernel<S, T, WS, KW, KCP, Epi>), grid, dim3(P::NT), lds, st,
+                       meta, values, X, epi, rows, cols, n, ms, vs, segs);
+    return 0;
+}
+
+// The staged launch for n tokens (the tile of staged_shape); the caller has
+// checked staged_ok.
+template <class Epi>
+int launch_staged_for(const uint32_t* meta, const uint32_t* values, const int8_t* X,
+                      const Epi& epi, int rows, int cols, int n, int ms, int vs, hipStream_t st,
+                      const GemmSegs& g) {
+    switch (staged_shape(n)) {
+        case kStagedN16:
+            return launch_staged<1, 1, 2, 4, 10>(meta, values, X, epi, rows, cols, n, ms, vs, st, g);
+        case kStagedN64:
+            return launch_staged<2, 2, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g);
+        default:
+            return launch_staged<2, 4, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g);
+    }
+}
+
+// Raises the LDS limit of the three staged tiles with epilogue Epi (0 = done).
+template <class Epi>
+int staged_prepare() {
+    return gemm_allow_lds(staged_fn<1, 1, 2, 4, 10, Epi>()) &&
+                   gemm_allow_lds(staged_fn<2, 2, 2, 4, 2, Epi>()) &&
+                   gemm_allow_lds(staged_fn<2, 4, 2, 4, 2, Epi>())
+               ? 0
+               : 1;
+}
+
+// The int32 products, token-major Y [n][rows] (the entry point's output).
+struct Int32Out {
+    int32_t* Y;
+    int rows;
+    __device__ void store4(int tok, int row, v4i acc) const {
+        *reinterpret_cast<v4i*>(Y + static_cast<long>(tok) * rows + row) = acc;
+    }
+};
+
+// Up to three stacked projections (equal columns and strides) in one
+// launch with epilogue Epi, rows of the stack in order.  Returns 1 (nothing
+// launched) when the shapes do not allow it: columns or strides differ, the
+// staged kernel's conditions fail, or a segment boundary falls inside a
+// block's row tile; 2 on a launch error, 0 when launched.
+template <class Epi>
+int gemm_stacked_epi(const spb_sparse_linear* const* segs, int nseg, const int8_t* X,
+                     const Epi& epi, int n, hipStream_t st) {
+    if (nseg < 1 || nseg > 3 || n <= 0 || (n + 15) / 16 > 65535) return 1;
+    const spb_sparse_linear& a = *segs[0];
+    int rows = 0, ends[3] = {0, 0, 0};
+    for (int i = 0; i < nseg; ++i) {
+        const spb_sparse_linear& l = *segs[i];
+        if (l.cols != a.cols || l.meta_stride != a.meta_stride ||
+            l.values_stride != a.values_stride || !l.meta || !l.values)
+            return 1;
+        rows += l.rows;
+        ends[i] = rows;
+    }
+    if (!staged_ok(a.meta, a.values, X, a.cols, a.meta_stride, a.values_stride)) return 1;
+    const int rb = staged_row_block(n);
+    GemmSegs g{0, 0, 0, 0, ends[0], nseg > 1 ? ends[1] : ends[0]};
+    if (nseg == 1) g.end0 = g.end1 = rows;
+    for (int i = 1; i < nseg; ++i) {
+        // every segment's rows must start a block, on a 16-byte boundary
+        if (ends[i - 1] % rb || !gemm_aligned(segs[i]->meta, 16) ||
+            !gemm_aligned(segs[i]->values, 16))
+            return 1;
+        const long om = (segs[i]->meta - a.meta) - static_cast<long>(ends[i - 1]) * a.meta_stride;
+        const long ov = (segs[i]->values - a.values) -
+                        static_cast<long>(ends[i - 1]) * a.values_stride;
+        if (i == 1) {
+            g.om1 = om;
+            g.ov1 = ov;
+            g.om2 = om;  // two segments: rows past end1 do not exist
+            g.ov2 = ov;
+        } else {
+            g.om2 = om;
+            g.ov2 = ov;
+        }
+    }
+    if (nseg == 2) g.end1 = rows;
+    if (launch_staged_for(a.meta, a.values, X, epi, rows, a.cols, n, a.meta_stride,
+                          a.values_stride, st, g))
+        return 2;
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // namespace
+}  // namespace spb
