@@ -1253,8 +1253,9 @@ __device__ __forceinline__ void split_weighted_v(const uint32_t (&vs)[kAttnSplit
     }
 }
 
-// The per-split work of one query (the decode kernels and the prefill kernel
-// share it): once its q (qs, float) and the split's V rows (vs, bf16) are in
+// The per-split work of one query (the bs=1 and batched decode kernels share
+// it; the prefill kernel runs the same operations on register-held K and V):
+// once its q (qs, float) and the split's V rows (vs, bf16) are in
 // LDS behind a barrier and the thread holds its quarter of K row p = tid / 4
 // (kq; quarter tid % 4), the scores, the split's softmax and the weighted V
 // sum, stored as the split's partials of heads kvh * G .. kvh * G + G - 1.
@@ -1621,7 +1622,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
 // sequence's position before loading K and V: with many sequences most
 // blocks lie past their sequence's position (splits up to max_seq), and
 // their loads would be wasted.  The per-split arithmetic is attention_split,
-// as in the bs=1 and prefill kernels.
+// as in the bs=1 kernel.
 template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attention_batch_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
