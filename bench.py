@@ -226,8 +226,8 @@ def main() -> int:
 
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the reference is "
-              "single-GPU; DESIGN.md describes how the GEMV would shard). Run with --gpus 1.",
-              file=sys.stderr)
+              "single-GPU; the GEMV would shard by rows, or by 128-column K slices with an "
+              "exact int32 all-reduce). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import numpy as np
