@@ -130,6 +130,27 @@ def test_engine_long_context_4096(gpu):
     eng.close()
 
 
+def test_engine_split_combine_logits(gpu):
+    """Steps on both sides of the 8-split boundary (position 512), logits bit
+    for bit against the oracle at every step from 500: up to 8 splits the o
+    projection's prologue folds them, past that attn_combine_kernel does
+    (GQA groups 1, 4 and 8 at head_dim 64, 4 and 8 at head_dim 128)."""
+    for nh, nkv, hd in [(8, 2, 64), (8, 8, 64), (8, 1, 64), (4, 1, 128), (8, 1, 128)]:
+        cfg = _small_config(num_hidden_layers=1, hidden_size=nh * hd, num_attention_heads=nh,
+                            num_key_value_heads=nkv, head_dim=hd, max_position_embeddings=1024)
+        print(f"split combine nh={nh} nkv={nkv} hd={hd}", flush=True)
+        model, eng, ora = _engine_pair(cfg, seed=71 + nkv + hd, max_seq=1024)
+        for i, t in enumerate(_prompt(600, cfg.vocab_size, 3 + nkv)):
+            got = eng.forward(t)
+            want_tok, want = ora.step(t)
+            if i >= 500:
+                got = got.cpu().numpy()
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+                    f"nh={nh} nkv={nkv} hd={hd} step {i}: max |diff| {np.abs(got - want).max()}"
+                assert int(np.argmax(got)) == want_tok
+        eng.close()
+
+
 def test_engine_long_context_gqa_groups(gpu):
     """Past 4 splits the o projection's prologue loads the remaining splits in
     groups: GQA groups 1, 2 and 8 with head_dim 64 and group 4 with head_dim
