@@ -1316,14 +1316,16 @@ __device__ __forceinline__ void attention_split(const uint4 (&kq)[HD / 32], floa
 // maxima, w_s = exp(m_s - M) (computed once per split here, by one thread,
 // and shared through LDS), then l and each element's sum accumulated split
 // by split; thread d writes bf16r(sum_d / l).  The element's partials of the
-// first kCombineBatch splits and the split maxima and sums are loaded
-// together, right after the position (loads of splits past it, whose
-// partials are old and cold, would hold up the live ones).
+// first NB splits and the split maxima and sums are loaded together, right
+// after the position (loads of splits past it, whose partials are old and
+// cold, would hold up the live ones).  NB: the token-step graph's splits
+// rounded up to a multiple of 8, at most kCombineBatch (a batch of loads per
+// thread no larger than the splits the graph can reach).
 constexpr int kCombineBatch = 64;
 // Token-step graphs whose attention reaches at most this many splits keep the
 // combine in the o projection's prologue; longer ones launch attn_combine_kernel.
 constexpr int kFusedCombineSplits = 8;
-template <int HD>
+template <int HD, int NB>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ pm,
                                                           const float* __restrict__ pl,
                                                           const float* __restrict__ pacc,
@@ -1339,9 +1341,9 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
     const float* mh = pm + static_cast<long>(h) * S;
     const float* lh = pl + static_cast<long>(h) * S;
     const float* ph = pacc + static_cast<long>(h) * S * HD + d;
-    float pv[kCombineBatch];
+    float pv[NB];
 #pragma unroll
-    for (int k = 0; k < kCombineBatch; ++k) pv[k] = ph[static_cast<long>(k < ns ? k : ns - 1) * HD];
+    for (int k = 0; k < NB; ++k) pv[k] = ph[static_cast<long>(k < ns ? k : ns - 1) * HD];
     const float m0 = d < ns ? mh[d] : -INFINITY;
     const float l0 = d < ns ? lh[d] : 0.0f;
     float M = m0;
@@ -1362,14 +1364,14 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
     }
     __syncthreads();
     float l = 0.0f, a = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += kCombineBatch) {
+    for (int s0 = 0; s0 < ns; s0 += NB) {
         if (s0) {
 #pragma unroll
-            for (int k = 0; k < kCombineBatch; ++k)
+            for (int k = 0; k < NB; ++k)
                 pv[k] = ph[static_cast<long>(s0 + k < ns ? s0 + k : ns - 1) * HD];
         }
 #pragma unroll
-        for (int k = 0; k < kCombineBatch; ++k) {
+        for (int k = 0; k < NB; ++k) {
             if (s0 + k < ns) {
                 const float w = wl[s0 + k];
                 l = __builtin_fmaf(w, wl[S + s0 + k], l);
@@ -2598,6 +2600,38 @@ void launch_prefill_sink(const Sink& sink, long stride, const float* amax, const
                        sink, stride, amax, y0, y1, y2, end0, end1, rows, ld0, ld1, ld2);
 }
 
+// attn_combine_kernel for a token-step graph whose attention reaches
+// `splits` splits: a load batch of the splits rounded up to 8, at most
+// kCombineBatch.
+template <int HD, int NB>
+void launch_attn_combine_nb(int nh, hipStream_t s, const float* pm, const float* pl,
+                            const float* pacc, float* comb, const EngineState* st, int S) {
+    const size_t lds = 2 * static_cast<size_t>(S) * sizeof(float);
+    hipLaunchKernelGGL((attn_combine_kernel<HD, NB>), dim3(nh), dim3(HD), lds, s, pm, pl, pacc,
+                       comb, st, S);
+}
+template <int HD>
+void launch_attn_combine_hd(int nh, int splits, hipStream_t s, const float* pm, const float* pl,
+                            const float* pacc, float* comb, const EngineState* st, int S) {
+    switch ((splits + 7) / 8) {
+    case 0: case 1: case 2: launch_attn_combine_nb<HD, 16>(nh, s, pm, pl, pacc, comb, st, S); break;
+    case 3: launch_attn_combine_nb<HD, 24>(nh, s, pm, pl, pacc, comb, st, S); break;
+    case 4: launch_attn_combine_nb<HD, 32>(nh, s, pm, pl, pacc, comb, st, S); break;
+    case 5: launch_attn_combine_nb<HD, 40>(nh, s, pm, pl, pacc, comb, st, S); break;
+    case 6: launch_attn_combine_nb<HD, 48>(nh, s, pm, pl, pacc, comb, st, S); break;
+    case 7: launch_attn_combine_nb<HD, 56>(nh, s, pm, pl, pacc, comb, st, S); break;
+    default: launch_attn_combine_nb<HD, kCombineBatch>(nh, s, pm, pl, pacc, comb, st, S); break;
+    }
+}
+void launch_attn_combine(int hd, int nh, int splits, hipStream_t s, const float* pm,
+                         const float* pl, const float* pacc, float* comb, const EngineState* st,
+                         int S) {
+    if (hd == 64)
+        launch_attn_combine_hd<64>(nh, splits, s, pm, pl, pacc, comb, st, S);
+    else
+        launch_attn_combine_hd<128>(nh, splits, s, pm, pl, pacc, comb, st, S);
+}
+
 // The first `splits` splits of S (the partials' stride stays S).
 void launch_attention(int hd, int G, int S, int splits, int nkv, hipStream_t s,
                       const uint16_t* qkv, const uint16_t* kc, const uint16_t* vc, float* pm,
@@ -2933,13 +2967,7 @@ struct spb_engine {
                     launch_projection(single_weights(L.o_proj), p, st, sink, s);
                 } else {
                     // long contexts: fold once per head, then read the result
-                    const size_t lds = 2 * static_cast<size_t>(S) * sizeof(float);
-                    if (hd == 64)
-                        hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(nh), dim3(64), lds, s,
-                                           pm, pl, pacc, comb, st, S);
-                    else
-                        hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(nh), dim3(128), lds, s,
-                                           pm, pl, pacc, comb, st, S);
+                    launch_attn_combine(hd, nh, splits, s, pm, pl, pacc, comb, st, S);
                     CombinedAttn p{comb, nh * hd};
                     launch_projection(single_weights(L.o_proj), p, st, sink, s);
                 }
