@@ -1348,8 +1348,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
     const float l0 = d < ns ? lh[d] : 0.0f;
     float M = m0;
     for (int s = d + HD; s < ns; s += HD) M = __builtin_fmaxf(M, mh[s]);
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) M = __builtin_fmaxf(M, __shfl_xor(M, off, kWave));
+    M = wave_max_tree(M);  // DPP rows and readlanes (a maximum: exact in any order)
     if (lane == 0) red[wave] = M;
     __syncthreads();
 #pragma unroll
