@@ -47,7 +47,7 @@ namespace {
 
 constexpr int kAttnSplit = 64;    // positions per attention split (one per lane)
 constexpr int kAttnThreads = 256;
-constexpr int kAttnBucketSplits = 8;  // splits per position bucket of the decode graphs
+constexpr int kAttnBucketSplits = 4;  // splits per position bucket of the decode graphs
 constexpr int kPrefillChunk = 1024;      // prompt tokens per batched-prefill pass (at most)
 constexpr long kPrefillPartialBytes = 1L << 30;  // split partials of one pass (at most)
 constexpr int kPrefillMinDefault = 16;   // prompt tokens before the last that switch to it
@@ -1319,7 +1319,7 @@ __device__ __forceinline__ void attention_split(const uint4 (&kq)[HD / 32], floa
 // first NB splits and the split maxima and sums are loaded together, right
 // after the position (loads of splits past it, whose partials are old and
 // cold, would hold up the live ones).  NB: the token-step graph's splits
-// rounded up to a multiple of 8, at most kCombineBatch (a batch of loads per
+// rounded up to a multiple of 4, at most kCombineBatch (a batch of loads per
 // thread no larger than the splits the graph can reach).
 constexpr int kCombineBatch = 64;
 // Token-step graphs whose attention reaches at most this many splits keep the
@@ -2600,8 +2600,8 @@ void launch_prefill_sink(const Sink& sink, long stride, const float* amax, const
 }
 
 // attn_combine_kernel for a token-step graph whose attention reaches
-// `splits` splits: a load batch of the splits rounded up to 8, at most
-// kCombineBatch.
+// `splits` splits: a load batch of the splits rounded up to a multiple of 4
+// (at least 12), at most kCombineBatch.
 template <int HD, int NB>
 void launch_attn_combine_nb(int nh, hipStream_t s, const float* pm, const float* pl,
                             const float* pacc, float* comb, const EngineState* st, int S) {
@@ -2612,15 +2612,24 @@ void launch_attn_combine_nb(int nh, hipStream_t s, const float* pm, const float*
 template <int HD>
 void launch_attn_combine_hd(int nh, int splits, hipStream_t s, const float* pm, const float* pl,
                             const float* pacc, float* comb, const EngineState* st, int S) {
-    switch ((splits + 7) / 8) {
-    case 0: case 1: case 2: launch_attn_combine_nb<HD, 16>(nh, s, pm, pl, pacc, comb, st, S); break;
-    case 3: launch_attn_combine_nb<HD, 24>(nh, s, pm, pl, pacc, comb, st, S); break;
-    case 4: launch_attn_combine_nb<HD, 32>(nh, s, pm, pl, pacc, comb, st, S); break;
-    case 5: launch_attn_combine_nb<HD, 40>(nh, s, pm, pl, pacc, comb, st, S); break;
-    case 6: launch_attn_combine_nb<HD, 48>(nh, s, pm, pl, pacc, comb, st, S); break;
-    case 7: launch_attn_combine_nb<HD, 56>(nh, s, pm, pl, pacc, comb, st, S); break;
-    default: launch_attn_combine_nb<HD, kCombineBatch>(nh, s, pm, pl, pacc, comb, st, S); break;
+#define SPB_COMBINE_NB(nb) launch_attn_combine_nb<HD, nb>(nh, s, pm, pl, pacc, comb, st, S); break
+    switch ((splits + 3) / 4) {
+    case 0: case 1: case 2: case 3: SPB_COMBINE_NB(12);
+    case 4: SPB_COMBINE_NB(16);
+    case 5: SPB_COMBINE_NB(20);
+    case 6: SPB_COMBINE_NB(24);
+    case 7: SPB_COMBINE_NB(28);
+    case 8: SPB_COMBINE_NB(32);
+    case 9: SPB_COMBINE_NB(36);
+    case 10: SPB_COMBINE_NB(40);
+    case 11: SPB_COMBINE_NB(44);
+    case 12: SPB_COMBINE_NB(48);
+    case 13: SPB_COMBINE_NB(52);
+    case 14: SPB_COMBINE_NB(56);
+    case 15: SPB_COMBINE_NB(60);
+    default: SPB_COMBINE_NB(kCombineBatch);
     }
+#undef SPB_COMBINE_NB
 }
 void launch_attn_combine(int hd, int nh, int splits, hipStream_t s, const float* pm,
                          const float* pl, const float* pacc, float* comb, const EngineState* st,
@@ -3190,8 +3199,9 @@ extern "C" int spb_engine_create(const spb_model_config* cfg, const spb_transfor
         delete e;
         return launch_status(fn);
     }
-    // Capture the token step once per position bucket: buckets of 8 splits
-    // (512 positions), or of S/8 splits past 64 splits (at most 8 graphs).
+    // Capture the token step once per position bucket: buckets of 4 splits
+    // (256 positions; at most 16 graphs), or of S/8 splits past 64 splits
+    // (at most 8 graphs).
     {
         const int per = e->S <= 64 ? kAttnBucketSplits : (e->S + 7) / 8;
         e->bucket_pos = per * kAttnSplit;
