@@ -1310,12 +1310,13 @@ __device__ __forceinline__ void attention_split(const uint4 (&kq)[HD / 32], floa
     split_weighted_v<HD, G>(vs, sc, hmax, hsum, jn, s, kvh, S, pm, pl, pacc);
 }
 
-// Split combine of one decode step, once per head (long contexts): block h
-// folds head h's splits 0 .. ns - 1 (those holding positions 0 .. pos) with
-// AttnCombine::combine's operations in its order: M = max of the split
-// maxima, w_s = exp(m_s - M) (computed once per split here, by one thread,
-// and shared through LDS), then l and each element's sum accumulated split
-// by split; thread d writes bf16r(sum_d / l).  The element's partials of the
+// Split combine of one decode step, once per head (long contexts): block h,
+// one wave, folds head h's splits 0 .. ns - 1 (those holding positions
+// 0 .. pos) with AttnCombine::combine's operations in its order: M = max of
+// the split maxima (a DPP wave tree, no LDS exchange), w_s = exp(m_s - M)
+// (computed once per split here, by one lane, and shared through LDS), then
+// l and each element's sum accumulated split by split; lane t writes
+// bf16r(sum_d / l) for its HD / 64 adjacent elements d.  The element's partials of the
 // first NB splits and the split maxima and sums are loaded together, right
 // after the position (loads of splits past it, whose partials are old and
 // cold, would hold up the live ones).  NB: the token-step graph's splits
@@ -1326,59 +1327,69 @@ constexpr int kCombineBatch = 64;
 // combine in the o projection's prologue; longer ones launch attn_combine_kernel.
 constexpr int kFusedCombineSplits = 8;
 template <int HD, int NB>
-__global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ pm,
-                                                          const float* __restrict__ pl,
-                                                          const float* __restrict__ pacc,
-                                                          float* __restrict__ out,
-                                                          const EngineState* __restrict__ st,
-                                                          int S) {
+__global__ __launch_bounds__(kWave) void attn_combine_kernel(const float* __restrict__ pm,
+                                                             const float* __restrict__ pl,
+                                                             const float* __restrict__ pacc,
+                                                             float* __restrict__ out,
+                                                             const EngineState* __restrict__ st,
+                                                             int S) {
+    constexpr int E = HD / kWave;  // adjacent elements per lane (one wave per head)
     extern __shared__ float wl[];  // [2][S]: w_s, l_s
-    __shared__ float red[HD / kWave];
-    const int h = blockIdx.x, d = threadIdx.x, lane = d & (kWave - 1), wave = d / kWave;
+    const int h = blockIdx.x, t = threadIdx.x;
     const int pos = state_pos(st);
     int ns = (pos >> 6) + 1;
     ns = ns < S ? ns : S;
     const float* mh = pm + static_cast<long>(h) * S;
     const float* lh = pl + static_cast<long>(h) * S;
-    const float* ph = pacc + static_cast<long>(h) * S * HD + d;
-    float pv[NB];
+    const float* ph = pacc + static_cast<long>(h) * S * HD + E * t;
+    auto load = [&](int s, float (&v)[E]) {
+        if constexpr (E == 2) {
+            const float2 x = *reinterpret_cast<const float2*>(ph + static_cast<long>(s) * HD);
+            v[0] = x.x;
+            v[1] = x.y;
+        } else {
+            v[0] = ph[static_cast<long>(s) * HD];
+        }
+    };
+    float pv[NB][E];
 #pragma unroll
-    for (int k = 0; k < NB; ++k) pv[k] = ph[static_cast<long>(k < ns ? k : ns - 1) * HD];
-    const float m0 = d < ns ? mh[d] : -INFINITY;
-    const float l0 = d < ns ? lh[d] : 0.0f;
+    for (int k = 0; k < NB; ++k) load(k < ns ? k : ns - 1, pv[k]);
+    const float m0 = t < ns ? mh[t] : -INFINITY;
+    const float l0 = t < ns ? lh[t] : 0.0f;
     float M = m0;
-    for (int s = d + HD; s < ns; s += HD) M = __builtin_fmaxf(M, mh[s]);
+    for (int s = t + kWave; s < ns; s += kWave) M = __builtin_fmaxf(M, mh[s]);
     M = wave_max_tree(M);  // DPP rows and readlanes (a maximum: exact in any order)
-    if (lane == 0) red[wave] = M;
-    __syncthreads();
-#pragma unroll
-    for (int w = 0; w < HD / kWave; ++w) M = __builtin_fmaxf(M, red[w]);
-    if (d < ns) {
-        wl[d] = exp_neg(m0 - M);
-        wl[S + d] = l0;
+    if (t < ns) {
+        wl[t] = exp_neg(m0 - M);
+        wl[S + t] = l0;
     }
-    for (int s = d + HD; s < ns; s += HD) {
+    for (int s = t + kWave; s < ns; s += kWave) {
         wl[s] = exp_neg(mh[s] - M);
         wl[S + s] = lh[s];
     }
-    __syncthreads();
-    float l = 0.0f, a = 0.0f;
+    __syncthreads();  // one wave: orders its LDS writes and reads
+    float l = 0.0f, a[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) a[e] = 0.0f;
     for (int s0 = 0; s0 < ns; s0 += NB) {
         if (s0) {
 #pragma unroll
-            for (int k = 0; k < NB; ++k)
-                pv[k] = ph[static_cast<long>(s0 + k < ns ? s0 + k : ns - 1) * HD];
+            for (int k = 0; k < NB; ++k) load(s0 + k < ns ? s0 + k : ns - 1, pv[k]);
         }
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
             if (s0 + k < ns) {
                 const float w = wl[s0 + k];
                 l = __builtin_fmaf(w, wl[S + s0 + k], l);
-                a = __builtin_fmaf(w, pv[k], a);
+#pragma unroll
+                for (int e = 0; e < E; ++e) a[e] = __builtin_fmaf(w, pv[k][e], a[e]);
             }
         }
     }
-    out[h * HD + d] = bf16r(a / l);
+    if constexpr (E == 2)
+        *reinterpret_cast<float2*>(out + h * HD + 2 * t) = make_float2(bf16r(a[0] / l), bf16r(a[1] / l));
+    else
+        out[h * HD + t] = bf16r(a[0] / l);
 }
 
 template <int HD, int G>
@@ -2606,8 +2617,8 @@ template <int HD, int NB>
 void launch_attn_combine_nb(int nh, hipStream_t s, const float* pm, const float* pl,
                             const float* pacc, float* comb, const EngineState* st, int S) {
     const size_t lds = 2 * static_cast<size_t>(S) * sizeof(float);
-    hipLaunchKernelGGL((attn_combine_kernel<HD, NB>), dim3(nh), dim3(HD), lds, s, pm, pl, pacc,
-                       comb, st, S);
+    hipLaunchKernelGGL((attn_combine_kernel<HD, NB>), dim3(nh), dim3(kWave), lds, s, pm, pl,
+                       pacc, comb, st, S);
 }
 template <int HD>
 void launch_attn_combine_hd(int nh, int splits, hipStream_t s, const float* pm, const float* pl,
