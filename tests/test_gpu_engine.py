@@ -368,3 +368,25 @@ def test_full_width_long_context(gpu):
         want = list(pool.map(lambda p: O.EngineOracle(host, 4096).generate(p, 24), [p0, p1]))
     assert got0 == want[0]
     assert got == want
+
+
+def test_engine_decode_step_runs_cross_buckets(gpu):
+    """decode_steps() replays runs of several token steps as one graph, taking
+    the position bucket of the run's last step: runs that start below and end
+    above a 256-position bucket edge, and the 512-position edge where the
+    split combine moves out of the o projection, leave the same tokens and
+    logits as the oracle's one step at a time."""
+    cfg = _small_config(num_hidden_layers=2)
+    model, eng, ora = _engine_pair(cfg, seed=53, max_seq=1024)
+    for plen, steps in ((250, 11), (507, 10)):
+        prompt = _prompt(plen, cfg.vocab_size, plen)
+        assert eng.generate(prompt, 0, stop_at_eos=False) == []
+        eng.decode_steps(steps)
+        assert eng.seq_len() == len(prompt) - 1 + steps
+        want = ora.generate(prompt, steps)
+        g = eng.forward(want[-1]).cpu().numpy()
+        wt, w = ora.step(want[-1])
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), plen
+        got = eng.generate(prompt, steps, stop_at_eos=False)
+        assert got == want[:steps], plen
+    eng.close()
