@@ -61,6 +61,18 @@ def lib():
         L.spbo_fused_bitlinear.argtypes = [_P, _P, _P, _F, _F, _I, _I, _I, _I, _P, _P]
         L.spbo_bf16_round_array.argtypes = [_P, _I, _P]
         L.spbo_planes.argtypes = [_P, _I, _P]
+        L.spbo_gen_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        L.spbo_gen_normal.restype = _F
+        L.spbo_gen_ln_u24.argtypes = [ctypes.c_uint32]
+        L.spbo_gen_ln_u24.restype = ctypes.c_double
+        L.spbo_gen_sqrt.argtypes = [ctypes.c_double]
+        L.spbo_gen_sqrt.restype = ctypes.c_double
+        L.spbo_gen_cos_u24.argtypes = [ctypes.c_uint32]
+        L.spbo_gen_cos_u24.restype = ctypes.c_double
+        L.spbo_gen_normals.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_long, _P]
+        L.spbo_gen_normal_bf16.argtypes = [ctypes.c_uint64, ctypes.c_long, _F, _P]
+        L.spbo_gen_gamma.argtypes = [_P, _I, _I]
+        L.spbo_gen_gamma.restype = _F
         _lib = L
     return _lib
 
@@ -284,6 +296,63 @@ def ref_make_test_case(seed: int, rows: int, cols: int, want_x: bool):
     x = np.zeros(cols, np.int8)
     ref().ref_make_test_case(seed, rows, cols, int(want_x), _p(w), _p(mask), _p(x))
     return w, mask, (x if want_x else None)
+
+
+# ---- random-init model generator (spb_gen.c) ----------------------------------------
+
+def gen_normals(seed: int, n: int, start: int = 0) -> np.ndarray:
+    """The generator's latent N(0,1) values normal(seed, start + i), i < n."""
+    out = np.empty(n, np.float32)
+    lib().spbo_gen_normals(seed & 0xFFFFFFFFFFFFFFFF, start, n, _p(out))
+    return out
+
+
+def gen_sparse_ternary(seed: int, rows: int, cols: int):
+    """(meta, values, gamma) of spb_generate_sparse_ternary: the latent of
+    gen_normals packed by python/convert_model.py's recipe (mask_top2,
+    kept_sign, pack above) and gamma in the device's summation order."""
+    w = gen_normals(seed, rows * cols).reshape(rows, cols)
+    mask = mask_top2(w)
+    meta, values = pack(kept_sign(w, mask), mask)
+    gamma = float(np.float32(lib().spbo_gen_gamma(_p(w), rows, cols)))
+    return meta, values, gamma
+
+
+def gen_normal_bf16(seed: int, n: int, std: float) -> np.ndarray:
+    """bf16 bits of spb_generate_normal_bf16 (the embedding)."""
+    out = np.empty(n, np.uint16)
+    lib().spbo_gen_normal_bf16(seed & 0xFFFFFFFFFFFFFFFF, n, float(std), _p(out))
+    return out
+
+
+def host_random_model(config, seed: int = 0, embed_std: float = 0.02,
+                      sub_norms: bool = True) -> dict:
+    """The host copy (the layout of spbitnet_amd.model.Model.to_host()) of
+    Model.random(config, seed, embed_std=embed_std, sub_norms=sub_norms),
+    generated on the CPU: the same per-tensor seeds, latents, packing, gamma
+    bits and bf16 embedding, so the oracle can decode the models the GPU
+    decodes without a GPU."""
+    from spbitnet_amd.weights import seed_for
+    c = config
+    H, I, kvd = c.hidden_size, c.intermediate_size, c.num_key_value_heads * c.head_dim
+    shapes = {"q_proj": (H, H), "k_proj": (kvd, H), "v_proj": (kvd, H), "o_proj": (H, H),
+              "gate_proj": (I, H), "up_proj": (I, H), "down_proj": (H, I)}
+    out = {"config": c, "layers": []}
+    for li in range(c.num_hidden_layers):
+        d = {}
+        for name in EngineOracle.PROJ:
+            rows, cols = shapes[name]
+            meta, values, gamma = gen_sparse_ternary(seed_for("model", seed, li, name), rows, cols)
+            d[name] = (meta, values, gamma, rows, cols, meta.shape[1], values.shape[1])
+        ones = np.ones(H, np.float32)
+        d["norms"] = [ones, ones.copy(), ones.copy() if sub_norms else None,
+                      np.ones(I, np.float32) if sub_norms else None]
+        out["layers"].append(d)
+    out["embed"] = gen_normal_bf16(seed_for("model", seed, "embed"), c.vocab_size * H,
+                                   embed_std).reshape(c.vocab_size, H)
+    out["lm_head"] = None
+    out["final_norm"] = np.ones(H, np.float32)
+    return out
 
 
 # ---- decode-step restatement (spb_engine_oracle.c) ---------------------------------

@@ -2398,12 +2398,99 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
-// N(0,1) float from the counter (seed, i): Box-Muller on two 24-bit uniforms.
+// N(0,1) float from the counter (seed, i): Box-Muller on two 24-bit
+// uniforms, u1 = (k + 1) / 2^24 in (0, 1] and u2 = j / 2^24 in [0, 1),
+// normal = sqrt(-2 ln u1) * cos(2 pi u2).  The logarithm, square root and
+// cosine are fixed sequences of IEEE double adds and multiplies (no library
+// call, no division, no fused multiply-add: the library is built with
+// -ffp-contract=off), so every bit of the result follows from the counter
+// alone and a host program evaluating the same sequence reproduces the
+// weights exactly.
+//   ln: u1 = m 2^(e - 24), m in (1/sqrt2, sqrt2]; ln(1 + t) = t sum_{i<=40}
+//       (-1)^i t^i / (i + 1) with t = m - 1 (exact), |t| <= 0.4143, so the
+//       truncation is below 1e-17;
+//   sqrt: y * rsqrt(y), rsqrt from a bit-pattern guess and four Newton steps
+//       r <- r (1.5 - (0.5 y r) r);
+//   cos: the octant reduction on the 24-bit integer j (exact), then the
+//       Taylor series of cos or sin to degree 20 / 21 on [0, pi/4].
+__device__ __constant__ double kGenLogC[41] = {
+    0x1.0000000000000p+0, -0x1.0000000000000p-1, 0x1.5555555555555p-2, -0x1.0000000000000p-2,
+    0x1.999999999999ap-3, -0x1.5555555555555p-3, 0x1.2492492492492p-3, -0x1.0000000000000p-3,
+    0x1.c71c71c71c71cp-4, -0x1.999999999999ap-4, 0x1.745d1745d1746p-4, -0x1.5555555555555p-4,
+    0x1.3b13b13b13b14p-4, -0x1.2492492492492p-4, 0x1.1111111111111p-4, -0x1.0000000000000p-4,
+    0x1.e1e1e1e1e1e1ep-5, -0x1.c71c71c71c71cp-5, 0x1.af286bca1af28p-5, -0x1.999999999999ap-5,
+    0x1.8618618618618p-5, -0x1.745d1745d1746p-5, 0x1.642c8590b2164p-5, -0x1.5555555555555p-5,
+    0x1.47ae147ae147bp-5, -0x1.3b13b13b13b14p-5, 0x1.2f684bda12f68p-5, -0x1.2492492492492p-5,
+    0x1.1a7b9611a7b96p-5, -0x1.1111111111111p-5, 0x1.0842108421084p-5, -0x1.0000000000000p-5,
+    0x1.f07c1f07c1f08p-6, -0x1.e1e1e1e1e1e1ep-6, 0x1.d41d41d41d41dp-6, -0x1.c71c71c71c71cp-6,
+    0x1.bacf914c1bad0p-6, -0x1.af286bca1af28p-6, 0x1.a41a41a41a41ap-6, -0x1.999999999999ap-6,
+    0x1.8f9c18f9c18fap-6};
+__device__ __constant__ double kGenCosC[11] = {
+    0x1.0000000000000p+0,  -0x1.0000000000000p-1,  0x1.5555555555555p-5,  -0x1.6c16c16c16c17p-10,
+    0x1.a01a01a01a01ap-16, -0x1.27e4fb7789f5cp-22, 0x1.1eed8eff8d898p-29, -0x1.93974a8c07c9dp-37,
+    0x1.ae7f3e733b81fp-45, -0x1.6827863b97d97p-53, 0x1.e542ba4020225p-62};
+__device__ __constant__ double kGenSinC[11] = {
+    0x1.0000000000000p+0,  -0x1.5555555555555p-3,  0x1.1111111111111p-7,  -0x1.a01a01a01a01ap-13,
+    0x1.71de3a556c734p-19, -0x1.ae64567f544e4p-26, 0x1.6124613a86d09p-33, -0x1.ae7f3e733b81fp-41,
+    0x1.952c77030ad4ap-49, -0x1.2f49b46814157p-57, 0x1.71b8ef6dcf572p-66};
+
+// ln(k / 2^24) for k in [1, 2^24]
+__device__ __forceinline__ double gen_ln_u24(uint32_t k) {
+    int e = 31 - __builtin_clz(k);  // floor(log2 k)
+    double m = static_cast<double>(k) *
+               __builtin_bit_cast(double, static_cast<uint64_t>(1023 - e) << 52);  // [1, 2)
+    if (m > 0x1.6a09e667f3bcdp+0) {  // sqrt(2)
+        m = m * 0.5;
+        e = e + 1;
+    }
+    const double t = m - 1.0;
+    double p = kGenLogC[40];
+#pragma unroll
+    for (int i = 39; i >= 0; --i) p = p * t + kGenLogC[i];
+    return static_cast<double>(e - 24) * 0x1.62e42fefa39efp-1 + t * p;
+}
+
+__device__ __forceinline__ double gen_sqrt(double y) {
+    if (!(y > 0.0)) return 0.0;
+    const uint64_t b = 0x5FE6EB50C7B537A9ull - (__builtin_bit_cast(uint64_t, y) >> 1);
+    double r = __builtin_bit_cast(double, b);
+    const double h = 0.5 * y;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r = r * (1.5 - (h * r) * r);
+    return y * r;
+}
+
+// cos(2 pi j / 2^24) for j in [0, 2^24)
+__device__ __forceinline__ double gen_cos_u24(uint32_t j) {
+    bool neg = false;
+    if (j >= (1u << 23)) j = (1u << 24) - j;  // cos(2 pi - x) = cos x
+    if (j > (1u << 22)) {                      // cos(pi - x) = -cos x
+        j = (1u << 23) - j;
+        neg = true;
+    }
+    const bool use_sin = j > (1u << 21);  // cos(pi/2 - x) = sin x
+    const double x = static_cast<double>(use_sin ? (1u << 22) - j : j) * 0x1.921fb54442d18p-22;
+    const double x2 = x * x;
+    double p;
+    if (use_sin) {
+        p = kGenSinC[10];
+#pragma unroll
+        for (int i = 9; i >= 0; --i) p = p * x2 + kGenSinC[i];
+        p = x * p;
+    } else {
+        p = kGenCosC[10];
+#pragma unroll
+        for (int i = 9; i >= 0; --i) p = p * x2 + kGenCosC[i];
+    }
+    return neg ? -p : p;
+}
+
 __device__ __forceinline__ float normal_at(uint64_t seed, uint64_t i) {
     const uint64_t z = splitmix64(seed ^ splitmix64(i));
-    const float u1 = (static_cast<float>(z >> 40) + 1.0f) * (1.0f / 16777216.0f);
-    const float u2 = static_cast<float>((z >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);
-    return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958648f * u2);
+    const uint32_t k = static_cast<uint32_t>(z >> 40) + 1u;
+    const uint32_t j = static_cast<uint32_t>((z >> 16) & 0xFFFFFFull);
+    const double r = gen_sqrt(-2.0 * gen_ln_u24(k));
+    return static_cast<float>(r * gen_cos_u24(j));
 }
 
 constexpr int kGenBlocks = 1024;

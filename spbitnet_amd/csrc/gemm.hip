@@ -198,7 +198,8 @@ int launch_smfmac_for(const uint32_t* meta, const uint32_t* values, const int8_t
                       const GemmSegs* segs) {
     if (staged_ok(meta, values, X, cols, ms, vs)) {
         const GemmSegs one{0, 0, 0, 0, rows, rows};
-        return launch_staged_for(meta, values, X, Int32Out{Y, rows}, rows, cols, n, ms, vs, st,
+        const Int32Out out{Y, rows, rows % 4 == 0 && gemm_aligned(Y, 16)};
+        return launch_staged_for(meta, values, X, out, rows, cols, n, ms, vs, st,
                                  segs ? *segs : one);
     }
     int strips = 0, tiles = 0;

@@ -163,6 +163,9 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
     // Block-relative buffer resources: rows and tokens past the matrix read
     // zeros (their results are not stored); columns past the end in the last
     // chunk read other in-range bytes or zeros and feed only masked steps.
+    // Every byte offset, the chunk's included, goes in the VGPR offset, which
+    // the hardware checks against the resource's extent (the scalar offset
+    // is not checked), so no load reads past a buffer's end.
     const int brows = min(rows - r0, P::RB), btoks = min(n - t0, P::TB);
     const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(meta + static_cast<long>(r0) * ms), static_cast<short>(0),
@@ -194,19 +197,20 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
             for (int kj = 0; kj < P::KJM; ++kj)
                 if (P::RMK * (kr + 1) <= P::RB || trm + kr * P::RMK < P::RB)
                     sm[kr][kj] = __builtin_amdgcn_raw_buffer_load_b128(
-                        rm, gm0 + kr * P::RMK * ms * 4 + kj * P::GM * 16, cm, 0);
+                        rm, gm0 + kr * P::RMK * ms * 4 + kj * P::GM * 16 + cm, 0, 0);
 #pragma unroll
         for (int kr = 0; kr < P::KRV; ++kr)
 #pragma unroll
             for (int kj = 0; kj < P::KJV; ++kj)
                 if (P::RVK * (kr + 1) <= P::RB || trv + kr * P::RVK < P::RB)
                     sv[kr][kj] = __builtin_amdgcn_raw_buffer_load_b128(
-                        rv, gv0 + kr * P::RVK * vs * 4 + kj * P::GV * 16, cv, 0);
+                        rv, gv0 + kr * P::RVK * vs * 4 + kj * P::GV * 16 + cv, 0, 0);
 #pragma unroll
         for (int r = 0; r < P::KIB; ++r) {
             const int item = gk + r * P::G16, t = item & (P::TB - 1), pr = item / P::TB;
             if ((P::TB * KCP) % P::G16 == 0 || item < P::TB * KCP)
-                sb[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, t * cols + pr * 256 + src16, cb, 0);
+                sb[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, t * cols + pr * 256 + src16 + cb,
+                                                              0, 0);
         }
     };
     auto store_chunk = [&](int buf) {
@@ -411,11 +415,24 @@ int staged_prepare() {
 }
 
 // The int32 products, token-major Y [n][rows] (the entry point's output).
+// A lane's four rows row .. row + 3 (row a multiple of 4, row < rows) are one
+// 16-byte store when every token's run of Y starts 16-byte aligned (rows a
+// multiple of 4 and Y aligned, `quads`); otherwise each row is stored on its
+// own and rows past the last are dropped, so no token's rows spill into the
+// next token's and nothing is written past Y's end.
 struct Int32Out {
     int32_t* Y;
     int rows;
+    bool quads;
     __device__ void store4(int tok, int row, v4i acc) const {
-        *reinterpret_cast<v4i*>(Y + static_cast<long>(tok) * rows + row) = acc;
+        int32_t* y = Y + static_cast<long>(tok) * rows + row;
+        if (quads) {
+            *reinterpret_cast<v4i*>(y) = acc;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (row + k < rows) y[k] = acc[k];
+        }
     }
 };
 

@@ -64,6 +64,55 @@ def test_generator_matches_host_packing(gpu):
         assert abs(g - O.absmean(w)) <= 1e-6 * O.absmean(w)
 
 
+@pytest.mark.parametrize("rows,cols,seed", [(6912, 2560, 11), (2560, 6912, 12), (33, 640, 13),
+                                            (1, 64, 14)])
+def test_generator_matches_host(gpu, rows, cols, seed):
+    """The device generator equals its host restatement (oracle/spb_gen.c) bit
+    for bit: every latent value, the packed words and the gamma bits."""
+    from spbitnet_amd import _lib
+    L = _lib.load()
+    ms, vs = cols // 32, cols // 64
+    meta = torch.empty((rows, ms), dtype=torch.int32, device="cuda")
+    values = torch.empty((rows, vs), dtype=torch.int32, device="cuda")
+    gamma = torch.zeros(1, dtype=torch.float32, device="cuda")
+    latent = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    print(f"generator vs host rows={rows} cols={cols}", flush=True)
+    _lib.check(L.spb_generate_sparse_ternary(seed, rows, cols, meta.data_ptr(), values.data_ptr(),
+                                             ms, vs, gamma.data_ptr(), latent.data_ptr(), None),
+               "generate")
+    torch.cuda.synchronize()
+    assert np.array_equal(latent.cpu().numpy().view(np.uint32).ravel(),
+                          O.gen_normals(seed, rows * cols).view(np.uint32))
+    hm, hv, hg = O.gen_sparse_ternary(seed, rows, cols)
+    assert np.array_equal(meta.cpu().numpy().view(np.uint32), hm)
+    assert np.array_equal(values.cpu().numpy().view(np.uint32), hv)
+    assert np.float32(gamma.item()).view(np.uint32) == np.float32(hg).view(np.uint32)
+
+
+def test_random_model_matches_host_model(gpu):
+    """Model.random at the 2.4B shape (the model of the golden decode tokens)
+    equals oracle.host_random_model: layers 0 and 29 word for word with their
+    gamma bits, and the whole bf16 embedding / LM head."""
+    from spbitnet_amd.model import Model, ModelConfig
+    cfg = ModelConfig.bitnet_b158_2b4t()
+    print("Model.random 2.4B vs host generator", flush=True)
+    model = Model.random(cfg, seed=2025)
+    torch.cuda.synchronize()
+    from spbitnet_amd.weights import seed_for
+    for li in (0, cfg.num_hidden_layers - 1):
+        for name in O.EngineOracle.PROJ:
+            s = getattr(model.layers[li], name)
+            hm, hv, hg = O.gen_sparse_ternary(seed_for("model", 2025, li, name), s.rows, s.cols)
+            assert np.array_equal(s.meta.cpu().numpy().view(np.uint32), hm), (li, name)
+            assert np.array_equal(s.values.cpu().numpy().view(np.uint32), hv), (li, name)
+            assert np.float32(s.gamma).view(np.uint32) == np.float32(hg).view(np.uint32)
+    emb = model.embed_tokens.view(torch.int16).cpu().numpy().view(np.uint16).ravel()
+    want = O.gen_normal_bf16(seed_for("model", 2025, "embed"), emb.size, 0.02)
+    assert np.array_equal(emb, want)
+    del model
+    torch.cuda.empty_cache()
+
+
 def _engine_pair(cfg, seed, max_seq, **kw):
     from spbitnet_amd.model import InferenceEngine, Model
     model = Model.random(cfg, seed=seed, **kw)
@@ -371,11 +420,11 @@ def test_full_width_long_context(gpu):
 
 
 def test_engine_decode_step_runs_cross_buckets(gpu):
-    """decode_steps() replays runs of several token steps as one graph, taking
-    the position bucket of the run's last step: runs that start below and end
-    above a 256-position bucket edge, and the 512-position edge where the
-    split combine moves out of the o projection, leave the same tokens and
-    logits as the oracle's one step at a time."""
+    """decode_steps() replays one token-step graph per step, each chosen by the
+    bucket of its own position: runs that cross a 256-position bucket edge,
+    and the 512-position edge where the split combine moves out of the o
+    projection, leave the same tokens and logits as the oracle's one step at
+    a time."""
     cfg = _small_config(num_hidden_layers=2)
     model, eng, ora = _engine_pair(cfg, seed=53, max_seq=1024)
     for plen, steps in ((250, 11), (507, 10)):

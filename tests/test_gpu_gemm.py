@@ -115,3 +115,41 @@ def test_gemm_padded_strides(gpu, pad_m, pad_v, n):
                               values.shape[1])
     torch.cuda.synchronize()
     assert (Y.cpu().numpy() == expected(L, X)).all()
+
+
+@pytest.mark.parametrize("rows,cols,n", [(333, 512, 5), (6, 256, 17), (2561, 2560, 100),
+                                         (18, 768, 64), (1001, 2816, 33)])
+def test_gemm_staged_rows_not_multiple_of_4(gpu, rows, cols, n):
+    """The staged matrix-core kernel (kernel id 2) on row counts that are not a
+    multiple of 4: each token's rows are stored one by one, so no token's
+    rows overwrite the next token's and nothing lands past Y's end (checked
+    with guard words after Y)."""
+    L = W.random_layer(rows, cols, W.seed_for("gemm-rows4", rows, cols, n))
+    X = np.random.default_rng(rows + 3 * cols + n).integers(-128, 128, (n, cols)).astype(np.int8)
+    m_dev, v_dev, X_dev = dev_u32(L.meta, gpu), dev_u32(L.values, gpu), dev(X, gpu)
+    assert K.gemm_kernel_id(m_dev, v_dev, X_dev, rows, cols, n, L.meta_stride,
+                            L.values_stride) == 2
+    guard = 64
+    buf = torch.full((n * rows + guard,), -7, dtype=torch.int32, device=gpu)
+    K.sparse_ternary_gemm_gpu(m_dev, v_dev, X_dev, buf, rows, cols, n, L.meta_stride,
+                              L.values_stride)
+    torch.cuda.synchronize()
+    out = buf.cpu().numpy()
+    assert (out[:n * rows].reshape(n, rows) == expected(L, X)).all()
+    assert (out[n * rows:] == -7).all()
+
+
+def test_gemm_staged_unaligned_output(gpu):
+    """Y that starts 4 bytes past a 16-byte boundary (rows a multiple of 4):
+    the staged kernel stores rows one by one instead of 16-byte quads."""
+    rows, cols, n = 256, 512, 20
+    L = W.random_layer(rows, cols, W.seed_for("gemm-unaligned-y"))
+    X = np.random.default_rng(91).integers(-128, 128, (n, cols)).astype(np.int8)
+    buf = torch.full((n * rows + 8,), -7, dtype=torch.int32, device=gpu)
+    Y = buf[1:1 + n * rows]
+    K.sparse_ternary_gemm_gpu(dev_u32(L.meta, gpu), dev_u32(L.values, gpu), dev(X, gpu), Y,
+                              rows, cols, n, L.meta_stride, L.values_stride)
+    torch.cuda.synchronize()
+    out = buf.cpu().numpy()
+    assert out[0] == -7 and (out[1 + n * rows:] == -7).all()
+    assert (out[1:1 + n * rows].reshape(n, rows) == expected(L, X)).all()

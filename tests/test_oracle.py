@@ -286,3 +286,78 @@ def test_planes_round_trip_and_identity():
     bits = ((x.astype(np.int64)[None, :] & 0xFF) >> np.arange(8)[:, None]) & 1
     c = np.array([1, 2, 4, 8, 16, 32, 64, -128])
     assert (dense.astype(np.int64) @ (c @ bits) == O.gemv(meta, values, x, 8, 64)).all()
+
+
+# ---- the random-init model generator's host restatement (spb_gen.c) ----------
+
+def test_generator_ln_sqrt_cos_match_libm():
+    """The add/multiply-only ln, sqrt and cos of the generator against libm
+    (float64), over the generator's whole input ranges' edges and random
+    points: within 1e-14 relative (ln, sqrt) and 1e-15 absolute (cos)."""
+    import math
+    L = O.lib()
+    rng = np.random.default_rng(5)
+    ks = [1, 2, 3, 1 << 23, (1 << 23) + 1, (1 << 24) - 1, 1 << 24, 11863283, 11863284]
+    ks += [int(k) for k in rng.integers(1, (1 << 24) + 1, 20000)]
+    for k in ks:
+        want = math.log(k / 2.0 ** 24)
+        got = L.spbo_gen_ln_u24(k)
+        assert abs(got - want) <= 1e-14 * abs(want), k
+    js = [0, 1, (1 << 21) - 1, 1 << 21, (1 << 21) + 1, 1 << 22, (1 << 22) + 1, 1 << 23,
+          (1 << 23) + 1, (1 << 24) - 1] + [int(j) for j in rng.integers(0, 1 << 24, 20000)]
+    for j in js:
+        assert abs(L.spbo_gen_cos_u24(j) - math.cos(2 * math.pi * j / 2.0 ** 24)) <= 1e-15, j
+    for y in [0.0, 1e-8, 0.5, 1.0, 2.0, 33.27] + list(rng.uniform(0, 34, 5000)):
+        want = math.sqrt(y)
+        assert abs(L.spbo_gen_sqrt(y) - want) <= 1e-15 * max(want, 1e-300), y
+    # u1 = 1 gives radius 0; cos at the octant edges is exact where it must be
+    assert L.spbo_gen_ln_u24(1 << 24) == 0.0 and L.spbo_gen_sqrt(0.0) == 0.0
+    assert L.spbo_gen_cos_u24(0) == 1.0 and L.spbo_gen_cos_u24(1 << 23) == -1.0
+
+
+def test_generator_normals_are_standard_normal_and_deterministic():
+    x = O.gen_normals(2025, 4_000_000)
+    assert np.array_equal(x, O.gen_normals(2025, 4_000_000))
+    assert np.array_equal(x[1000:1100], O.gen_normals(2025, 100, start=1000))
+    assert abs(x.mean()) < 3e-3 and abs(x.std() - 1) < 2e-3
+    assert abs(np.abs(x).mean() - np.sqrt(2 / np.pi)) < 2e-3
+    assert abs((x.astype(np.float64) ** 4).mean() - 3) < 0.03
+    # every float equals the float64 Box-Muller value rounded once (a wrong
+    # branch of the cos reduction or a dropped log term would not)
+    import math
+    z = O.gen_normals(77, 2000)
+    M = 0xFFFFFFFFFFFFFFFF
+
+    def sm(v):
+        v = (v + 0x9E3779B97F4A7C15) & M
+        v = ((v ^ (v >> 30)) * 0xBF58476D1CE4E5B9) & M
+        v = ((v ^ (v >> 27)) * 0x94D049BB133111EB) & M
+        return v ^ (v >> 31)
+
+    for i in range(2000):
+        h = sm(77 ^ sm(i))
+        u1 = ((h >> 40) + 1) / 2.0 ** 24
+        u2 = ((h >> 16) & 0xFFFFFF) / 2.0 ** 24
+        v = math.sqrt(-2 * math.log(u1)) * math.cos(2 * math.pi * u2)
+        assert abs(float(z[i]) - v) <= 2 ** -23 * abs(v) + 1e-12, i
+
+
+def test_generator_packing_equals_host_packer_and_gamma():
+    """gen_sparse_ternary packs its latent exactly as the library's host
+    packer (make_layer_from_latent) does, and its gamma (the device's double
+    summation order) equals mean |W| to float rounding."""
+    from spbitnet_amd import weights as Wt
+    for rows, cols, seed in [(64, 256, 1), (33, 640, 2), (1, 64, 3), (300, 2560, 4)]:
+        meta, values, gamma = O.gen_sparse_ternary(seed, rows, cols)
+        w = O.gen_normals(seed, rows * cols).reshape(rows, cols)
+        want = Wt.make_layer_from_latent(w)
+        assert np.array_equal(meta, want.meta) and np.array_equal(values, want.values)
+        exact = float(np.abs(w.astype(np.float64)).sum() / (rows * cols))
+        assert abs(gamma - exact) <= 2 ** -23 * exact
+
+
+def test_generator_bf16_embedding():
+    n, std = 5000, 0.02
+    got = O.gen_normal_bf16(99, n, std)
+    want = O.to_bf16_bits(O.gen_normals(99, n) * np.float32(std))
+    assert np.array_equal(got, want)
