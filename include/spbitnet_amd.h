@@ -170,6 +170,56 @@ int spb_sparse_ternary_gemm_kernel_id(const uint32_t* meta, const uint32_t* valu
                                       const int8_t* X, int rows, int cols, int n,
                                       int meta_row_stride, int values_row_stride);
 
+/* ---- 2:4 structured-sparse int8 GEMM (the cuSPARSELt backend) ------------
+ * Replaces spbitnet::CuSparseLtGemm (reference include/spbitnet/
+ * cusparselt_backend.h:28-77, src/cusparselt_backend.cu:38-219): a dense
+ * int8 weight matrix A [m][k] (row-major; any int8 values) is pruned to 2:4
+ * along k and compressed once (prepare), then D = A_pruned * B runs on the
+ * int8 sparse matrix cores (execute).  Pruning keeps, in every group of
+ * four columns, the two largest |a| (on equal magnitudes the higher index);
+ * a group with at most two non-zeros is kept whole, so a matrix already in
+ * 2:4 form is unchanged (the reference uses cuSPARSELt's STRIP rule, which
+ * is not specified there).  The compressed operand is this build's own
+ * tile-ordered layout (the library's internal format in the reference):
+ * callers size it with spb_sparse_i8_compressed_size and treat it as
+ * opaque.  k must be a multiple of 4; m * k < 2^31.  Nothing allocates. */
+
+/* Bytes of the compressed operand of an m x k matrix (the size query of
+ * cusparseLtSpMMACompressedSize, src/cusparselt_backend.cu:140-146);
+ * -1 for a rejected shape (k % 4 != 0, negative, m * k >= 2^31). */
+long spb_sparse_i8_compressed_size(int m, int k);
+
+/* CuSparseLtGemm::prepare (src/cusparselt_backend.cu:107-166): prune A and
+ * write the compressed operand; `pruned` (nullable) receives the pruned
+ * dense matrix [m][k].  A and pruned 4-byte aligned, compressed 16-byte
+ * aligned. */
+int spb_sparse_i8_prune_compress(const int8_t* A, int8_t* pruned, void* compressed, int m, int k,
+                                 spb_stream_t stream);
+
+/* cusparseLtSpMMAPruneCheck as prepare uses it (src/cusparselt_backend.cu:
+ * 123-136): *d_invalid (device int) receives the number of groups of A with
+ * more than two non-zeros (0 = A is in 2:4 form). */
+int spb_sparse_i8_prune_check(const int8_t* A, int m, int k, int* d_invalid, spb_stream_t stream);
+
+/* CuSparseLtGemm::get_pruned_weights (src/cusparselt_backend.cu:209-217):
+ * the pruned dense matrix [m][k] from the compressed operand.  out 4-byte
+ * aligned. */
+int spb_sparse_i8_decompress(const void* compressed, int8_t* out, int m, int k,
+                             spb_stream_t stream);
+
+/* CuSparseLtGemm::execute (src/cusparselt_backend.cu:173-207):
+ * D = A_pruned * B with exact int32 accumulation; B int8 [k x n]
+ * column-major (= [n][k], token-major), D int32 [m x n] column-major
+ * (= [n][m]).  Any n >= 1 (the reference requires n >= 16,
+ * src/cusparselt_backend.cu:41-45).  Runs on v_smfmac_i32_16x16x128_i8 when
+ * k % 16 == 0 and B is 16-byte aligned, else on a general kernel. */
+int spb_sparse_i8_gemm(const void* compressed, const int8_t* B, int32_t* D, int m, int k, int n,
+                       spb_stream_t stream);
+
+/* Which kernel spb_sparse_i8_gemm would run: 1 the matrix-core kernel,
+ * 0 the general kernel.  Host-only query; no reference counterpart. */
+int spb_sparse_i8_gemm_kernel_id(const void* compressed, const int8_t* B, int m, int k, int n);
+
 /* ---- Bit-plane activation layout -------------------------------------------
  * No reference counterpart: an activation layout of this build.  An int8
  * vector of `cols` columns is stored as 8 * ceil(cols/32) uint32 words;

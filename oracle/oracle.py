@@ -61,6 +61,8 @@ def lib():
         L.spbo_fused_bitlinear.argtypes = [_P, _P, _P, _F, _F, _I, _I, _I, _I, _P, _P]
         L.spbo_bf16_round_array.argtypes = [_P, _I, _P]
         L.spbo_planes.argtypes = [_P, _I, _P]
+        L.spbo_prune24_i8.argtypes = [_P, _I, _I, _P]
+        L.spbo_int8_gemm.argtypes = [_P, _P, _P, _I, _I, _I]
         L.spbo_gen_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
         L.spbo_gen_normal.restype = _F
         L.spbo_gen_ln_u24.argtypes = [ctypes.c_uint32]
@@ -296,6 +298,30 @@ def ref_make_test_case(seed: int, rows: int, cols: int, want_x: bool):
     x = np.zeros(cols, np.int8)
     ref().ref_make_test_case(seed, rows, cols, int(want_x), _p(w), _p(mask), _p(x))
     return w, mask, (x if want_x else None)
+
+
+# ---- the structured-sparse int8 GEMM (the cuSPARSELt backend) -------------------------
+
+def prune24_i8(A: np.ndarray) -> np.ndarray:
+    """The build's 2:4 pruning of a dense int8 [m][k] matrix along k (see
+    spbo_prune24_i8; the reference's cuSPARSELt STRIP rule is unspecified)."""
+    A = np.ascontiguousarray(A, dtype=np.int8)
+    m, k = A.shape
+    out = np.zeros_like(A)
+    lib().spbo_prune24_i8(_p(A), m, k, _p(out))
+    return out
+
+
+def int8_gemm(A: np.ndarray, B: np.ndarray) -> np.ndarray:
+    """cpu_int8_gemm (tests/test_cusparselt.cu:16-28): A int8 [m][k], B int8
+    [n][k] (column-major [k x n]); returns D int32 [n][m] (column-major [m x n])."""
+    A = np.ascontiguousarray(A, dtype=np.int8)
+    B = np.ascontiguousarray(B, dtype=np.int8)
+    m, k = A.shape
+    n = B.shape[0]
+    D = np.zeros((n, m), np.int32)
+    lib().spbo_int8_gemm(_p(A), _p(B), _p(D), m, k, n)
+    return D
 
 
 # ---- random-init model generator (spb_gen.c) ----------------------------------------

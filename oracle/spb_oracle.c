@@ -317,3 +317,44 @@ void spbo_planes(const int8_t* x, int cols, uint32_t* planes) {
             planes[(c / 32) * 8 + b] |= ((byte >> b) & 1u) << (c % 32);
     }
 }
+
+/*
+ * 2:4 pruning of a dense int8 matrix A [m][k] along k, the structured-sparse
+ * int8 GEMM's prepare (the cuSPARSELt backend, src/cusparselt_backend.cu:
+ * 107-166).  The reference leaves the selection to cuSPARSELt's STRIP rule,
+ * which it does not specify (its test only checks the 2:4 property and the
+ * value range, tests/test_cusparselt.cu:68-117); the build's rule is the one
+ * of spbo_mask_top2 on |a|: keep the two largest |a| of each group of four,
+ * on equal magnitudes the higher index.  out [m][k] receives the kept
+ * values and zeros.
+ */
+void spbo_prune24_i8(const int8_t* A, int m, int k, int8_t* out) {
+    for (long r = 0; r < m; ++r)
+        for (int g = 0; g < k / 4; ++g) {
+            const int8_t* p = A + r * k + 4 * g;
+            int8_t* o = out + r * k + 4 * g;
+            for (int i = 0; i < 4; ++i) {
+                int beaten_by = 0;
+                for (int j = 0; j < 4; ++j) {
+                    if (j == i) continue;
+                    const int ai = abs((int)p[i]), aj = abs((int)p[j]);
+                    if (aj > ai || (aj == ai && j > i)) ++beaten_by;
+                }
+                o[i] = beaten_by < 2 ? p[i] : 0;
+            }
+        }
+}
+
+/*
+ * cpu_int8_gemm (tests/test_cusparselt.cu:16-28): D = A * B in int32, with
+ * A [m][k] row-major and B, D in the column-major layouts the backend takes
+ * (B [k x n] = [n][k], D [m x n] = [n][m], src/cusparselt_backend.cu:53-78).
+ */
+void spbo_int8_gemm(const int8_t* A, const int8_t* B, int32_t* D, int m, int k, int n) {
+    for (long t = 0; t < n; ++t)
+        for (long r = 0; r < m; ++r) {
+            int32_t s = 0;
+            for (int j = 0; j < k; ++j) s += (int32_t)A[r * k + j] * (int32_t)B[t * k + j];
+            D[t * m + r] = s;
+        }
+}

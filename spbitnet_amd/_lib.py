@@ -93,9 +93,17 @@ SIGNATURES = {
     "spb_model_info": [_P, _P, _P, _P, _P, _P, _P],
     "spb_generate_sparse_ternary": [ctypes.c_uint64, _I, _I, _P, _P, _I, _I, _P, _P, _P],
     "spb_generate_normal_bf16": [ctypes.c_uint64, ctypes.c_long, _F, _P, _P],
+    # 2:4 structured-sparse int8 GEMM (the cuSPARSELt backend)
+    "spb_sparse_i8_compressed_size": [_I, _I],
+    "spb_sparse_i8_prune_compress": [_P, _P, _P, _I, _I, _P],
+    "spb_sparse_i8_prune_check": [_P, _I, _I, _P, _P],
+    "spb_sparse_i8_decompress": [_P, _P, _I, _I, _P],
+    "spb_sparse_i8_gemm": [_P, _P, _P, _I, _I, _I, _P],
+    "spb_sparse_i8_gemm_kernel_id": [_P, _P, _I, _I, _I],
 }
 _RESTYPES = {"spb_last_error_string": ctypes.c_char_p,
-             "spb_bitlinear_workspace_size": ctypes.c_size_t}
+             "spb_bitlinear_workspace_size": ctypes.c_size_t,
+             "spb_sparse_i8_compressed_size": ctypes.c_long}
 
 
 class SparseLinearC(ctypes.Structure):

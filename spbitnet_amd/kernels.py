@@ -156,6 +156,93 @@ def gemm_kernel_id(meta, values, X, rows, cols, n, meta_row_stride, values_row_s
         values_row_stride)
 
 
+# ---- 2:4 structured-sparse int8 GEMM (the cuSPARSELt backend) ---------------
+
+def sparse_i8_compressed_size(m: int, k: int) -> int:
+    """Bytes of the compressed operand of an m x k int8 matrix (the size query
+    of cusparseLtSpMMACompressedSize, reference src/cusparselt_backend.cu:140-146)."""
+    L = _lib.load()
+    n = L.spb_sparse_i8_compressed_size(m, k)
+    if n < 0:
+        _lib.check(1, "sparse_i8_compressed_size")
+    return int(n)
+
+
+def sparse_i8_prune_check(d_weights, m: int, k: int, stream=None) -> int:
+    """Groups of the int8 [m][k] matrix with more than two non-zeros
+    (0 = already 2:4), cusparseLtSpMMAPruneCheck as prepare uses it
+    (reference src/cusparselt_backend.cu:123-136)."""
+    pa = _dev(d_weights, "d_weights", torch.int8, m * k)
+    res = torch.empty(1, dtype=torch.int32, device=d_weights.device)
+    _lib.check(_lib.load().spb_sparse_i8_prune_check(pa, m, k, res.data_ptr(),
+                                                       _stream_ptr(stream)),
+               "sparse_i8_prune_check")
+    return int(res.item())
+
+
+class CuSparseLtGemm:
+    """CuSparseLtGemm (reference include/spbitnet/cusparselt_backend.h:28-77,
+    src/cusparselt_backend.cu:38-219): D[m,n] = A_pruned[m,k] * B[k,n] with
+    int32 accumulation on the int8 sparse matrix cores.
+
+    prepare(d_weights) prunes a device int8 [m][k] row-major matrix (any int8
+    values, k a multiple of 4) to 2:4 along k -- the two largest |a| of each
+    group of four, on equal magnitudes the higher index; groups with at most
+    two non-zeros are kept whole -- and compresses it into a device buffer
+    this object owns.  execute(d_B, d_D) takes B int8 [k x n] column-major
+    (a [n][k] tensor) and writes D int32 [m x n] column-major (a [n][m]
+    tensor).  Any n >= 1 (the reference needs n >= 16)."""
+
+    def __init__(self, m: int, k: int, n: int, device="cuda"):
+        if n < 1:
+            raise ValueError("n must be >= 1")
+        self._m, self._k, self._n = m, k, n
+        size = sparse_i8_compressed_size(m, k)
+        self._comp = torch.empty(max(size, 16), dtype=torch.uint8, device=device)
+        self._prepared = False
+
+    def m(self) -> int:
+        return self._m
+
+    def k(self) -> int:
+        return self._k
+
+    def n(self) -> int:
+        return self._n
+
+    def prepare(self, d_weights, stream=None) -> None:
+        """Prune to 2:4 and compress (src/cusparselt_backend.cu:107-166)."""
+        pa = _dev(d_weights, "d_weights", torch.int8, self._m * self._k)
+        _lib.check(_lib.load().spb_sparse_i8_prune_compress(
+            pa, None, self._comp.data_ptr(), self._m, self._k, _stream_ptr(stream)),
+            "CuSparseLtGemm.prepare")
+        self._prepared = True
+
+    def execute(self, d_B, d_D, stream=None) -> None:
+        """D = A_pruned * B (src/cusparselt_backend.cu:173-207)."""
+        if not self._prepared:
+            raise RuntimeError("CuSparseLtGemm.execute() called before prepare()")
+        pb = _dev(d_B, "d_B", torch.int8, self._n * self._k)
+        pd = _dev(d_D, "d_D", torch.int32, self._n * self._m)
+        _lib.check(_lib.load().spb_sparse_i8_gemm(self._comp.data_ptr(), pb, pd, self._m,
+                                                    self._k, self._n, _stream_ptr(stream)),
+                   "CuSparseLtGemm.execute")
+
+    def get_pruned_weights(self, d_out, stream=None) -> None:
+        """The pruned dense int8 [m][k] matrix (src/cusparselt_backend.cu:209-217)."""
+        if not self._prepared:
+            raise RuntimeError("CuSparseLtGemm.get_pruned_weights(): not prepared")
+        po = _dev(d_out, "d_out", torch.int8, self._m * self._k)
+        _lib.check(_lib.load().spb_sparse_i8_decompress(self._comp.data_ptr(), po, self._m,
+                                                          self._k, _stream_ptr(stream)),
+                   "CuSparseLtGemm.get_pruned_weights")
+
+    def kernel_id(self, d_B) -> int:
+        """1 when execute runs the matrix-core kernel for d_B, 0 the general one."""
+        return _lib.load().spb_sparse_i8_gemm_kernel_id(self._comp.data_ptr(), d_B.data_ptr(),
+                                                        self._m, self._k, self._n)
+
+
 # ---- bit-plane activation layout (no reference counterpart) -----------------
 
 def planes_words(cols: int) -> int:

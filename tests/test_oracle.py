@@ -361,3 +361,64 @@ def test_generator_bf16_embedding():
     got = O.gen_normal_bf16(99, n, std)
     want = O.to_bf16_bits(O.gen_normals(99, n) * np.float32(std))
     assert np.array_equal(got, want)
+
+
+# ---- structured-sparse int8 GEMM (the cuSPARSELt backend) --------------------
+
+def _prune_by_stable_argsort(A):
+    """Independent statement of the pruning rule: np.argsort(|a|, kind='stable')
+    ascending per group and keep the last two (python/convert_model.py:88-119's
+    formulation, where the later index sorts later among equal magnitudes)."""
+    m, k = A.shape
+    g = A.reshape(m, k // 4, 4).astype(np.int64)
+    order = np.argsort(np.abs(g), axis=-1, kind="stable")
+    keep = np.zeros(g.shape, bool)
+    np.put_along_axis(keep, order[..., 2:], True, axis=-1)
+    return np.where(keep, g, 0).reshape(m, k).astype(np.int8)
+
+
+def test_prune24_i8_brute_force_and_argsort():
+    vals = np.array(list(itertools.product(range(-2, 3), repeat=4)), np.int8).reshape(1, -1)
+    assert np.array_equal(O.prune24_i8(vals), _prune_by_stable_argsort(vals))
+    rng = np.random.default_rng(3)
+    A = rng.integers(-128, 128, (37, 256)).astype(np.int8)
+    A[:, ::7] = -128  # the magnitude 128 only -128 has
+    assert np.array_equal(O.prune24_i8(A), _prune_by_stable_argsort(A))
+    T = rng.integers(-1, 2, (64, 256)).astype(np.int8)  # the reference test's {-1,0,1}
+    assert np.array_equal(O.prune24_i8(T), _prune_by_stable_argsort(T))
+
+
+def test_prune24_i8_properties():
+    rng = np.random.default_rng(4)
+    A = rng.integers(-128, 128, (50, 512)).astype(np.int8)
+    P = O.prune24_i8(A)
+    g = P.reshape(50, -1, 4)
+    assert ((g != 0).sum(-1) <= 2).all()
+    assert ((P == 0) | (P == A)).all()                      # kept values come from A
+    assert np.array_equal(O.prune24_i8(P), P)               # idempotent
+    # groups with at most two non-zeros are kept whole
+    B = A.reshape(50, -1, 4).copy()
+    B[..., 1] = 0
+    B[..., 3] = 0
+    B = B.reshape(50, 512)
+    assert np.array_equal(O.prune24_i8(B), B)
+    # the kept pair carries the two largest magnitudes of its group
+    ga = np.abs(A.reshape(50, -1, 4).astype(np.int32))
+    top2 = np.sort(ga, -1)[..., 2:].sum(-1)
+    assert np.array_equal(np.abs(g.astype(np.int32)).sum(-1), top2)
+
+
+def test_int8_gemm_closed_forms():
+    rng = np.random.default_rng(8)
+    m, k, n = 33, 260, 19
+    A = rng.integers(-128, 128, (m, k)).astype(np.int8)
+    B = rng.integers(-128, 128, (n, k)).astype(np.int8)
+    D = O.int8_gemm(A, B)
+    assert np.array_equal(D, (B.astype(np.float64) @ A.astype(np.float64).T).astype(np.int32))
+    E = np.zeros((k, k), np.int8)
+    np.fill_diagonal(E, 1)
+    assert np.array_equal(O.int8_gemm(A, E), A.T.astype(np.int32))   # B = e_j reads column j
+    ones = np.ones((1, k), np.int8)
+    assert np.array_equal(O.int8_gemm(A, ones)[0], A.astype(np.int32).sum(1))
+    ext = np.full((1, 4096), -128, np.int8)  # |sum| = 2^26: int32, no overflow
+    assert O.int8_gemm(ext, ext)[0, 0] == 128 * 128 * 4096
