@@ -25,8 +25,9 @@ and under "detail":
   protocol_b2b     BASELINE's protocol literally: 160 distinct copies of each
                    FFN shape as 160 separate launches in one HIP graph (one
                    serial chain, and four independent chains)
-  mall_resident    48 stacked copies (159 MB, below the 256 MB Infinity
-                   Cache) re-streamed back to back
+  mall_resident    48 and 24 stacked copies (160 / 80 MB, below the 256 MB
+                   Infinity Cache) re-streamed back to back, with the
+                   non-temporal and the default load policy
   shapes           every config 0/1/4 shape: one cold launch (caches flushed
                    by a 1 GiB write) and warm launches back to back from a
                    graph (the 1-4 MB matrix stays in the caches)
@@ -120,8 +121,30 @@ def host_info() -> dict:
     except (OSError, subprocess.SubprocessError):
         pass
     import torch
-    return {"nproc": os.cpu_count(), "lscpu_model": model,
-            "torch_threads": torch.get_num_threads()}
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
+    quota = None  # CPUs the cgroup's CPU quota allows (cgroup v2 cpu.max, else v1)
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()[:2]
+        if q != "max":
+            quota = int(q) / int(per)
+    except (OSError, ValueError):
+        try:
+            with open("/sys/fs/cgroup/cpu/cpu.cfs_quota_us") as f:
+                q = int(f.read())
+            with open("/sys/fs/cgroup/cpu/cpu.cfs_period_us") as f:
+                per = int(f.read())
+            if q > 0:
+                quota = q / per
+        except (OSError, ValueError):
+            pass
+    usable = affinity or os.cpu_count() or 1
+    if quota is not None:
+        usable = max(1, min(usable, int(quota)))
+    return {"nproc": os.cpu_count(), "sched_affinity_cpus": affinity,
+            "cgroup_cpu_quota": None if quota is None else round(quota, 2),
+            "usable_cores": usable, "lscpu_model": model,
+            "torch_threads_default": torch.get_num_threads()}
 
 
 def golden_decode():
@@ -199,10 +222,12 @@ def main() -> int:
     ap.add_argument("--no-stepwise-prefill", action="store_true",
                     help="config 4: skip timing the prefill as one decode step per token")
     ap.add_argument("--only-batch-decode", action="store_true",
-                    help="profiling: run only the config-4 batched decode (no JSON line)")
+                    help="profiling: run only the config-4 batched decode and print its results")
     ap.add_argument("--only-mall-resident", action="store_true",
                     help="profiling: run only the Infinity-Cache-resident GEMV protocol "
                          "(for a rocprofv3 FETCH_SIZE pass) and print its timings")
+    ap.add_argument("--only-gemm", action="store_true",
+                    help="profiling: run only the config-2 batched GEMMs and print their timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB once (known bytes, for scaling rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE) and exit")
@@ -240,7 +265,7 @@ def main() -> int:
     dev, stream, log, ev = B.dev, B.stream, B.log, B.ev
 
     if args.only_batch_decode:
-        decode_runs(B, args, batch_only=True)
+        print(json.dumps(decode_runs(B, args, batch_only=True)), flush=True)
         return 0
 
     log("generating weights")
@@ -266,6 +291,9 @@ def main() -> int:
 
     if args.only_mall_resident:
         print(json.dumps(mall_resident(B, base, dev_base, d_x, want)), flush=True)
+        return 0
+    if args.only_gemm:
+        print(json.dumps(gemm_config2(B, base, dev_base, W, K)), flush=True)
         return 0
 
     # ---- the timed step: streamed, one launch per shape over stacked copies
@@ -473,37 +501,55 @@ def protocol_b2b(B, base, dev_base, d_x, want, copies=160):
     return res
 
 
-def mall_resident(B, base, dev_base, d_x, want, copies=48, reps=20):
-    """48 stacked copies (159 MB, below the 256 MB Infinity Cache) of each FFN
-    shape re-streamed by one launch each, back to back from a graph: the
-    kernel's rate when the weights stay in the Infinity Cache."""
+def mall_resident(B, base, dev_base, d_x, want, copies=(48, 24), reps=20):
+    """Stacked copies of each FFN shape small enough to stay in the 256 MB
+    Infinity Cache (48 copies = 160 MB, 24 = 80 MB per shape), re-streamed by
+    one launch each, `reps` launches back to back from a graph, with two load
+    policies: "nt" (the drop-in entry point's non-temporal weight loads, the
+    cold stream's policy) and "default" (spb_sparse_ternary_gemv_resident: the
+    default cache policy, which lets the set stay in the cache)."""
     from spbitnet_amd import kernels as K
     torch = B.torch
-    res = {"copies": copies}
+    res = {"copies": list(copies), "policies": {
+        "nt": "spb_sparse_ternary_gemv (non-temporal weight loads)",
+        "default": "spb_sparse_ternary_gemv_resident (default cache policy)"}}
     for name, k in (("6912x2560", "gate"), ("2560x6912", "down")):
         L = base[k]
         m, v = dev_base[k]
-        sm = m.repeat(copies, 1)
-        sv = v.repeat(copies, 1)
-        rows = L.rows * copies
-        y = torch.empty(rows, dtype=torch.int32, device=B.dev)
-
-        def body():
-            for _ in range(reps):
-                K.sparse_ternary_gemv_gpu(sm, sv, d_x[k], y, rows, L.cols, L.meta_stride,
-                                          L.values_stride)
-        g = B.graph_of(body)
-        for _ in range(3):
-            g.replay()
-        ms_rep = B.time_replays(g, 3)
-        ok = bool((y.cpu().numpy().reshape(copies, -1) == want[k][None, :]).all())
-        us = ms_rep * 1e3 / reps
-        nb = gemv_bytes(rows, L.cols)
-        res[name] = {"MB": round(nb / 1e6, 1), "us_per_launch": round(us, 2),
-                     "GBs": round(nb / (us * 1e-6) / 1e9, 1),
-                     "frac_of_hbm_peak": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "exact": ok}
-        del g, sm, sv, y
+        for nc in copies:
+            sm = m.repeat(nc, 1)
+            sv = v.repeat(nc, 1)
+            rows = L.rows * nc
+            y = torch.empty(rows, dtype=torch.int32, device=B.dev)
+            for pol in ("nt", "default"):
+                def body():
+                    for _ in range(reps):
+                        K.sparse_ternary_gemv_gpu(sm, sv, d_x[k], y, rows, L.cols,
+                                                  L.meta_stride, L.values_stride,
+                                                  resident=(pol == "default"))
+                g = B.graph_of(body)
+                for _ in range(3):
+                    g.replay()
+                ms_rep = B.time_replays(g, 3)
+                ok = bool((y.cpu().numpy().reshape(nc, -1) == want[k][None, :]).all())
+                us = ms_rep * 1e3 / reps
+                nb = gemv_bytes(rows, L.cols)
+                res[f"{name}_x{nc}_{pol}"] = {
+                    "MB": round(nb / 1e6, 1), "us_per_launch": round(us, 2),
+                    "GBs": round(nb / (us * 1e-6) / 1e9, 1),
+                    "frac_of_hbm_peak": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                    "exact": ok}
+                del g
+            del sm, sv, y
+        # the rate per added byte between the two set sizes: a launch has a
+        # fixed cost (~2 us: launch, first loads' latency, tail) that the
+        # smaller sets amortise over fewer bytes
+        lo, hi = min(copies), max(copies)
+        for pol in ("nt", "default"):
+            a, b = res[f"{name}_x{lo}_{pol}"], res[f"{name}_x{hi}_{pol}"]
+            dus = b["us_per_launch"] - a["us_per_launch"]
+            dmb = b["MB"] - a["MB"]
+            res[f"{name}_marginal_{pol}_GBs"] = round(dmb * 1e6 / (dus * 1e-6) / 1e9, 1) if dus > 0 else None
     B.log("mall_resident done")
     return res
 
@@ -628,6 +674,32 @@ def gemm_config2(B, base, dev_base, W, K):
             row[f"{name}_GBs"] = round(nb / (us * 1e-6) / 1e9, 1)
             row[f"{name}_dense_equiv_TOPS"] = round(2.0 * L.rows * L.cols * n / (us * 1e-6) / 1e12, 2)
         g2[f"n{n}"] = row
+    # the cuSPARSELt backend's drop-in (CuSparseLtGemm: any-int8 weights pruned
+    # to 2:4 and compressed, then D = A_pruned * B) on the same shape, with
+    # int8 weights over the whole range
+    rng = np.random.default_rng(2)
+    A = torch.from_numpy(rng.integers(-128, 128, (L.rows, L.cols)).astype(np.int8)).to(B.dev)
+    for n in (16, 64, 256):
+        ctx = K.CuSparseLtGemm(L.rows, L.cols, n, device=B.dev)
+        ctx.prepare(A)
+        Xb = torch.from_numpy(rng.integers(-128, 128, (n, L.cols)).astype(np.int8)).to(B.dev)
+        D = torch.empty((n, L.rows), dtype=torch.int32, device=B.dev)
+        ctx.execute(Xb, D)
+        P = torch.empty_like(A)
+        ctx.get_pruned_weights(P)
+        torch.cuda.synchronize()
+        want = (Xb.cpu().numpy().astype(np.float64) @
+                P.cpu().numpy().astype(np.float64).T).astype(np.int32)
+        gph = B.graph_of(lambda: [ctx.execute(Xb, D) for _ in range(20)])
+        us = B.time_replays(gph, 5) * 1e3 / 20
+        del gph
+        nb = K.sparse_i8_compressed_size(L.rows, L.cols) + n * L.cols + 4 * n * L.rows
+        g2[f"n{n}"]["i8_sparse_us"] = round(us, 2)
+        g2[f"n{n}"]["i8_sparse_GBs"] = round(nb / (us * 1e-6) / 1e9, 1)
+        g2[f"n{n}"]["i8_sparse_dense_equiv_TOPS"] = round(
+            2.0 * L.rows * L.cols * n / (us * 1e-6) / 1e12, 2)
+        g2[f"n{n}"]["i8_sparse_exact"] = bool((D.cpu().numpy() == want).all())
+        del ctx, P, D
     return g2
 
 
@@ -792,7 +864,9 @@ def cpu_baselines(B, args, base, x_h, shape_layers, W):
         "value": round(n * nb / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
         "sample": f"{n} calls of cpu_sparse_gemv (unpack_to_int8 + int32 MAC) on the 6912x2560 "
                   f"gate matrix, {dt:.1f} s, {dt / n * 1e3:.1f} ms/call; host: {info['nproc']} "
-                  f"logical CPUs, {info['lscpu_model']}"}
+                  f"logical CPUs, {info['usable_cores']} usable by this process (affinity "
+                  f"{info['sched_affinity_cpus']}, cgroup quota {info['cgroup_cpu_quota']}), "
+                  f"{info['lscpu_model']}"}
     dense = O.unpack(L.meta, L.values, L.rows, L.cols)
     n2, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < 2.0 or n2 < 3:
@@ -804,7 +878,8 @@ def cpu_baselines(B, args, base, x_h, shape_layers, W):
                                          "ms_with_unpack": round(dt / n * 1e3, 2),
                                          "ms_mac_only": round(dt2 / n2 * 1e3, 2)},
               "A11_torch_bitlinear": {}}
-    threads_all = torch.get_num_threads()
+    threads_default = torch.get_num_threads()
+    threads_all = info["usable_cores"]  # the cores this process may actually run on
     layers = shape_layers or {(r, c): W.random_layer(r, c, W.seed_for("bench-shape", r, c))
                               for r, c in SHAPES}
     for (rows, cols), Lx in layers.items():
@@ -822,7 +897,7 @@ def cpu_baselines(B, args, base, x_h, shape_layers, W):
             med = sorted(ts)[len(ts) // 2]
             row[f"{label}_us"] = round(med * 1e6, 1)
             row[f"{label}_threads"] = nt
-        torch.set_num_threads(threads_all)
+        torch.set_num_threads(threads_default)
         detail["A11_torch_bitlinear"][f"{rows}x{cols}"] = row
     B.log("cpu baselines done")
     return primary, detail

@@ -240,6 +240,16 @@ int spb_absmax_quantize_planes_f16(const uint16_t* input, uint32_t* planes, int8
 int spb_absmax_quantize_planes_bf16(const uint16_t* input, uint32_t* planes, int8_t* output,
                                     float* d_absmax, int size, spb_stream_t stream);
 
+/* spb_sparse_ternary_gemv with the weight loads on the default cache policy
+ * instead of the non-temporal one: for matrices re-read while they stay in
+ * the 256 MB Infinity Cache (a model or a set of layers that fits it), where
+ * the streaming hint would evict them.  Same arguments, results and shape
+ * rules.  No reference counterpart (the reference has one GEMV). */
+int spb_sparse_ternary_gemv_resident(const uint32_t* meta, const uint32_t* values,
+                                     const int8_t* x, int32_t* y, int rows, int cols,
+                                     int meta_row_stride, int values_row_stride,
+                                     spb_stream_t stream);
+
 /* spb_sparse_ternary_gemv with the activations given as planes; results are
  * identical to the int8 entry point on the same activations. */
 int spb_sparse_ternary_gemv_planes(const uint32_t* meta, const uint32_t* values,

@@ -24,6 +24,7 @@ SIGNATURES = {
     "spb_last_error_string": [],
     "spb_sparse_ternary_unpack": [_P, _P, _P, _I, _I, _I, _I, _P],
     "spb_sparse_ternary_gemv": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "spb_sparse_ternary_gemv_resident": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "spb_fused_sparse_bitlinear_f16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
     "spb_fused_sparse_bitlinear_bf16": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _P],
     "spb_absmax_reduce_f16": [_P, _P, _I, _P],

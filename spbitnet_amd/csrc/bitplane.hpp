@@ -659,7 +659,10 @@ constexpr int kBufferFlags = 0x00020000;
 // Cache policy of the streamed weight loads: nt (non-temporal).  Every weight
 // byte is read once; on MI355X the hint took a cold 265 MB launch with three
 // blocks per CU from ~49.5 to ~46.8 us (it made no difference with one).
+// kResidentLoadPolicy (0, the default policy) is for weights meant to stay in
+// the Infinity Cache between launches (spb_sparse_ternary_gemv_resident).
 constexpr int kStreamLoadPolicy = 2;
+constexpr int kResidentLoadPolicy = 0;
 // Buffer extents are capped at kExtentCap bytes, so an offset of kOutOfRange
 // puts every dword of a 16-byte load out of range (the load returns zeros and
 // reads no memory).
@@ -684,7 +687,7 @@ struct StreamSplit {
     int row_base;      // first row of this launch in the output
 };
 
-template <class Act, class Sink, int D>
+template <class Act, class Sink, int D, int Pol>
 __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act, Sink sink, StreamSplit sp) {
     extern __shared__ uint32_t smem[];
     const int nwords = wt.cols >> 5;
@@ -732,8 +735,8 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
             const_cast<uint32_t*>(wt.values + static_cast<long>(ub) * wt.vs),
             static_cast<short>(0), (left < cap_v ? left : cap_v) * vs4, kBufferFlags);
         StreamLoad L;
-        L.k = as_uint4(__builtin_amdgcn_raw_buffer_load_b128(rm, om, 0, kStreamLoadPolicy));
-        L.v = as_uint2(__builtin_amdgcn_raw_buffer_load_b64(rv, ov, 0, kStreamLoadPolicy));
+        L.k = as_uint4(__builtin_amdgcn_raw_buffer_load_b128(rm, om, 0, Pol));
+        L.v = as_uint2(__builtin_amdgcn_raw_buffer_load_b64(rv, ov, 0, Pol));
         return L;
     };
 
@@ -806,7 +809,7 @@ __global__ __launch_bounds__(kBlock) void gemv_stream_kernel(Weights wt, Act act
 // ranges, one launch each.
 constexpr int kStreamBlocksPerCU = 3;
 
-template <class Act, class Sink>
+template <class Act, class Sink, int Pol = kStreamLoadPolicy>
 void launch_stream(const Weights& wt, Act act, Sink sink, hipStream_t stream) {
     const int C = wt.cols / kChunk;
     const long RS = kBlock / C;
@@ -831,7 +834,7 @@ void launch_stream(const Weights& wt, Act act, Sink sink, hipStream_t stream) {
         const StreamSplit sp{static_cast<int>(nfull), static_cast<int>(nfull / grid),
                              static_cast<int>(nfull % grid), static_cast<int>(RS),
                              kExtentCap / (wt.ms * 4), kExtentCap / (wt.vs * 4), static_cast<int>(r0)};
-        hipLaunchKernelGGL((gemv_stream_kernel<Act, Sink, kStreamDepth>), dim3(static_cast<int>(grid)),
+        hipLaunchKernelGGL((gemv_stream_kernel<Act, Sink, kStreamDepth, Pol>), dim3(static_cast<int>(grid)),
                            dim3(kBlock), lds, stream, part, act, sink, sp);
         r0 += n;
     }

@@ -2063,47 +2063,34 @@ LmKernel lm_head_for(int H) {
     return (H % 512 == 0) ? lm_head_for_nc<true>(nc) : lm_head_for_nc<false>(nc);
 }
 
-// Batched decode: the LM head for a group of gn <= kLmGroup sequences
-// (g0 .. g0 + gn - 1) of a batch.  Every logit is computed with exactly the
-// operations of lm_head_kernel: the final RMSNorm in the unit order of
-// kLmBlock threads, then, for each of 64 "virtual lanes" v, the fma chain
-// over the row's 8-element chunks v, v + 64, ... (element order), then the
-// balanced pairwise tree over the 64 virtual lanes.  Here a row belongs to
-// 32 real lanes: lane j carries virtual lanes j (A) and j + 32 (B).  The
-// tree's first four levels are DPP steps inside each 16-lane row, applied to
-// A and B alike (A's rows then hold lm_head_kernel's row sums r0, r1, B's r2,
-// r3), the fifth is a lane swap across the two rows (r0 + r1, r2 + r3), the
-// last the in-lane A + B, so each sequence's logits equal a bs=1 step's bit
-// for bit.  Each half of a wave takes 4 rows at once: every x chunk read
-// from LDS feeds 4 rows x 8 fma (the matrix multiply-adds, not the LDS, bound
-// the kernel), the weight loads of a 64-chunk step are 512 contiguous bytes
-// per row and instruction, and the next step's loads are in flight while one
-// step is reduced.  The normalised vectors sit in LDS as float with 16 bytes
-// of padding per 8 chunks, so the 16 lanes of a read fall in distinct banks.
-// Per-sequence argmax (lowest index among maxima) and decode-state update by
-// the last block to finish (ticket of the group's first sequence), as in the
-// bs=1 kernel; done sequences are not updated.
-constexpr int kLmGroup = 8;          // sequences per batched LM-head block (at most)
-constexpr int kLmBatchMaxRows = 512;  // rows per block (blocks per group >= vocab / 512)
-constexpr int kLmRows = 4;            // rows per half wave at once
-constexpr int kLmBatchBlock = 512;    // threads per batched LM-head block
-// The batched LM head holds a group's normalised vectors in LDS, so it
-// takes hidden sizes up to kLmBatchMaxH (NC <= 8 chunks per lane).
+// Batched decode: the final norm writes each sequence's normalised vector
+// for the batched LM head (lm_head_mfma_kernel / lm_select_kernel below).
+// The batched final norm holds a normalised vector in LDS, so the batched
+// engine takes hidden sizes up to kLmBatchMaxH.
 constexpr int kLmBatchMaxH = 4096;
 
-// float index of chunk c's first element in the padded LDS vector
+// float index of chunk c's first element in a padded normalised vector
 __device__ __forceinline__ int lm_xpad(int c) { return 8 * c + 4 * (c >> 3); }
+
+// A non-negative double rounded up to float.
+__device__ __forceinline__ float lm_round_up(double d) {
+    float f = static_cast<float>(d);
+    if (static_cast<double>(f) < d) f = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, f) + 1u);
+    return f;
+}
 
 // Batched decode: the final RMSNorm of sequence blockIdx.x with
 // lm_head_kernel's prologue (same threads, same order), written padded for
-// lm_head_batch_kernel: xn[b][lm_xpad(c) ..] = chunk c of the normalised
-// vector (bf16-rounded floats), zeros for chunks c >= H / 8 up to nc64.
+// the LM head: xn[b][lm_xpad(c) ..] = chunk c of the normalised vector
+// (bf16-rounded floats), zeros for chunks c >= H / 8 up to nc64; xnorm[b] =
+// its Euclidean norm (summed in double, rounded up to float).
 template <bool kOne>
 __global__ __launch_bounds__(kLmBlock) void final_norm_batch_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ wn, float eps,
-    float* __restrict__ xn, int H, int nc64, int xstride) {
+    float* __restrict__ xn, float* __restrict__ xnorm, int H, int nc64, int xstride) {
     __shared__ __align__(16) float xs[kLmBatchMaxH];
     __shared__ float red[kLmBlock / kWave];
+    __shared__ double dred[kLmBlock / kWave];
     const int tid = threadIdx.x, nch = H >> 3;
     const uint16_t* xg = x + static_cast<long>(blockIdx.x) * H;
     HeldWeights<kLmBlock> hw;
@@ -2114,6 +2101,22 @@ __global__ __launch_bounds__(kLmBlock) void final_norm_batch_kernel(
     const float inv = inv_rms(block_sum<kLmBlock>(ss, red), H, eps);
     hw.template apply<kOne>(xs, wn, inv, nch, tid);
     __syncthreads();
+    {
+        double q = 0.0;
+        for (int i = tid; i < H; i += kLmBlock) {
+            const double v = xs[i];
+            q += v * v;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) q += __shfl_xor(q, off, kWave);
+        if ((tid & (kWave - 1)) == 0) dred[tid / kWave] = q;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double q = 0.0;
+        for (int w = 0; w < kLmBlock / kWave; ++w) q += dred[w];
+        xnorm[blockIdx.x] = lm_round_up(__builtin_sqrt(q));
+    }
     float* dst = xn + static_cast<long>(blockIdx.x) * xstride;
     for (int c = tid; c < nc64; c += kLmBlock) {
         float f[8];
@@ -2127,266 +2130,327 @@ __global__ __launch_bounds__(kLmBlock) void final_norm_batch_kernel(
     }
 }
 
-// One launch covers every group of kLmGroup sequences: nblk row blocks per
-// group, block x -> (row block, group) such that the groups' blocks of one
-// row block are dispatched together to the same XCD (x % 8), so the table's
-// rows come from HBM once and from that XCD's L2 for the other groups.
-template <int NC, bool kFull>
-__global__ __launch_bounds__(kLmBatchBlock) void lm_head_batch_kernel(
-    const uint16_t* __restrict__ W, const float* __restrict__ xn, float* __restrict__ logits,
-    float* __restrict__ part_v, int* __restrict__ part_i, EngineState* __restrict__ st,
-    int* __restrict__ tokens, long tok_stride, int V, int H, const float2* __restrict__ rope,
-    float2* __restrict__ cur_rope, int half_hd, int max_seq, int rbase, int rrem, int nblk,
-    int B) {
-    constexpr int kWaves = kLmBatchBlock / kWave;
-    extern __shared__ __align__(16) float lds[];
-    const int nch = H >> 3;
-    const int xstride = lm_xpad(NC * kWave);          // floats per padded vector
-    float* xs = lds;                                   // [gn][xstride]
-    float* lg = lds + static_cast<long>(kLmGroup) * xstride;  // [gn][kLmBatchMaxRows]
-    __shared__ float wv[kWaves];
-    __shared__ int wi[kWaves];
-    __shared__ int last;
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int j = lane & 31, hg = lane >> 5;  // virtual lanes j, j + 32 of the half's rows
-    const int ng = (B + kLmGroup - 1) / kLmGroup;
-    const int bq = blockIdx.x >> 3, grp = bq % ng;
-    const int blk = (bq / ng) * 8 + (blockIdx.x & 7);  // nblk % 8 == 0
-    const int g0 = grp * kLmGroup, gn = B - g0 < kLmGroup ? B - g0 : kLmGroup;
-    const long b0 = static_cast<long>(blk) * rbase + (blk < rrem ? blk : rrem);
-    const long b1 = b0 + rbase + (blk < rrem ? 1 : 0);
-    const long noct = (b1 - b0 + 7) >> 3;  // row octets of the block
-    {
-        const uint4* src = reinterpret_cast<const uint4*>(xn + static_cast<long>(g0) * xstride);
-        uint4* dst = reinterpret_cast<uint4*>(xs);
-        for (int i = tid; i < gn * (xstride >> 2); i += kLmBatchBlock) dst[i] = src[i];
-    }
-    __syncthreads();
-
-    float best[kLmGroup];
-    int best_i[kLmGroup];
-#pragma unroll
-    for (int g = 0; g < kLmGroup; ++g) {
-        best[g] = -INFINITY;
-        best_i[g] = 0x7FFFFFFF;
-    }
-    // step k of the 4 rows from rb: chunks k * 64 + j (A) and k * 64 + 32 + j (B)
-    auto load_step = [&](long rb, int k, uint4 (&w)[kLmRows][2]) {
-#pragma unroll
-        for (int r = 0; r < kLmRows; ++r) {
-            const long row = rb + r;
-            const uint4* wr = reinterpret_cast<const uint4*>(W + (row < V ? row : V - 1) * H);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int c = k * kWave + 32 * i + j;
-                if (kFull)
-                    w[r][i] = nt_load(wr + c);
-                else
-                    w[r][i] = c < nch ? nt_load(wr + c) : make_uint4(0, 0, 0, 0);
-            }
-        }
-    };
-    for (long o = wave; o < noct; o += kWaves) {
-        const long rb = b0 + 8 * o + kLmRows * hg;
-        float acc[kLmGroup][kLmRows][2];
-#pragma unroll
-        for (int g = 0; g < kLmGroup; ++g)
-#pragma unroll
-            for (int r = 0; r < kLmRows; ++r) acc[g][r][0] = acc[g][r][1] = 0.0f;
-        uint4 wa[kLmRows][2], wb[kLmRows][2];
-        load_step(rb, 0, wa);
-#pragma unroll
-        for (int k = 0; k < NC; ++k) {
-            uint4 (&cur)[kLmRows][2] = (k & 1) ? wb : wa;
-            uint4 (&nxt)[kLmRows][2] = (k & 1) ? wa : wb;
-            if (k + 1 < NC) load_step(rb, k + 1, nxt);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int c = k * kWave + 32 * i + j;
-                if (kFull || c < nch) {  // lm_head_kernel's chunks only
-                    float wf[kLmRows][8];
-#pragma unroll
-                    for (int r = 0; r < kLmRows; ++r) unpack_bf16x8(cur[r][i], wf[r]);
-#pragma unroll
-                    for (int g = 0; g < kLmGroup; ++g) {
-                        if (g < gn) {
-                            float xv[8];
-                            load_f8(xs + static_cast<long>(g) * xstride + lm_xpad(c), xv);
-#pragma unroll
-                            for (int r = 0; r < kLmRows; ++r)
-#pragma unroll
-                                for (int e = 0; e < 8; ++e)
-                                    acc[g][r][i] = __builtin_fmaf(wf[r][e], xv[e], acc[g][r][i]);
-                        }
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < kLmGroup; ++g) {
-            if (g < gn) {
-#pragma unroll
-                for (int r = 0; r < kLmRows; ++r) {
-                    float a = acc[g][r][0], b = acc[g][r][1];
-                    a += dpp_f<0xB1>(a);   // quad_perm [1,0,3,2]
-                    b += dpp_f<0xB1>(b);
-                    a += dpp_f<0x4E>(a);   // quad_perm [2,3,0,1]
-                    b += dpp_f<0x4E>(b);
-                    a += dpp_f<0x141>(a);  // row_half_mirror
-                    b += dpp_f<0x141>(b);
-                    a += dpp_f<0x140>(a);  // row_mirror: r0 | r1 (A), r2 | r3 (B)
-                    b += dpp_f<0x140>(b);
-                    a += __shfl_xor(a, 16, kWave);  // r0 + r1
-                    b += __shfl_xor(b, 16, kWave);  // r2 + r3
-                    const float t = a + b;
-                    const long row = rb + r;
-                    if (j == 0 && row < b1) {
-                        lg[g * kLmBatchMaxRows + (row - b0)] = t;
-                        if (t > best[g]) {  // a lane's rows ascend: strict > keeps the first maximum
-                            best[g] = t;
-                            best_i[g] = static_cast<int>(row);
-                        }
-                    }
-                }
-            }
-        }
-    }
-    __syncthreads();
-    for (int g = 0; g < gn; ++g)
-        for (long jj = tid; jj < b1 - b0; jj += kLmBatchBlock)
-            logits[static_cast<long>(g0 + g) * V + b0 + jj] = lg[g * kLmBatchMaxRows + jj];
-    // per-sequence block maxima: the two halves of each wave, then the waves
-#pragma unroll
-    for (int g = 0; g < kLmGroup; ++g) {
-        if (g < gn) {
-            float bv = best[g];
-            int bi = best_i[g];
-#pragma unroll
-            for (int off = 32; off < kWave; off <<= 1) {  // lanes 0 and 32 hold the rows
-                const float ov = __shfl_xor(bv, off, kWave);
-                const int oi = __shfl_xor(bi, off, kWave);
-                if (ov > bv || (ov == bv && oi < bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            if (lane == 0) {
-                wv[wave] = bv;
-                wi[wave] = bi;
-            }
-            __syncthreads();
-            if (tid == 0) {
-                float b = wv[0];
-                int bb = wi[0];
-                for (int w = 1; w < kWaves; ++w)
-                    if (wv[w] > b || (wv[w] == b && wi[w] < bb)) {
-                        b = wv[w];
-                        bb = wi[w];
-                    }
-                part_v[static_cast<long>(g0 + g) * nblk + blk] = b;
-                part_i[static_cast<long>(g0 + g) * nblk + blk] = bb;
-            }
-            __syncthreads();
-        }
-    }
-    if (tid == 0) {
-        __threadfence();
-        const unsigned tk = atomicAdd(&st[g0].ticket, 1u);
-        last = tk == static_cast<unsigned>(nblk) - 1;
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    for (int g = 0; g < gn; ++g) {
-        EngineState* sg = st + g0 + g;
-        const float* pv = part_v + static_cast<long>(g0 + g) * nblk;
-        const int* pi = part_i + static_cast<long>(g0 + g) * nblk;
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
-        for (int k = tid; k < nblk; k += kLmBatchBlock) {
-            const float v = __hip_atomic_load(&pv[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const int ii = __hip_atomic_load(&pi[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (v > bv || (v == bv && ii < bi)) {
-                bv = v;
-                bi = ii;
-            }
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, kWave);
-            const int oi = __shfl_xor(bi, off, kWave);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if (lane == 0) {
-            wv[wave] = bv;
-            wi[wave] = bi;
-        }
-        __syncthreads();
-        const int done = sg->done, pos_old = sg->pos;
-        __syncthreads();  // every thread has read the state before thread 0 changes it
-        if (done) continue;  // uniform
-        if (tid == 0) {
-            for (int w = 1; w < kWaves; ++w)
-                if (wv[w] > bv || (wv[w] == bv && wi[w] < bi)) {
-                    bv = wv[w];
-                    bi = wi[w];
-                }
-            const int tok = bi == 0x7FFFFFFF ? 0 : bi;  // all-NaN logits: token 0
-            const int nxt = pos_old + 1;
-            int* tk = tokens + static_cast<long>(g0 + g) * tok_stride;
-            if (nxt >= sg->prompt_len && nxt < sg->limit) {
-                tk[nxt] = tok;
-                sg->generated += 1;
-                if (sg->stop_eos && tok == sg->eos) sg->done = 1;
-            }
-            sg->pos = nxt;
-            if (nxt >= sg->limit) sg->done = 1;
-        }
-        const int p = pos_old + 1 < max_seq ? pos_old + 1 : max_seq - 1;
-        float2* cr = cur_rope + static_cast<long>(g0 + g) * half_hd;
-        for (int k = tid; k < half_hd; k += kLmBatchBlock)
-            cr[k] = rope[static_cast<long>(p) * half_hd + k];
-        __syncthreads();  // wv / wi are reused by the next sequence
-    }
-    if (tid == 0) st[g0].ticket = 0u;
-}
-
-typedef void (*LmBatchKernel)(const uint16_t*, const float*, float*, float*, int*,
-                              EngineState*, int*, long, int, int, const float2*, float2*, int,
-                              int, int, int, int, int);
-
-template <bool kFull>
-LmBatchKernel lm_head_batch_for_nc(int nc) {
-    switch (nc) {
-        case 1: return lm_head_batch_kernel<1, kFull>;
-        case 2: return lm_head_batch_kernel<2, kFull>;
-        case 3: return lm_head_batch_kernel<3, kFull>;
-        case 4: return lm_head_batch_kernel<4, kFull>;
-        case 5: return lm_head_batch_kernel<5, kFull>;
-        case 6: return lm_head_batch_kernel<6, kFull>;
-        case 7: return lm_head_batch_kernel<7, kFull>;
-        default: return lm_head_batch_kernel<8, kFull>;
-    }
-}
-
-LmBatchKernel lm_head_batch_for(int H) {
-    const int nc = (H / 8 + kWave - 1) / kWave;
-    return (H % 512 == 0) ? lm_head_batch_for_nc<true>(nc) : lm_head_batch_for_nc<false>(nc);
-}
-
 // floats per padded normalised vector: lm_xpad(nc * 64), nc = ceil(H / 512)
 int lm_head_batch_xstride(int H) {
     const int nc = (H / 8 + kWave - 1) / kWave;
     return 8 * (nc * kWave) + 4 * ((nc * kWave) >> 3);
 }
 
-size_t lm_head_batch_lds(int H) {
-    return (static_cast<size_t>(kLmGroup) * lm_head_batch_xstride(H) +
-            static_cast<size_t>(kLmGroup) * kLmBatchMaxRows) * sizeof(float);
+
+// ---- batched decode: the LM head on the bf16 matrix cores ------------------------
+//
+// logits[t][r] = W[r] . xn[t] for the B sequences of a step (W the bf16
+// [V][H] table, xn[t] the final-normed vector, bf16 values), in two launches:
+//   lm_head_mfma_kernel: v_mfma_f32_16x16x32_bf16 over blocks of 512 rows and
+//     32 tokens: approximate logits a[t][r] (every product exact, the sums in
+//     the matrix cores' float32 accumulation), stored, and per block and
+//     token the largest lower bound a - d and upper bound a + d, with
+//     d[t][r] = c |W[r]| |xn[t]| (Euclidean norms rounded up);
+//   lm_select_kernel (one block per sequence): M = the largest lower bound;
+//     every row whose upper bound reaches M (in the blocks whose largest
+//     upper bound does) is recomputed with exactly the operations of the bs=1
+//     kernel (lm_head_kernel: 64 fma chains over 8-element chunks, then the
+//     pairwise tree), its exact logit stored, and the argmax (lowest index
+//     among maxima) taken over those rows.
+// Why the token equals the bs=1 kernel's: with e the bs=1 value and S the
+// real dot product, |e - S| <= (H/64 + 6) 2^-24 sum |w x| (H/64 fma per
+// chain, a 6-level tree), |a - S| <= H 2^-23 sum |w x| (at most one float32
+// rounding, truncation allowed, per accumulated product), and sum |w x| <=
+// |w| |x|; c = 1.25 (H + H/64 + 8) 2^-23 covers both with a margin for the
+// rounding of the bounds themselves.  A row outside the candidates has
+// e <= a + d < M <= max_j (a_j - d_j) <= max_j e_j, so it is not the argmax,
+// which is therefore among the recomputed rows, whose values are the bs=1
+// kernel's.  The other rows keep the approximate logits (|a - e| <= 2 d).
+// NaN upper bounds count as candidates; more than kLmCandMax candidates in a
+// sequence (e.g. NaN logits everywhere) fall back to recomputing every row.
+constexpr int kLmMfmaBlock = 512;                     // 8 waves
+constexpr int kLmMfmaStrips = 4;                      // 16-row strips per wave
+constexpr int kLmMfmaRows = 8 * kLmMfmaStrips * 16;   // rows per block
+constexpr int kLmMfmaSeg = 1024;                      // hidden elements per staged x segment
+constexpr int kLmMfmaTok = 32;                        // tokens per block (two 16-token tiles)
+constexpr int kLmCandMax = 1024;                      // candidate rows per sequence
+constexpr int kLmSelMaxBlocks = 2048;                 // row blocks (vocabulary <= 1M rows)
+constexpr int kLmSelectBlock = 256;
+
+typedef __bf16 lm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float lm_f32x4 __attribute__((ext_vector_type(4)));
+
+float lm_bound_c(int H) {
+    return static_cast<float>(1.25 * (H + H / 64 + 8) * 0x1p-23);
+}
+
+// |W[r]| (rounded up), one wave per row, once per engine.
+__global__ __launch_bounds__(256) void lm_row_norm_kernel(const uint16_t* __restrict__ W,
+                                                          float* __restrict__ out, int V, int H) {
+    const long r = static_cast<long>(blockIdx.x) * 4 + threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (r >= V) return;
+    double s = 0.0;
+    for (int c = lane; c < H; c += kWave) {
+        const double w = BF16::to_float(W[r * H + c]);
+        s += w * w;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
+    if (lane == 0) out[r] = lm_round_up(__builtin_sqrt(s));
+}
+
+// Block (row block x, token group y): 8 waves, wave w owning the strips
+// 4w .. 4w + 3 (16 rows each) of the block's 512 rows and both 16-token
+// tiles.  x is staged in LDS segment by segment (1024 hidden elements, 32
+// tokens, bf16, the 16-byte chunk c of token t at c ^ (t & 15): the 16 lanes
+// of a tile read 16 distinct bank groups).  A 64-element step of a strip is
+// two MFMAs: lane (i, q) holds row i's elements 16 q + [0, 8) and 16 q +
+// [8, 16) of the step (one 32-byte weight load) and the same elements of
+// token i (the dot product's K order inside an MFMA is the matrix cores'
+// own, as in any fp32 sum order).
+template <int NT>
+__global__ __launch_bounds__(kLmMfmaBlock) void lm_head_mfma_kernel(
+    const uint16_t* __restrict__ W, const float* __restrict__ xn, int xstride,
+    const float* __restrict__ wnorm, const float* __restrict__ xnorm, float cbound,
+    float* __restrict__ logits, float* __restrict__ part_lo, float* __restrict__ part_hi, int V,
+    int H, int B, int nblk) {
+    __shared__ __align__(16) uint16_t xs[kLmMfmaTok * kLmMfmaSeg];
+    __shared__ float red_lo[8][kLmMfmaTok], red_hi[8][kLmMfmaTok];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int li = lane & 15, q = lane >> 4;
+    const int blk = blockIdx.x, t0 = blockIdx.y * kLmMfmaTok;
+    const int ntok = B - t0 < kLmMfmaTok ? B - t0 : kLmMfmaTok;
+    const long r0 = static_cast<long>(blk) * kLmMfmaRows + wave * (kLmMfmaStrips * 16);
+    const uint16_t* wrow[kLmMfmaStrips];
+#pragma unroll
+    for (int s = 0; s < kLmMfmaStrips; ++s) {
+        const long r = r0 + 16 * s + li;
+        wrow[s] = W + (r < V ? r : V - 1) * static_cast<long>(H);
+    }
+    lm_f32x4 acc[kLmMfmaStrips][NT];
+#pragma unroll
+    for (int s = 0; s < kLmMfmaStrips; ++s)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[s][t] = (lm_f32x4){0.f, 0.f, 0.f, 0.f};
+    // weights of step e0 (global element index) of every strip; elements past
+    // H read as zeros (H % 8 == 0: each 16-byte half is wholly in or out)
+    auto load_w = [&](int e0, uint4 (&w)[kLmMfmaStrips][2]) {
+        const int e = e0 + 16 * q;
+#pragma unroll
+        for (int s = 0; s < kLmMfmaStrips; ++s) {
+            const uint4* p = reinterpret_cast<const uint4*>(wrow[s] + e);
+            w[s][0] = e < H ? nt_load(p) : make_uint4(0, 0, 0, 0);
+            w[s][1] = e + 8 < H ? nt_load(p + 1) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    for (int seg0 = 0; seg0 < H; seg0 += kLmMfmaSeg) {
+        const int sl = H - seg0 < kLmMfmaSeg ? H - seg0 : kLmMfmaSeg;
+        const int nstep = (sl + 63) / 64;
+        __syncthreads();  // the previous segment's operand reads are done
+        for (int i = tid; i < kLmMfmaTok * (kLmMfmaSeg / 8); i += kLmMfmaBlock) {
+            const int t = i / (kLmMfmaSeg / 8), c = i % (kLmMfmaSeg / 8);
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (t < ntok && 8 * c < sl) {
+                float f[8];
+                load_f8(xn + static_cast<long>(t0 + t) * xstride + lm_xpad((seg0 >> 3) + c), f);
+                uint32_t u[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)  // bf16-rounded floats: the high halves are exact
+                    u[k] = (__builtin_bit_cast(uint32_t, f[2 * k]) >> 16) |
+                           (__builtin_bit_cast(uint32_t, f[2 * k + 1]) & 0xFFFF0000u);
+                v = make_uint4(u[0], u[1], u[2], u[3]);
+            }
+            *reinterpret_cast<uint4*>(xs + t * kLmMfmaSeg + 8 * (c ^ (t & 15))) = v;
+        }
+        __syncthreads();
+        // step stp (64 elements) of every strip from the weights in w
+        auto compute = [&](const uint4 (&w)[kLmMfmaStrips][2], int stp) {
+            const int c1 = 8 * stp + 2 * q;  // local 16-byte chunk of the lane's first 8 elements
+            lm_bf16x8 xb[NT][2];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const uint16_t* xr = xs + (16 * t + li) * kLmMfmaSeg;
+                xb[t][0] = __builtin_bit_cast(lm_bf16x8,
+                                              *reinterpret_cast<const uint4*>(xr + 8 * (c1 ^ li)));
+                xb[t][1] = __builtin_bit_cast(
+                    lm_bf16x8, *reinterpret_cast<const uint4*>(xr + 8 * ((c1 + 1) ^ li)));
+            }
+#pragma unroll
+            for (int s = 0; s < kLmMfmaStrips; ++s) {
+                const lm_bf16x8 w0 = __builtin_bit_cast(lm_bf16x8, w[s][0]);
+                const lm_bf16x8 w1 = __builtin_bit_cast(lm_bf16x8, w[s][1]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xb[t][0], acc[s][t], 0, 0, 0);
+                    acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xb[t][1], acc[s][t], 0, 0, 0);
+                }
+            }
+        };
+        // two weight buffers: each is refilled right after its step is used
+        uint4 wa[kLmMfmaStrips][2], wb[kLmMfmaStrips][2];
+        load_w(seg0, wa);
+        for (int d = 0; d < nstep; d += 2) {
+            if (d + 1 < nstep) load_w(seg0 + 64 * (d + 1), wb);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(wa, d);
+            if (d + 2 < nstep) load_w(seg0 + 64 * (d + 2), wa);
+            __builtin_amdgcn_sched_barrier(0);
+            if (d + 1 < nstep) compute(wb, d + 1);
+        }
+    }
+    // lane (i, q) of strip s, tile t holds rows r0 + 16 s + 4 q + v of token
+    // t0 + 16 t + i
+    float mlo[NT], mhi[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        mlo[t] = -INFINITY;
+        mhi[t] = -INFINITY;
+        const int tok = t0 + 16 * t + li;
+        if (tok >= B) continue;
+        const float xnt = xnorm[tok];
+#pragma unroll
+        for (int s = 0; s < kLmMfmaStrips; ++s) {
+            const long row = r0 + 16 * s + 4 * q;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (row + v >= V) continue;
+                const float a = acc[s][t][v];
+                const float dd = (cbound * wnorm[row + v]) * xnt;
+                logits[static_cast<long>(tok) * V + row + v] = a;
+                mlo[t] = __builtin_fmaxf(mlo[t], a - dd);
+                const float hi = a + dd;
+                mhi[t] = hi != hi ? INFINITY : __builtin_fmaxf(mhi[t], hi);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int off = 16; off < kWave; off <<= 1) {
+            mlo[t] = __builtin_fmaxf(mlo[t], __shfl_xor(mlo[t], off, kWave));
+            mhi[t] = __builtin_fmaxf(mhi[t], __shfl_xor(mhi[t], off, kWave));
+        }
+        if (q == 0) {
+            red_lo[wave][16 * t + li] = mlo[t];
+            red_hi[wave][16 * t + li] = mhi[t];
+        }
+    }
+    __syncthreads();
+    if (tid < kLmMfmaTok && tid < ntok) {
+        float lo = red_lo[0][tid], hi = red_hi[0][tid];
+        for (int w = 1; w < 8; ++w) {
+            lo = __builtin_fmaxf(lo, red_lo[w][tid]);
+            hi = __builtin_fmaxf(hi, red_hi[w][tid]);
+        }
+        part_lo[static_cast<long>(t0 + tid) * nblk + blk] = lo;
+        part_hi[static_cast<long>(t0 + tid) * nblk + blk] = hi;
+    }
+}
+
+// Sequence blockIdx.x: the candidate rows' exact logits (the bs=1 chain),
+// the argmax over them and the decode-state update of lm_head_batch_kernel.
+__global__ __launch_bounds__(kLmSelectBlock) void lm_select_kernel(
+    const uint16_t* __restrict__ W, const float* __restrict__ xn, int xstride,
+    const float* __restrict__ wnorm, const float* __restrict__ xnorm, float cbound,
+    float* __restrict__ logits, const float* __restrict__ part_lo,
+    const float* __restrict__ part_hi, EngineState* __restrict__ st, int* __restrict__ tokens,
+    long tok_stride, int V, int H, const float2* __restrict__ rope, float2* __restrict__ cur_rope,
+    int half_hd, int max_seq, int nblk) {
+    constexpr int kWaves = kLmSelectBlock / kWave;
+    __shared__ int cand[kLmCandMax];
+    __shared__ int selb[kLmSelMaxBlocks];
+    __shared__ int ncand, nsel;
+    __shared__ float red[kWaves];
+    __shared__ float wv[kWaves];
+    __shared__ int wi[kWaves];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int b = blockIdx.x;
+    const float* lo = part_lo + static_cast<long>(b) * nblk;
+    const float* hi = part_hi + static_cast<long>(b) * nblk;
+    float* lg = logits + static_cast<long>(b) * V;
+    const float* x = xn + static_cast<long>(b) * xstride;
+    float m = -INFINITY;
+    for (int k = tid; k < nblk; k += kLmSelectBlock) m = __builtin_fmaxf(m, lo[k]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off, kWave));
+    if (lane == 0) red[wave] = m;
+    if (tid == 0) {
+        ncand = 0;
+        nsel = 0;
+    }
+    __syncthreads();
+    m = red[0];
+    for (int w = 1; w < kWaves; ++w) m = __builtin_fmaxf(m, red[w]);
+    // the blocks whose largest upper bound reaches m (NaN bounds are +inf)
+    for (int k = tid; k < nblk; k += kLmSelectBlock)
+        if (!(hi[k] < m)) selb[atomicAdd(&nsel, 1)] = k;
+    __syncthreads();
+    const float xnt = xnorm[b];
+    const int ns = nsel;
+    for (int j = 0; j < ns; ++j) {
+        const int k = selb[j];
+        const long e = static_cast<long>(k + 1) * kLmMfmaRows < V ? static_cast<long>(k + 1) * kLmMfmaRows : V;
+        for (long r = static_cast<long>(k) * kLmMfmaRows + tid; r < e; r += kLmSelectBlock) {
+            const float a = lg[r];
+            const float dd = (cbound * wnorm[r]) * xnt;
+            if (!(a + dd < m)) {
+                const int slot = atomicAdd(&ncand, 1);
+                if (slot < kLmCandMax) cand[slot] = static_cast<int>(r);
+            }
+        }
+    }
+    __syncthreads();
+    const int nc = ncand;
+    const bool all = nc > kLmCandMax;  // recompute every row
+    const int nrows = all ? V : nc;
+    const int nch = H >> 3;
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int k = wave; k < nrows; k += kWaves) {
+        const int r = all ? k : cand[k];
+        const uint4* wr = reinterpret_cast<const uint4*>(W + static_cast<long>(r) * H);
+        float a = 0.0f;
+        for (int c = lane; c < nch; c += kWave) {  // lm_head_kernel's chain of virtual lane `lane`
+            float wf[8], xv[8];
+            unpack_bf16x8(wr[c], wf);
+            load_f8(x + lm_xpad(c), xv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a = __builtin_fmaf(wf[e], xv[e], a);
+        }
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) a += __shfl_xor(a, off, kWave);  // pairwise tree
+        if (lane == 0) lg[r] = a;
+        if (a > bv || (a == bv && r < bi)) {
+            bv = a;
+            bi = r;
+        }
+    }
+    if (lane == 0) {
+        wv[wave] = bv;
+        wi[wave] = bi;
+    }
+    __syncthreads();
+    EngineState* sg = st + b;
+    const int done = sg->done, pos_old = sg->pos;
+    __syncthreads();  // every thread has read the state before thread 0 changes it
+    if (done) return;  // uniform
+    if (tid == 0) {
+        for (int w = 1; w < kWaves; ++w)
+            if (wv[w] > bv || (wv[w] == bv && wi[w] < bi)) {
+                bv = wv[w];
+                bi = wi[w];
+            }
+        const int tok = bi == 0x7FFFFFFF ? 0 : bi;  // all-NaN logits: token 0
+        const int nxt = pos_old + 1;
+        int* tk = tokens + static_cast<long>(b) * tok_stride;
+        if (nxt >= sg->prompt_len && nxt < sg->limit) {
+            tk[nxt] = tok;
+            sg->generated += 1;
+            if (sg->stop_eos && tok == sg->eos) sg->done = 1;
+        }
+        sg->pos = nxt;
+        if (nxt >= sg->limit) sg->done = 1;
+    }
+    const int p = pos_old + 1 < max_seq ? pos_old + 1 : max_seq - 1;
+    float2* cr = cur_rope + static_cast<long>(b) * half_hd;
+    for (int k = tid; k < half_hd; k += kLmSelectBlock) cr[k] = rope[static_cast<long>(p) * half_hd + k];
 }
 
 // ---- random-init weights (model generation on the device) ------------------------
@@ -3559,15 +3623,17 @@ struct spb_batch_engine {
     const float* final_norm = nullptr;
     int max_seq = 0, S = 0, batch = 0, lm_grid = 0;
     long kv_seq = 0;  // cache elements of one sequence in one layer's K (or V) cache
-    LmBatchKernel lm_kernel = nullptr;
+    float lm_c = 0.f;  // the LM head's error-bound constant (lm_bound_c)
     std::vector<void*> owned;
     std::vector<uint16_t*> kcache, vcache;  // per layer: [batch][kv head][max_seq][head_dim]
     PrefillBufs step;  // the decode step's per-token buffers (batch tokens)
     PrefillBufs pf;    // the prompt prefill's buffers
     float* logits = nullptr;              // [batch][vocab]
     float* xn = nullptr;                  // [batch][padded hidden]: final-normed vectors
-    float* part_v = nullptr;              // [batch][lm_grid]
-    int* part_i = nullptr;                // [batch][lm_grid]
+    float* part_lo = nullptr;             // [batch][lm_grid]: largest lower bound per row block
+    float* part_hi = nullptr;             // [batch][lm_grid]: largest upper bound per row block
+    float* wnorm = nullptr;               // [vocab]: |LM-head row| (rounded up)
+    float* xnorm = nullptr;               // [batch]: |normalised vector| (rounded up)
     int* tokens = nullptr;                // [batch][max_seq + 1]
     float2* rope = nullptr;               // [max_seq][head_dim / 2]
     float2* cur_rope = nullptr;           // [batch][head_dim / 2]
@@ -3589,8 +3655,9 @@ struct spb_batch_engine {
 
     // One decode step of every sequence: per layer the producer, GEMM(s)
     // and sink of each projection over the batch's tokens and the batched
-    // attention; then the final norm and the LM head (groups of kLmGroup
-    // sequences in one launch).
+    // attention; then the final norm and the LM head (the matrix-core
+    // logits over every sequence, then the exact candidates and the argmax
+    // per sequence).
     hipError_t enqueue_step(hipStream_t s) const {
         const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
         const int nkv = cfg.num_key_value_heads, H = cfg.hidden_size;
@@ -3671,13 +3738,20 @@ struct spb_batch_engine {
         }
         const int V = cfg.vocab_size, xstride = lm_head_batch_xstride(H);
         const int nc64 = (H / 8 + kWave - 1) / kWave * kWave;
-        const int ng = (B + kLmGroup - 1) / kLmGroup;
         hipLaunchKernelGGL(final_norm_batch_kernel<true>, dim3(B), dim3(kLmBlock), 0, s, step.r,
-                           final_norm, eps, xn, H, nc64, xstride);
-        hipLaunchKernelGGL(lm_kernel, dim3(lm_grid * ng), dim3(kLmBatchBlock),
-                           lm_head_batch_lds(H), s, lm_head, xn, logits, part_v, part_i, st,
-                           tokens, tok_stride(), V, H, rope, cur_rope, hd / 2, max_seq,
-                           V / lm_grid, V % lm_grid, lm_grid, B);
+                           final_norm, eps, xn, xnorm, H, nc64, xstride);
+        const dim3 grid(lm_grid, (B + kLmMfmaTok - 1) / kLmMfmaTok);
+        if (B > 16)
+            hipLaunchKernelGGL(lm_head_mfma_kernel<2>, grid, dim3(kLmMfmaBlock), 0, s, lm_head, xn,
+                               xstride, wnorm, xnorm, lm_c, logits, part_lo, part_hi, V, H, B,
+                               lm_grid);
+        else
+            hipLaunchKernelGGL(lm_head_mfma_kernel<1>, grid, dim3(kLmMfmaBlock), 0, s, lm_head, xn,
+                               xstride, wnorm, xnorm, lm_c, logits, part_lo, part_hi, V, H, B,
+                               lm_grid);
+        hipLaunchKernelGGL(lm_select_kernel, dim3(B), dim3(kLmSelectBlock), 0, s, lm_head, xn,
+                           xstride, wnorm, xnorm, lm_c, logits, part_lo, part_hi, st, tokens,
+                           tok_stride(), V, H, rope, cur_rope, hd / 2, max_seq, lm_grid);
         return hipGetLastError();
     }
 };
@@ -3710,16 +3784,13 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
     e->batch = batch;
     e->S = (max_seq + kAttnSplit - 1) / kAttnSplit;
     e->kv_seq = static_cast<long>(nkv) * max_seq * hd;
-    e->lm_kernel = lm_head_batch_for(H);
-    // blocks per group: one per CU, at least vocab / kLmBatchMaxRows (the
-    // rows of a block are staged in LDS), a multiple of 8 (one per XCD)
-    const long lm_need = (static_cast<long>(V) + 8 * kLmBatchBlock / kWave - 1) /
-                         (8 * kLmBatchBlock / kWave);  // an octet of rows per wave
-    const long lm_min = (static_cast<long>(V) + kLmBatchMaxRows - 1) / kLmBatchMaxRows;
-    long lm_grid = device_cu_count();
-    if (lm_grid > lm_need) lm_grid = lm_need;
-    lm_grid = lm_grid > lm_min ? lm_grid : lm_min;
-    e->lm_grid = static_cast<int>((lm_grid + 7) / 8 * 8);
+    e->lm_c = lm_bound_c(H);
+    e->lm_grid = (V + kLmMfmaRows - 1) / kLmMfmaRows;
+    if (e->lm_grid > kLmSelMaxBlocks) {
+        delete e;
+        return invalid("%s: vocabulary %d exceeds the batched LM head's %d rows", fn, V,
+                       kLmSelMaxBlocks * kLmMfmaRows);
+    }
 
     auto& own = e->owned;
     const size_t kv = static_cast<size_t>(batch) * e->kv_seq;
@@ -3734,8 +3805,10 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
          alloc_prefill(e->pf, *cfg, e->S, own) &&
          (e->logits = dev_alloc<float>(B * V, own)) &&
          (e->xn = dev_alloc<float>(B * lm_head_batch_xstride(H), own)) &&
-         (e->part_v = dev_alloc<float>(B * e->lm_grid, own)) &&
-         (e->part_i = dev_alloc<int>(B * e->lm_grid, own)) &&
+         (e->part_lo = dev_alloc<float>(B * e->lm_grid, own)) &&
+         (e->part_hi = dev_alloc<float>(B * e->lm_grid, own)) &&
+         (e->wnorm = dev_alloc<float>(static_cast<size_t>(V), own)) &&
+         (e->xnorm = dev_alloc<float>(B, own)) &&
          (e->tokens = dev_alloc<int>(B * (max_seq + 1), own)) &&
          (e->rope = dev_alloc<float2>(static_cast<size_t>(max_seq) * (hd / 2), own)) &&
          (e->cur_rope = dev_alloc<float2>(B * (hd / 2), own)) &&
@@ -3745,12 +3818,15 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
         return invalid("%s: device allocation failed", fn);
     }
     (void)nh;
-    // the LM head's dynamic LDS (8 normalised vectors + staged logits) may
-    // exceed 64 KB (96 KB at hidden 2560)
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(e->lm_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(lm_head_batch_lds(H))) != hipSuccess ||
-        gemm_prepare() != 0 || gemm_sink_prepare() != 0) {
+    if (gemm_prepare() != 0 || gemm_sink_prepare() != 0) {
+        delete e;
+        return launch_status(fn);
+    }
+    // the LM-head rows' norms for the error bounds (the table is the model's,
+    // unchanged while the engine lives)
+    hipLaunchKernelGGL(lm_row_norm_kernel, dim3((V + 3) / 4), dim3(256), 0, nullptr, e->lm_head,
+                       e->wnorm, V, H);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         delete e;
         return launch_status(fn);
     }

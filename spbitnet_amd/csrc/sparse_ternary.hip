@@ -226,6 +226,23 @@ extern "C" int spb_sparse_ternary_gemv(const uint32_t* meta, const uint32_t* val
     return launch_status(fn);
 }
 
+extern "C" int spb_sparse_ternary_gemv_resident(const uint32_t* meta, const uint32_t* values,
+                                                const int8_t* x, int32_t* y, int rows, int cols,
+                                                int ms, int vs, spb_stream_t stream) {
+    clear_error();
+    const char* fn = "spb_sparse_ternary_gemv_resident";
+    if (int e = check_weights(fn, meta, values, rows, cols, ms, vs)) return e;
+    if (rows == 0 || cols == 0) return 0;
+    if (!x || !y) return invalid("%s: null activation or output pointer", fn);
+    const Weights wt{meta, values, rows, cols, ms, vs};
+    if (bitplane_ok(meta, values, cols, ms, vs) && aligned(x, 16))
+        launch_stream<BuildPlanes<Int8Src>, Int32Sink, kResidentLoadPolicy>(
+            wt, BuildPlanes<Int8Src>{Int8Src{x}}, Int32Sink{y}, as_stream(stream));
+    else
+        launch_general(wt, Int8Src{x}, Int32Sink{y}, as_stream(stream));
+    return launch_status(fn);
+}
+
 extern "C" int spb_sparse_ternary_gemv_planes(const uint32_t* meta, const uint32_t* values,
                                               const uint32_t* planes, int32_t* y, int rows,
                                               int cols, int ms, int vs, spb_stream_t stream) {

@@ -67,15 +67,19 @@ def sparse_ternary_unpack_gpu(meta, values, out, rows, cols, meta_row_stride,
 
 
 def sparse_ternary_gemv_gpu(meta, values, x, y, rows, cols, meta_row_stride,
-                            values_row_stride, stream=None):
-    """reference src/kernels/sparse_ternary.cu:256-272 (int8 x -> int32 y)"""
+                            values_row_stride, stream=None, resident=False):
+    """reference src/kernels/sparse_ternary.cu:256-272 (int8 x -> int32 y).
+    resident=True loads the weights on the default cache policy
+    (spb_sparse_ternary_gemv_resident: matrices that stay in the Infinity
+    Cache between calls) instead of the streaming one."""
     pm, pv = _weights(meta, values, rows, cols, meta_row_stride, values_row_stride)
     empty = rows == 0 or cols == 0
     px = _dev(x, "x", torch.int8, 0 if empty else cols)
     py = _dev(y, "y", torch.int32, 0 if empty else rows)
-    _lib.check(_lib.load().spb_sparse_ternary_gemv(pm, pv, px, py, rows, cols, meta_row_stride,
-                                                   values_row_stride, _stream_ptr(stream)),
-               "sparse_ternary_gemv_gpu")
+    L = _lib.load()
+    fn = L.spb_sparse_ternary_gemv_resident if resident else L.spb_sparse_ternary_gemv
+    _lib.check(fn(pm, pv, px, py, rows, cols, meta_row_stride, values_row_stride,
+                  _stream_ptr(stream)), "sparse_ternary_gemv_gpu")
 
 
 def fused_sparse_bitlinear_gpu(meta, values, x, output, d_absmax, gamma, rows, cols,

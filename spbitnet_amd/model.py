@@ -536,3 +536,18 @@ class BatchInferenceEngine:
         """Enqueue `steps` more batched steps (no host synchronisation)."""
         _lib.check(self._L.spb_batch_engine_decode_steps(self._h, int(steps)),
                    "spb_batch_engine_decode_steps")
+
+    def last_logits(self) -> torch.Tensor:
+        """A copy of the last step's float32 logits, [batch][vocab].  Each
+        sequence's argmax row holds the bs=1 engine's value bit for bit; the
+        other rows are the matrix-core products, within the LM head's error
+        bound of it (spb_batch_engine_create in csrc/engine.hip)."""
+        lp = ctypes.c_void_p()
+        _lib.check(self._L.spb_batch_engine_buffers(self._h, ctypes.byref(lp), None),
+                   "spb_batch_engine_buffers")
+        V = self.model.config.vocab_size
+        out = torch.empty((self.batch, V), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        _lib.memcpy_d2d(out.data_ptr(), lp.value, out.numel() * 4, None)
+        torch.cuda.synchronize()
+        return out

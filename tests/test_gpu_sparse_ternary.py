@@ -93,6 +93,19 @@ def test_gemv_config_shapes(gpu, rows, cols):
     assert (y == O.gemv(L.meta, L.values, x, rows, cols)).all()
 
 
+@pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (333, 384), (9, 36)])
+def test_gemv_resident_policy(gpu, rows, cols):
+    """spb_sparse_ternary_gemv_resident (default cache policy for the weight
+    loads) gives the drop-in GEMV's exact products, on both kernels."""
+    L = W.random_layer(rows, cols, W.seed_for("resident", rows, cols))
+    x = np.random.default_rng(rows + cols).integers(-128, 128, cols).astype(np.int8)
+    d_y = torch.full((rows,), -7, dtype=torch.int32, device=gpu)
+    K.sparse_ternary_gemv_gpu(dev_u32(L.meta, gpu), dev_u32(L.values, gpu), dev(x, gpu), d_y,
+                              rows, cols, L.meta_stride, L.values_stride, resident=True)
+    torch.cuda.synchronize()
+    assert (d_y.cpu().numpy() == O.gemv(L.meta, L.values, x, rows, cols)).all()
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 128), (7, 256), (333, 384), (1025, 128), (3, 4),
                                        (5, 8), (9, 36), (64, 100), (130, 132), (31, 2564),
                                        (97, 32768), (1501, 16384), (777, 4992)])
