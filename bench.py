@@ -226,6 +226,8 @@ def main() -> int:
     ap.add_argument("--only-mall-resident", action="store_true",
                     help="profiling: run only the Infinity-Cache-resident GEMV protocol "
                          "(for a rocprofv3 FETCH_SIZE pass) and print its timings")
+    ap.add_argument("--only-decode", action="store_true",
+                    help="profiling: run only the end-to-end decode measurements and print them")
     ap.add_argument("--only-gemm", action="store_true",
                     help="profiling: run only the config-2 batched GEMMs and print their timings")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -264,8 +266,8 @@ def main() -> int:
     B = Bench(args)
     dev, stream, log, ev = B.dev, B.stream, B.log, B.ev
 
-    if args.only_batch_decode:
-        print(json.dumps(decode_runs(B, args, batch_only=True)), flush=True)
+    if args.only_batch_decode or args.only_decode:
+        print(json.dumps(decode_runs(B, args, batch_only=args.only_batch_decode)), flush=True)
         return 0
 
     log("generating weights")
@@ -795,10 +797,11 @@ def decode_runs(B, args, batch_only=False):
             torch.cuda.synchronize()
             runs.append(a.elapsed_time(b))
         ms = sorted(runs)[1]
-        toks = eng.generate(prompts[:2], 8, stop_at_eos=False)
-        # the same two sequences decoded alone by the bs=1 engine
+        toks = eng.generate(prompts, n, stop_at_eos=False)
+        # two sequences decoded alone by the bs=1 engine
         one = InferenceEngine(model, max_seq=4096)
-        same = all(one.generate(prompts[b], 8, stop_at_eos=False) == toks[b] for b in range(2))
+        same = all(one.generate(prompts[b], n, stop_at_eos=False) == toks[b]
+                   for b in (0, bsz - 1))
         one.close()
         kv = kv_bytes_per_position(cfg) * sum(2048 + i for i in range(n)) / n  # per sequence
         r = {"model": desc, "batch": bsz, "max_seq": 4096, "prompt_tokens": 2048,
@@ -809,10 +812,20 @@ def decode_runs(B, args, batch_only=False):
              "prefill_ms": round(sorted(pre)[1], 1),
              "prefill_tok_per_s": round(bsz * 2047 / (sorted(pre)[1] * 1e-3), 1),
              "tokens_equal_bs1_engine": same}
-        gold = golden.get("config4_bs1")
-        if gold is not None and gold["prompt_len"] == 2048:
-            r["oracle_tokens_match"] = toks[0] == gold["tokens"][:8]
-            r["oracle_tokens_checked"] = 8
+        # every sequence of the batch with committed oracle tokens (sequence 0
+        # is config4_bs1's prompt; sequence b > 0 is config4_seq{4000 + b})
+        checked, match = [], True
+        for b in range(bsz):
+            gold = golden.get("config4_bs1" if b == 0 else f"config4_seq{4000 + b}")
+            if gold is None or gold["prompt_len"] != 2048:
+                continue
+            m = min(len(gold["tokens"]), len(toks[b]))
+            match = match and toks[b][:m] == gold["tokens"][:m]
+            checked.append(b)
+        if checked:
+            r["oracle_tokens_match"] = match
+            r["oracle_tokens_checked"] = min(n, 128)
+            r["oracle_sequences_checked"] = checked
         B.log(f"decode config4 batch {bsz}: {r['tok_per_s']} tok/s")
         eng.close()
         torch.cuda.empty_cache()
@@ -969,16 +982,29 @@ def pmc_summary(d):
     # fetches from the fabric, whether the Infinity Cache or HBM serves them:
     # it shows that each launch moves its algorithmic bytes once; the
     # residency itself shows in the launch time.
-    if glob.glob(os.path.join(d, "mall", "**", "*.db"), recursive=True):
-        mall = per_kernel("mall", "FETCH_SIZE", "gemv_stream_kernel")
+    mdbs = glob.glob(os.path.join(d, "mall", "**", "*.db"), recursive=True)
+    if mdbs:
+        import re
+        c = sqlite3.connect(mdbs[0])
+        rows = c.execute("select kernel_name, value, lds_block_size from counters_collection "
+                         "where counter_name='FETCH_SIZE'").fetchall()
+        mall = collections.defaultdict(list)
+        for kn, v, lds in rows:
+            if "gemv_stream_kernel" not in kn:
+                continue
+            pol = re.findall(r",\s*(\d+)\s*>\s*\(", kn)  # the load policy: last template argument
+            name = {"2": "nt", "0": "default"}.get(pol[-1] if pol else "", "?")
+            mall[f"lds{lds}_{name}"].append(v)
         out["mall_resident"] = {
             "command": "rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_stream/mall -o m -- python3 "
                        "-u bench.py --only-mall-resident",
-            "algorithmic_bytes": {"6912x2560x48": gemv_bytes(6912 * 48, 2560),
-                                  "2560x6912x48": gemv_bytes(2560 * 48, 6912)},
-            "per_launch": {f"lds{lds}": {"dispatches": len(v),
-                                          "fetch_bytes": int(sum(v) / len(v) * fs * 1024)}
-                           for lds, v in sorted(mall.items())}}
+            "algorithmic_bytes": {f"{shape}x{nc}": gemv_bytes(r * nc, k)
+                                  for shape, r, k in (("6912x2560", 6912, 2560),
+                                                      ("2560x6912", 2560, 6912))
+                                  for nc in (48, 24)},
+            "per_launch": {key: {"dispatches": len(v),
+                                 "fetch_bytes": int(sum(v) / len(v) * fs * 1024)}
+                           for key, v in sorted(mall.items())}}
         out["commands"].insert(4, out["mall_resident"]["command"])
     with open(PMC_JSON, "w") as fh:
         json.dump(out, fh, indent=1)

@@ -140,6 +140,42 @@ def test_engine_forward_logits_bit_exact(gpu):
     eng.close()
 
 
+def test_engine_tied_and_dominant_inputs(gpu):
+    """Embedding rows whose elements all have the same magnitude (every
+    element ties for the absmax of layer 0's q/k/v prologue) and rows with
+    one dominant element: logits bit-identical to the oracle on every step of
+    the decode engine, and the batched engine's tokens equal the oracle's."""
+    from spbitnet_amd.model import BatchInferenceEngine, InferenceEngine, Model
+    cfg = _small_config()
+    model = Model.random(cfg, seed=61)
+    H = cfg.hidden_size
+    emb = model.embed_tokens
+    for t in range(8):  # |x| all equal: every product ties
+        row = torch.full((H,), 0.5, dtype=torch.float32)
+        row[1::2] = -0.5
+        emb[t] = row.to(torch.bfloat16).to(emb.device)
+    for t in range(8, 16):  # one dominant element, the rest small and distinct
+        row = torch.linspace(-0.01, 0.01, H)
+        row[(t * 37) % H] = 1.5 if t % 2 else -1.5
+        emb[t] = row.to(torch.bfloat16).to(emb.device)
+    torch.cuda.synchronize()
+    eng = InferenceEngine(model, max_seq=64)
+    ora = O.EngineOracle(model.to_host(), 64)
+    toks = [3, 9, 0, 12, 7, 15, 1, 8, 5, 14, 2, 11]
+    for i, t in enumerate(toks):
+        print(f"shortcut step {i} token {t}", flush=True)
+        got = eng.forward(t).cpu().numpy()
+        _, want = ora.step(t)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"step {i}"
+    eng.close()
+    beng = BatchInferenceEngine(model, max_seq=64, batch=3)
+    prompts = [toks[:4], toks[4:9], toks[9:]]
+    got = beng.generate(prompts, 6, stop_at_eos=False)
+    beng.close()
+    host = model.to_host()
+    assert got == [O.EngineOracle(host, 64).generate(p, 6) for p in prompts]
+
+
 def test_engine_greedy_128_matches_oracle(gpu):
     cfg = _small_config()
     model, eng, ora = _engine_pair(cfg, seed=3, max_seq=256)
@@ -389,6 +425,74 @@ def test_engine_bitnet_2b4t_greedy_128_golden(gpu):
     eng.close()
     print("oracle: 4 live steps", flush=True)
     assert O.EngineOracle(model.to_host(), 64).generate(prompt, 4) == got[:4]
+
+
+def _bench_prompt(cfg, n, seed):
+    """bench.py's prompts: BOS + n - 1 ids from numpy default_rng(seed)."""
+    return [cfg.bos_token_id] + _prompt(n - 1, cfg.vocab_size, seed)
+
+
+def test_engine_bitnet_2b4t_config4_bs1_golden(gpu):
+    """Config 4 at full shape and batch 1: the 2.4B-parameter model, a
+    2048-token prompt into a 4096-position cache (the batched prefill), then
+    128 greedy steps past position 2048 (33-35 attention splits, the
+    separate split-combine kernel), tokens equal to the oracle's (committed
+    by tests/golden/make_decode_golden.py on the host-generated copy of the
+    same weights)."""
+    import json
+    from spbitnet_amd.model import InferenceEngine, Model, ModelConfig
+    gold = json.load(open(GOLDEN_2B4T))["config4_bs1"]
+    cfg = ModelConfig.bitnet_b158_2b4t()
+    print("generating the 2.4B-parameter random model", flush=True)
+    model = Model.random(cfg, seed=2025)
+    prompt = _bench_prompt(cfg, gold["prompt_len"], gold["prompt_seed"])
+    assert len(prompt) == 2048 and len(gold["tokens"]) == 128
+    eng = InferenceEngine(model, max_seq=gold["max_seq"])
+    print("config 4 bs=1: prefill + 128 steps", flush=True)
+    assert eng.generate(prompt, 128, stop_at_eos=False) == gold["tokens"]
+    eng.close()
+
+
+def test_batch_engine_bitnet_2b4t_config4_b32_golden(gpu):
+    """Config 4 at full shape and batch 32: bench.py's 32 prompts of 2048
+    tokens (sequence 0 from seed 2025, sequence b from seed 4000 + b) in
+    4096-position caches, 128 greedy steps on the batched engine.  Every
+    sequence with committed oracle tokens (0, 17, 31, and 7 when present)
+    equals them for all 128 steps; four more sequences equal the bs=1
+    engine's generate; and sequence 0's logits of the last step match the bs=1
+    engine's (argmax row bit for bit, every row within 1e-3 of the largest)."""
+    import json
+    from spbitnet_amd.model import BatchInferenceEngine, InferenceEngine, Model, ModelConfig
+    gold = json.load(open(GOLDEN_2B4T))
+    slots = {0: gold["config4_bs1"]}
+    for b in (7, 17, 31):
+        g = gold.get(f"config4_seq{4000 + b}")
+        if g is not None:
+            slots[b] = g
+    assert len(slots) >= 3
+    cfg = ModelConfig.bitnet_b158_2b4t()
+    print("generating the 2.4B-parameter random model", flush=True)
+    model = Model.random(cfg, seed=2025)
+    prompts = [_bench_prompt(cfg, 2048, 2025 if b == 0 else 4000 + b) for b in range(32)]
+    beng = BatchInferenceEngine(model, max_seq=4096, batch=32)
+    print("batch 32: prefill + 128 steps", flush=True)
+    got = beng.generate(prompts, 128, stop_at_eos=False)
+    blog = beng.last_logits()[0].cpu().numpy()
+    beng.close()
+    torch.cuda.empty_cache()
+    for b, g in slots.items():
+        assert got[b] == g["tokens"], f"sequence {b}"
+    eng = InferenceEngine(model, max_seq=4096)
+    print("bs=1 engine: sequences 0, 5, 12, 24, 30", flush=True)
+    for b in (5, 12, 24, 30):
+        assert eng.generate(prompts[b], 128, stop_at_eos=False) == got[b], f"sequence {b}"
+    eng.generate(prompts[0], 127, stop_at_eos=False)
+    one = eng.forward(got[0][126]).cpu().numpy()
+    eng.close()
+    tok = got[0][127]
+    assert int(np.argmax(one)) == tok
+    assert blog[tok].view(np.uint32) == one[tok].view(np.uint32)
+    assert np.abs(blog - one).max() <= 1e-3 * np.abs(one).max()
 
 
 def test_full_width_long_context(gpu):

@@ -153,3 +153,14 @@ def test_gemm_staged_unaligned_output(gpu):
     out = buf.cpu().numpy()
     assert out[0] == -7 and (out[1 + n * rows:] == -7).all()
     assert (out[1:1 + n * rows].reshape(n, rows) == expected(L, X)).all()
+
+
+@pytest.mark.parametrize("rows,cols,n", [(640, 2560, 40), (3840, 2560, 32), (100, 1024, 50),
+                                         (130, 2304, 17), (64, 256, 64), (6912, 2560, 64)])
+def test_gemm_n17_to_64_tiles(gpu, rows, cols, n):
+    """17-64 tokens (the 64-row x 32-token staged tile) on rows of at most
+    2560 columns: full and partial column pairs, rows that end inside a row
+    block, batches that end inside a token tile."""
+    L = W.random_layer(rows, cols, W.seed_for("gemm-n17-64", rows, cols, n))
+    X = np.random.default_rng(rows + 5 * cols + n).integers(-128, 128, (n, cols)).astype(np.int8)
+    assert (run(L, X, gpu) == expected(L, X)).all()
