@@ -49,6 +49,7 @@ constexpr int kAttnSplit = 64;    // positions per attention split (one per lane
 constexpr int kAttnThreads = 256;
 constexpr int kAttnBucketSplits = 4;  // splits per position bucket of the decode graphs
 constexpr int kPrefillChunk = 1024;      // prompt tokens per batched-prefill pass (at most)
+constexpr int kGemmSplitCounters = 1024;  // split-K tile counters of a batch engine (split launches have at most CUs / 2 tiles)
 constexpr long kPrefillPartialBytes = 1L << 30;  // split partials of one pass (at most)
 constexpr int kPrefillMinDefault = 16;   // prompt tokens before the last that switch to it
 constexpr int kAttnMaxGroup = 8;  // q heads per kv head
@@ -2902,11 +2903,12 @@ constexpr int kFuseTokens = 64;
 template <class Sink>
 hipError_t gemm_sink(const spb_sparse_linear* const* w, int nw, const int8_t* X,
                      const float* amax, const Sink& sink, long stride, int32_t* const* y, int n,
-                     hipStream_t s) {
+                     hipStream_t s, const GemmSplit* split = nullptr) {
     int rows = 0;
     for (int i = 0; i < nw; ++i) rows += w[i]->rows;
     if (n <= kFuseTokens || SinkFusesWide<Sink>::value) {
-        const int rc = gemm_stacked_epi(w, nw, X, SinkOut<Sink>{sink, stride, amax, rows}, n, s);
+        const int rc =
+            gemm_stacked_epi(w, nw, X, SinkOut<Sink>{sink, stride, amax, rows}, n, s, split);
         if (rc == 0) return hipSuccess;
         if (rc == 2) return hipErrorLaunchFailure;
     }
@@ -3638,6 +3640,7 @@ struct spb_batch_engine {
     float2* rope = nullptr;               // [max_seq][head_dim / 2]
     float2* cur_rope = nullptr;           // [batch][head_dim / 2]
     EngineState* st = nullptr;            // [batch]
+    GemmSplit split{};                    // split-K workspace of the step's GEMMs
     std::vector<float2> rope_host;
     hipStream_t stream = nullptr;
     hipStream_t cap_stream = nullptr;
@@ -3692,7 +3695,7 @@ struct spb_batch_engine {
                 sink.rope_tab = nullptr;  // each sequence's own RoPE row (cur_rope)
                 sink.kv_stride = kv_seq;
                 if (gemm_sink(qkv3, 3, step.x, step.amax, sink, qrows + 2 * kvdim, step.y, B,
-                              s) != hipSuccess)
+                              s, &split) != hipSuccess)
                     return hipErrorLaunchFailure;
             }
             launch_attention_batch(hd, nh / nkv, S, nkv, B, s, step.qkv, kcache[l], vcache[l],
@@ -3706,7 +3709,8 @@ struct spb_batch_engine {
                 const spb_sparse_linear* o1[1] = {&L.o_proj};
                 SegBf16Sink sink{step.o, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma, H, H,
                                  0.f, 0.f, 0.f};
-                if (gemm_sink(o1, 1, step.x, step.amax, sink, H, step.y, B, s) != hipSuccess)
+                if (gemm_sink(o1, 1, step.x, step.amax, sink, H, step.y, B, s, &split) !=
+                    hipSuccess)
                     return hipErrorLaunchFailure;
             }
             {
@@ -3718,7 +3722,7 @@ struct spb_batch_engine {
                 const spb_sparse_linear* gu2[2] = {&L.gate_proj, &L.up_proj};
                 SegBf16Sink sink{step.gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
                                  I, 2 * I, 0.f, 0.f, 0.f};
-                if (gemm_sink(gu2, 2, step.x, step.amax, sink, 2 * I, step.y, B, s) !=
+                if (gemm_sink(gu2, 2, step.x, step.amax, sink, 2 * I, step.y, B, s, &split) !=
                     hipSuccess)
                     return hipErrorLaunchFailure;
             }
@@ -3732,7 +3736,8 @@ struct spb_batch_engine {
             {
                 const spb_sparse_linear* d1[1] = {&L.down_proj};
                 ResidualSink sink{step.r, step.r2, L.down_proj.gamma, 0.f};
-                if (gemm_sink(d1, 1, step.x, step.amax, sink, H, step.y, B, s) != hipSuccess)
+                if (gemm_sink(d1, 1, step.x, step.amax, sink, H, step.y, B, s, &split) !=
+                    hipSuccess)
                     return hipErrorLaunchFailure;
             }
         }
@@ -3813,11 +3818,23 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
          (e->rope = dev_alloc<float2>(static_cast<size_t>(max_seq) * (hd / 2), own)) &&
          (e->cur_rope = dev_alloc<float2>(B * (hd / 2), own)) &&
          (e->st = dev_alloc<EngineState>(B, own));
+    // split-K workspace of the step's GEMMs (q|k|v, o, gate|up, down over the
+    // batch's tokens) and one counter per row x token tile
+    {
+        const int I = cfg->intermediate_size;
+        const int rows_h[3] = {nh * hd + 2 * nkv * hd, H, 2 * I};
+        const long w_h = staged_split_words(rows_h, 3, H, batch);
+        const long w_i = staged_split_words(&rows_h[1], 1, I, batch);
+        e->split.part_words = w_h > w_i ? w_h : w_i;
+        e->split.count_words = kGemmSplitCounters;
+        if (e->split.part_words > 0)
+            ok = ok && (e->split.part = dev_alloc<int32_t>(e->split.part_words, own)) &&
+                 (e->split.count = dev_alloc<unsigned>(kGemmSplitCounters, own));
+    }
     if (!ok) {
         delete e;
         return invalid("%s: device allocation failed", fn);
     }
-    (void)nh;
     if (gemm_prepare() != 0 || gemm_sink_prepare() != 0) {
         delete e;
         return launch_status(fn);
@@ -3839,6 +3856,8 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
     }
     if (err == hipSuccess) err = hipMemset(e->st, 0, B * sizeof(EngineState));
     if (err == hipSuccess) err = hipMemset(e->tokens, 0, B * (max_seq + 1) * sizeof(int));
+    if (err == hipSuccess && e->split.count)  // the split-K tile counters start (and end) at 0
+        err = hipMemset(e->split.count, 0, kGemmSplitCounters * sizeof(unsigned));
     if (err == hipSuccess) err = hipStreamCreateWithFlags(&e->cap_stream, hipStreamNonBlocking);
     if (err != hipSuccess) {
         delete e;

@@ -34,6 +34,23 @@ struct GemmSegs {
     int end0, end1;
 };
 
+// Split-K (engines' decode GEMMs whose row tiles leave most CUs idle): the
+// chunks of K split over gridDim.z blocks per tile.  Each block writes its
+// partial tile to part with write-through stores (cache policy sc1), waits
+// for them, and counts itself in the tile's counter; the block that counts
+// last reads the partials back with sc1 loads (past the per-XCD L2s, which
+// do not see each other's writes), adds them in z order (exact int32) and
+// runs the epilogue, then clears the counter for the next launch.  part
+// holds [tile][z][WS x S x T][64 lanes] x 4 int32; count one zeroed word per
+// tile (blockIdx.y * gridDim.x + blockIdx.x).
+struct GemmSplit {
+    int32_t* part;
+    unsigned* count;
+    long part_words;   // int32 capacity of part
+    int count_words;   // capacity of count
+};
+constexpr int kCachePolicySc1 = 16;  // buffer-op cache policy: agent-coherent (sc1)
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -140,11 +157,11 @@ struct StagedTile {
     }
 };
 
-template <int S, int T, int WS, int KW, int KCP, class Epi>
+template <int S, int T, int WS, int KW, int KCP, class Epi, bool kSplit = false>
 __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
     const uint32_t* __restrict__ meta, const uint32_t* __restrict__ values,
     const int8_t* __restrict__ X, Epi epi, int rows, int cols, int n, int ms, int vs,
-    GemmSegs segs) {
+    GemmSegs segs, GemmSplit sk) {
     using P = StagedTile<S, T, WS, KW, KCP>;
     extern __shared__ __align__(16) uint8_t gemm_smem[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -160,6 +177,13 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
     }
     const int npairs = cols >> 8;
     const int nch = (npairs + KCP - 1) / KCP;
+    // this block's chunks: all of them, or split-K part blockIdx.z
+    int c_begin = 0, c_end = nch;
+    if constexpr (kSplit) {
+        const int cpb = (nch + gridDim.z - 1) / gridDim.z;
+        c_begin = blockIdx.z * cpb;
+        c_end = min(nch, c_begin + cpb);
+    }
     // Block-relative buffer resources: rows and tokens past the matrix read
     // zeros (their results are not stored); columns past the end in the last
     // chunk read other in-range bytes or zeros and feed only masked steps.
@@ -251,12 +275,12 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[s][t] = (v4i){0, 0, 0, 0};
 
-    load_chunk(0);
+    load_chunk(c_begin);
     store_chunk(0);
     __syncthreads();
-    for (int c = 0; c < nch; ++c) {
-        if (c + 1 < nch) load_chunk(c + 1);  // in flight during this chunk's steps
-        const uint8_t* base = gemm_smem + (c & 1) * P::kBufBytes;
+    for (int c = c_begin; c < c_end; ++c) {
+        if (c + 1 < c_end) load_chunk(c + 1);  // in flight during this chunk's steps
+        const uint8_t* base = gemm_smem + ((c - c_begin) & 1) * P::kBufBytes;
         const uint32_t* am = reinterpret_cast<const uint32_t*>(base);
         const uint32_t* av = am + 8 * KCP * P::RBM;
         const u32x4v* bb = reinterpret_cast<const u32x4v*>(base + P::kABytes);
@@ -307,7 +331,7 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
                                                                            idx[s], 0, 0);
             }
         }
-        if (c + 1 < nch) store_chunk((c + 1) & 1);  // that buffer was last read a chunk ago
+        if (c + 1 < c_end) store_chunk((c + 1 - c_begin) & 1);  // that buffer was last read a chunk ago
         __syncthreads();
     }
     // split-K sum: every wave parks its partials; wave kw adds up and stores
@@ -329,6 +353,46 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
 #pragma unroll
                     for (int k = 1; k < KW; ++k)
                         sum += red[((k * WS + ws) * S * T + s * T + t) * kWave + lane];
+                    acc[s][t] = sum;
+                }
+    }
+    if constexpr (kSplit) {
+        // the flag goes in the (no longer read) LDS of the K-way sums: a static
+        // LDS variable would lower the dynamic limit below the CU's LDS
+        int& last_part = *reinterpret_cast<int*>(gemm_smem);
+        const int tile = blockIdx.y * gridDim.x + blockIdx.x, ks = gridDim.z;
+        // v4i slot of (tile, z, ws, s, t, lane); the extent ends the buffer
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+            sk.part, static_cast<short>(0), static_cast<int>(sk.part_words * 4), kRawBufferFlags);
+        auto slot = [&](int z, int s, int t) {
+            return (((static_cast<int>(tile) * ks + z) * WS + ws) * S * T + s * T + t) * kWave + lane;
+        };
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+                if (KW == 1 || (s * T + t) % KW == kw)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4v, acc[s][t]), rp, slot(blockIdx.z, s, t) * 16, 0,
+                        kCachePolicySc1);
+        __builtin_amdgcn_s_waitcnt(0);  // the partial stores are complete
+        __syncthreads();
+        if (tid == 0)
+            last_part = __hip_atomic_fetch_add(sk.count + tile, 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(ks - 1);
+        __syncthreads();
+        if (!last_part) return;  // uniform
+        if (tid == 0) __hip_atomic_store(sk.count + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+                if (KW == 1 || (s * T + t) % KW == kw) {
+                    v4i sum = (v4i){0, 0, 0, 0};
+                    for (int z = 0; z < ks; ++z)
+                        sum += __builtin_bit_cast(
+                            v4i, __builtin_amdgcn_raw_buffer_load_b128(rp, slot(z, s, t) * 16, 0,
+                                                                       kCachePolicySc1));
                     acc[s][t] = sum;
                 }
     }
@@ -368,48 +432,103 @@ enum StagedShape { kStagedN16, kStagedN64, kStagedWide };
 StagedShape staged_shape(int n) { return n <= 16 ? kStagedN16 : (n <= 64 ? kStagedN64 : kStagedWide); }
 int staged_row_block(int n) { return n <= 16 ? 32 : 64; }
 
-template <int S, int T, int WS, int KW, int KCP, class Epi>
+template <int S, int T, int WS, int KW, int KCP, class Epi, bool kSplit = false>
 const void* staged_fn() {
-    return reinterpret_cast<const void*>(&gemm_smfmac_kernel<S, T, WS, KW, KCP, Epi>);
+    return reinterpret_cast<const void*>(&gemm_smfmac_kernel<S, T, WS, KW, KCP, Epi, kSplit>);
+}
+
+// Split-K parts for a launch of `tiles` row x token tiles over nch chunks:
+// only for long rows (at least kSplitMinChunks chunks) whose tiles fill at
+// most half the CUs; enough parts to reach about one block per CU, at least
+// two chunks each (1: no split).  Measured on the 2.4B model's batch-32
+// decode step: the down projection (14 chunks, 40 tiles) went from 15.2 to
+// 10.3 us in 7 parts, while the 5-chunk q|k|v and o launches got slower
+// (9.5 -> 10.8 and 7.2 -> 7.7 us): the partials' round trip through memory
+// and the last block's sum cost more than their shorter chunk loops saved.
+constexpr int kSplitMinChunks = 6;
+int staged_split_parts(long tiles, int nch) {
+    const long cus = device_cu_count();
+    if (nch < kSplitMinChunks || 2 * tiles > cus) return 1;
+    int ks = static_cast<int>((cus + tiles - 1) / tiles);
+    if (ks > nch / 2) ks = nch / 2;
+    const int cpb = (nch + ks - 1) / ks;
+    return (nch + cpb - 1) / cpb;
 }
 
 template <int S, int T, int WS, int KW, int KCP, class Epi>
 int launch_staged(const uint32_t* meta, const uint32_t* values, const int8_t* X, const Epi& epi,
-                  int rows, int cols, int n, int ms, int vs, hipStream_t st, const GemmSegs& segs) {
+                  int rows, int cols, int n, int ms, int vs, hipStream_t st, const GemmSegs& segs,
+                  const GemmSplit* split = nullptr) {
     using P = StagedTile<S, T, WS, KW, KCP>;
     const int nch = (cols / 256 + KCP - 1) / KCP;
     const int lds = P::lds_bytes(nch);
-    if (lds > 65536 &&
-        (lds > device_lds_per_cu() || !gemm_allow_lds(staged_fn<S, T, WS, KW, KCP, Epi>())))
-        return invalid("spb_sparse_ternary_gemm: %d bytes of LDS unavailable", lds);
     const dim3 grid((rows + P::RB - 1) / P::RB, (n + P::TB - 1) / P::TB);
-    hipLaunchKernelGGL((gemm_smfmac_kernel<S, T, WS, KW, KCP, Epi>), grid, dim3(P::NT), lds, st,
-                       meta, values, X, epi, rows, cols, n, ms, vs, segs);
+    const long tiles = static_cast<long>(grid.x) * grid.y;
+    int ks = split ? staged_split_parts(tiles, nch) : 1;
+    // a workspace too small for this launch runs it unsplit
+    if (ks > 1 && (tiles > split->count_words ||
+                   tiles * ks * P::RB * P::TB > split->part_words))
+        ks = 1;
+    const void* fn = ks > 1 ? staged_fn<S, T, WS, KW, KCP, Epi, true>()
+                            : staged_fn<S, T, WS, KW, KCP, Epi, false>();
+    if (lds > 65536 && (lds > device_lds_per_cu() || !gemm_allow_lds(fn)))
+        return invalid("spb_sparse_ternary_gemm: %d bytes of LDS unavailable", lds);
+    if (ks > 1) {
+        hipLaunchKernelGGL((gemm_smfmac_kernel<S, T, WS, KW, KCP, Epi, true>),
+                           dim3(grid.x, grid.y, ks), dim3(P::NT), lds, st, meta, values, X, epi,
+                           rows, cols, n, ms, vs, segs, *split);
+    } else {
+        hipLaunchKernelGGL((gemm_smfmac_kernel<S, T, WS, KW, KCP, Epi, false>), grid, dim3(P::NT),
+                           lds, st, meta, values, X, epi, rows, cols, n, ms, vs, segs,
+                           GemmSplit{nullptr, nullptr, 0, 0});
+    }
     return 0;
 }
 
 // The staged launch for n tokens (the tile of staged_shape); the caller has
-// checked staged_ok.
+// checked staged_ok.  split: the caller's split-K workspace, or null.
 template <class Epi>
 int launch_staged_for(const uint32_t* meta, const uint32_t* values, const int8_t* X,
                       const Epi& epi, int rows, int cols, int n, int ms, int vs, hipStream_t st,
-                      const GemmSegs& g) {
+                      const GemmSegs& g, const GemmSplit* split = nullptr) {
     switch (staged_shape(n)) {
         case kStagedN16:
-            return launch_staged<1, 1, 2, 4, 10>(meta, values, X, epi, rows, cols, n, ms, vs, st, g);
+            return launch_staged<1, 1, 2, 4, 10>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
+                                                 split);
         case kStagedN64:
-            return launch_staged<2, 2, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g);
+            return launch_staged<2, 2, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
+                                                split);
         default:
-            return launch_staged<2, 4, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g);
+            return launch_staged<2, 4, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
+                                                split);
     }
 }
 
-// Raises the LDS limit of the three staged tiles with epilogue Epi (0 = done).
+// Split-K workspace (int32 words of part) that launches of up to n tokens
+// on these row counts and columns need at most.
+long staged_split_words(const int* rows, int nrows, int cols, int n) {
+    const int rb = staged_row_block(n), tb = n <= 16 ? 16 : (n <= 64 ? 32 : 64);
+    const int kcp = n <= 16 ? 10 : 2;
+    const int nch = (cols / 256 + kcp - 1) / kcp;
+    long words = 0;
+    for (int i = 0; i < nrows; ++i) {
+        const long tiles = static_cast<long>((rows[i] + rb - 1) / rb) * ((n + tb - 1) / tb);
+        const long w = tiles * staged_split_parts(tiles, nch) * rb * tb;
+        if (w > words) words = w;
+    }
+    return words;
+}
+
+// Raises the LDS limit of the three staged tiles with epilogue Epi, unsplit
+// and split (0 = done).
 template <class Epi>
 int staged_prepare() {
     return gemm_allow_lds(staged_fn<1, 1, 2, 4, 10, Epi>()) &&
                    gemm_allow_lds(staged_fn<2, 2, 2, 4, 2, Epi>()) &&
-                   gemm_allow_lds(staged_fn<2, 4, 2, 4, 2, Epi>())
+                   gemm_allow_lds(staged_fn<2, 4, 2, 4, 2, Epi>()) &&
+                   gemm_allow_lds(staged_fn<1, 1, 2, 4, 10, Epi, true>()) &&
+                   gemm_allow_lds(staged_fn<2, 2, 2, 4, 2, Epi, true>()) &&
+                   gemm_allow_lds(staged_fn<2, 4, 2, 4, 2, Epi, true>())
                ? 0
                : 1;
 }
@@ -443,7 +562,7 @@ struct Int32Out {
 // block's row tile; 2 on a launch error, 0 when launched.
 template <class Epi>
 int gemm_stacked_epi(const spb_sparse_linear* const* segs, int nseg, const int8_t* X,
-                     const Epi& epi, int n, hipStream_t st) {
+                     const Epi& epi, int n, hipStream_t st, const GemmSplit* split = nullptr) {
     if (nseg < 1 || nseg > 3 || n <= 0 || (n + 15) / 16 > 65535) return 1;
     const spb_sparse_linear& a = *segs[0];
     int rows = 0, ends[3] = {0, 0, 0};
@@ -479,7 +598,7 @@ int gemm_stacked_epi(const spb_sparse_linear* const* segs, int nseg, const int8_
     }
     if (nseg == 2) g.end1 = rows;
     if (launch_staged_for(a.meta, a.values, X, epi, rows, a.cols, n, a.meta_stride,
-                          a.values_stride, st, g))
+                          a.values_stride, st, g, split))
         return 2;
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }

@@ -101,6 +101,46 @@ def test_batch_decode_gqa_variants_and_eos(gpu):
         eng.close()
 
 
+@pytest.mark.parametrize("heads,kv,batch", [(8, 2, 17), (8, 1, 20), (4, 2, 16)])
+def test_batch_decode_split_k_head_dim_128(gpu, heads, kv, batch):
+    """Intermediate 3072 makes the down projection's rows 6 chunks long, so
+    its GEMM runs split over K (each part's partial tile written through to
+    memory, the last block of each tile adding them and running the residual
+    sink); head_dim 128 with GQA groups 4, 8 and 2 at 16-20 sequences.
+    Ragged prompts (1-300 tokens, 1-5 attention splits), EOS stops that
+    finish some sequences early, then a second generation with fewer
+    sequences than slots; tokens equal the oracle's single-sequence
+    generate."""
+    from spbitnet_amd.model import BatchInferenceEngine, Model
+    cfg = _cfg(hidden_size=heads * 128, num_attention_heads=heads, num_key_value_heads=kv,
+               head_dim=128, intermediate_size=3072, max_position_embeddings=512)
+    model = Model.random(cfg, seed=301 + heads + kv)
+    host = model.to_host()
+    prompts = _prompts(batch, cfg.vocab_size, 1, 300, seed=batch + heads)
+    prompts[1] = prompts[1][:1]
+    print(f"split-K G={heads // kv} batch {batch}: oracle", flush=True)
+    want = _oracle_tokens(host, 512, prompts, 12)
+    eng = BatchInferenceEngine(model, max_seq=512, batch=batch)
+    got = eng.generate(prompts, 12, stop_at_eos=False)
+    for b in range(batch):
+        assert got[b] == want[b], f"sequence {b} (prompt {len(prompts[b])})"
+    eng.close()
+    # EOS: the token sequence 0 generates at step 4 ends the sequences that
+    # produce it; the others run on
+    eos = want[0][4]
+    model.config = _cfg(hidden_size=heads * 128, num_attention_heads=heads,
+                        num_key_value_heads=kv, head_dim=128, intermediate_size=3072,
+                        max_position_embeddings=512, eos_token_id=eos)
+    eng = BatchInferenceEngine(model, max_seq=512, batch=batch)
+    got = eng.generate(prompts, 12, stop_at_eos=True)
+    for b in range(batch):
+        cut = want[b].index(eos) + 1 if eos in want[b] else 12
+        assert got[b] == want[b][:cut], f"sequence {b}"
+    again = eng.generate(prompts[: batch - 5], 6, stop_at_eos=False)
+    assert again == [w[:6] for w in want[: batch - 5]]
+    eng.close()
+
+
 def test_batch_engine_rejects_bad_input(gpu):
     from spbitnet_amd import _lib
     from spbitnet_amd.model import BatchInferenceEngine, Model
