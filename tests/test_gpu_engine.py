@@ -457,8 +457,8 @@ def test_batch_engine_bitnet_2b4t_config4_b32_golden(gpu):
     """Config 4 at full shape and batch 32: bench.py's 32 prompts of 2048
     tokens (sequence 0 from seed 2025, sequence b from seed 4000 + b) in
     4096-position caches, 128 greedy steps on the batched engine.  Every
-    sequence with committed oracle tokens (0, 17, 31, and 7 when present)
-    equals them for all 128 steps; four more sequences equal the bs=1
+    sequence with committed oracle tokens (0, 7, 17 and 31) equals them for
+    all 128 steps; four more sequences equal the bs=1
     engine's generate; and sequence 0's logits of the last step match the bs=1
     engine's (argmax row bit for bit, every row within 1e-3 of the largest)."""
     import json
@@ -469,7 +469,7 @@ def test_batch_engine_bitnet_2b4t_config4_b32_golden(gpu):
         g = gold.get(f"config4_seq{4000 + b}")
         if g is not None:
             slots[b] = g
-    assert len(slots) >= 3
+    assert len(slots) == 4
     cfg = ModelConfig.bitnet_b158_2b4t()
     print("generating the 2.4B-parameter random model", flush=True)
     model = Model.random(cfg, seed=2025)
