@@ -1973,15 +1973,19 @@ __global__ __launch_bounds__(kLmBlock) void lm_head_kernel(
                 b = wv[w];
                 bi = wi[w];
             }
-        part_v[blockIdx.x] = b;
-        part_i[blockIdx.x] = bi;
-        __threadfence();
-        const unsigned t = atomicAdd(&st->ticket, 1u);
+        // The partials go through to memory (agent-coherent stores, sc1) and
+        // are complete before the ticket counts this block, so the last
+        // block's agent-coherent loads see every block's; no fence (an L2
+        // write-back and invalidate per block) is needed.
+        __hip_atomic_store(&part_v[blockIdx.x], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&part_i[blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        const unsigned t =
+            __hip_atomic_fetch_add(&st->ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = t == gridDim.x - 1;
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     const int pos_old = st->pos;  // read before thread 0 advances it (barrier below)
     float b = -INFINITY;
     int bi = 0x7FFFFFFF;
