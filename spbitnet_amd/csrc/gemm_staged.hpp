@@ -429,8 +429,16 @@ bool staged_ok(const void* meta, const void* values, const void* X, int cols, in
 //   n > 64 : 64 rows x 64 tokens, 8 waves (2 row groups x 4 K ways), 78 KB
 // Kernels above 64 KB of LDS need their limit raised (gemm_prepare).
 enum StagedShape { kStagedN16, kStagedN64, kStagedWide };
-StagedShape staged_shape(int n) { return n <= 16 ? kStagedN16 : (n <= 64 ? kStagedN64 : kStagedWide); }
-int staged_row_block(int n) { return n <= 16 ? 32 : 64; }
+// Batches up to this size take the 32x16 tile (one chunk per 2560-column row,
+// the token tiles side by side).  At 32 tokens on the 2.4B model's decode
+// shapes it beat the 64x32 tile (more blocks, one memory round trip each:
+// 9,415 -> 9,750 tok/s at batch 32); at 64 tokens it lost (6912x2560: 10.5
+// against 5.6 us).
+constexpr int kStagedN16Max = 32;
+StagedShape staged_shape(int n) {
+    return n <= kStagedN16Max ? kStagedN16 : (n <= 64 ? kStagedN64 : kStagedWide);
+}
+int staged_row_block(int n) { return n <= kStagedN16Max ? 32 : 64; }
 
 template <int S, int T, int WS, int KW, int KCP, class Epi, bool kSplit = false>
 const void* staged_fn() {
@@ -441,10 +449,12 @@ const void* staged_fn() {
 // only for long rows (at least kSplitMinChunks chunks) whose tiles fill at
 // most half the CUs; enough parts to reach about one block per CU, at least
 // two chunks each (1: no split).  Measured on the 2.4B model's batch-32
-// decode step: the down projection (14 chunks, 40 tiles) went from 15.2 to
-// 10.3 us in 7 parts, while the 5-chunk q|k|v and o launches got slower
-// (9.5 -> 10.8 and 7.2 -> 7.7 us): the partials' round trip through memory
-// and the last block's sum cost more than their shorter chunk loops saved.
+// decode step on the 64x32 tile: the down projection (14 chunks, 40 tiles)
+// went from 15.2 to 10.3 us in 7 parts, while the 5-chunk q|k|v and o
+// launches got slower (9.5 -> 10.8 and 7.2 -> 7.7 us): the partials' round
+// trip through memory and the last block's sum cost more than their shorter
+// chunk loops saved.  (Batch 32 now takes the 32x16 tile, whose rows are at
+// most 3 chunks long; the split serves batches of 33-64 tokens.)
 constexpr int kSplitMinChunks = 6;
 int staged_split_parts(long tiles, int nch) {
     const long cus = device_cu_count();
@@ -507,8 +517,8 @@ int launch_staged_for(const uint32_t* meta, const uint32_t* values, const int8_t
 // Split-K workspace (int32 words of part) that launches of up to n tokens
 // on these row counts and columns need at most.
 long staged_split_words(const int* rows, int nrows, int cols, int n) {
-    const int rb = staged_row_block(n), tb = n <= 16 ? 16 : (n <= 64 ? 32 : 64);
-    const int kcp = n <= 16 ? 10 : 2;
+    const int rb = staged_row_block(n), tb = n <= kStagedN16Max ? 16 : (n <= 64 ? 32 : 64);
+    const int kcp = n <= kStagedN16Max ? 10 : 2;
     const int nch = (cols / 256 + kcp - 1) / kcp;
     long words = 0;
     for (int i = 0; i < nrows; ++i) {

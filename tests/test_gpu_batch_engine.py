@@ -101,12 +101,13 @@ def test_batch_decode_gqa_variants_and_eos(gpu):
         eng.close()
 
 
-@pytest.mark.parametrize("heads,kv,batch", [(8, 2, 17), (8, 1, 20), (4, 2, 16)])
+@pytest.mark.parametrize("heads,kv,batch", [(8, 2, 40), (8, 1, 36), (4, 2, 48)])
 def test_batch_decode_split_k_head_dim_128(gpu, heads, kv, batch):
-    """Intermediate 3072 makes the down projection's rows 6 chunks long, so
-    its GEMM runs split over K (each part's partial tile written through to
+    """At 33-64 sequences the GEMMs take the 64x32 tile (2-pair chunks), and
+    intermediate 3072 makes the down projection's rows 6 chunks long, so its
+    GEMM runs split over K (each part's partial tile written through to
     memory, the last block of each tile adding them and running the residual
-    sink); head_dim 128 with GQA groups 4, 8 and 2 at 16-20 sequences.
+    sink); head_dim 128 with GQA groups 4, 8 and 2 at 36-48 sequences.
     Ragged prompts (1-300 tokens, 1-5 attention splits), EOS stops that
     finish some sequences early, then a second generation with fewer
     sequences than slots; tokens equal the oracle's single-sequence
