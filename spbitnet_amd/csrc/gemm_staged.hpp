@@ -429,16 +429,22 @@ bool staged_ok(const void* meta, const void* values, const void* X, int cols, in
 //   n > 64 : 64 rows x 64 tokens, 8 waves (2 row groups x 4 K ways), 78 KB
 // Kernels above 64 KB of LDS need their limit raised (gemm_prepare).
 enum StagedShape { kStagedN16, kStagedN64, kStagedWide };
-// Batches up to this size take the 32x16 tile (one chunk per 2560-column row,
-// the token tiles side by side).  At 32 tokens on the 2.4B model's decode
-// shapes it beat the 64x32 tile (more blocks, one memory round trip each:
-// 9,415 -> 9,750 tok/s at batch 32); at 64 tokens it lost (6912x2560: 10.5
-// against 5.6 us).
+// Batches of up to 16 tokens take the 32x16 tile; so do batches of up to 32
+// whose 64x32 grid would fill at most half the CUs (the token tiles side by
+// side, one chunk per 2560-column row: more blocks, one memory round trip
+// each).  On the 2.4B model's batch-32 decode step the 32x16 tile took q|k|v
+// from 9.25 to 6.44 us (240 blocks instead of 60) and o / down from 7.2 /
+// 10.1 to ~6.4 us, but gate|up (216 tiles of 64x32 already) from 7.77 to
+// 11.8 us (864 blocks); at 64 tokens it lost (6912x2560: 10.5 against 5.6 us).
 constexpr int kStagedN16Max = 32;
-StagedShape staged_shape(int n) {
-    return n <= kStagedN16Max ? kStagedN16 : (n <= 64 ? kStagedN64 : kStagedWide);
+StagedShape staged_shape(int n, int rows) {
+    if (n <= 16) return kStagedN16;
+    if (n <= kStagedN16Max &&
+        2L * ((rows + 63) / 64) * ((n + 31) / 32) <= static_cast<long>(device_cu_count()))
+        return kStagedN16;
+    return n <= 64 ? kStagedN64 : kStagedWide;
 }
-int staged_row_block(int n) { return n <= kStagedN16Max ? 32 : 64; }
+int staged_row_block(int n, int rows) { return staged_shape(n, rows) == kStagedN16 ? 32 : 64; }
 
 template <int S, int T, int WS, int KW, int KCP, class Epi, bool kSplit = false>
 const void* staged_fn() {
@@ -501,7 +507,7 @@ template <class Epi>
 int launch_staged_for(const uint32_t* meta, const uint32_t* values, const int8_t* X,
                       const Epi& epi, int rows, int cols, int n, int ms, int vs, hipStream_t st,
                       const GemmSegs& g, const GemmSplit* split = nullptr) {
-    switch (staged_shape(n)) {
+    switch (staged_shape(n, rows)) {
         case kStagedN16:
             return launch_staged<1, 1, 2, 4, 10>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
                                                  split);
@@ -517,11 +523,12 @@ int launch_staged_for(const uint32_t* meta, const uint32_t* values, const int8_t
 // Split-K workspace (int32 words of part) that launches of up to n tokens
 // on these row counts and columns need at most.
 long staged_split_words(const int* rows, int nrows, int cols, int n) {
-    const int rb = staged_row_block(n), tb = n <= kStagedN16Max ? 16 : (n <= 64 ? 32 : 64);
-    const int kcp = n <= kStagedN16Max ? 10 : 2;
-    const int nch = (cols / 256 + kcp - 1) / kcp;
     long words = 0;
     for (int i = 0; i < nrows; ++i) {
+        const bool n16 = staged_shape(n, rows[i]) == kStagedN16;
+        const int rb = n16 ? 32 : 64, tb = n16 ? 16 : (n <= 64 ? 32 : 64);
+        const int kcp = n16 ? 10 : 2;
+        const int nch = (cols / 256 + kcp - 1) / kcp;
         const long tiles = static_cast<long>((rows[i] + rb - 1) / rb) * ((n + tb - 1) / tb);
         const long w = tiles * staged_split_parts(tiles, nch) * rb * tb;
         if (w > words) words = w;
@@ -585,7 +592,7 @@ int gemm_stacked_epi(const spb_sparse_linear* const* segs, int nseg, const int8_
         ends[i] = rows;
     }
     if (!staged_ok(a.meta, a.values, X, a.cols, a.meta_stride, a.values_stride)) return 1;
-    const int rb = staged_row_block(n);
+    const int rb = staged_row_block(n, rows);
     GemmSegs g{0, 0, 0, 0, ends[0], nseg > 1 ? ends[1] : ends[0]};
     if (nseg == 1) g.end0 = g.end1 = rows;
     for (int i = 1; i < nseg; ++i) {
