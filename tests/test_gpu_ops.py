@@ -121,6 +121,60 @@ def test_scatter_kv(gpu):
         _call("spb_scatter_kv", _p(src), _p(cache), nkv, hd, max_seq, max_seq, None)
 
 
+def test_scatter_kv_reference_kat(gpu):
+    """The reference's ScatterKV case (tests/test_inference_kernels.cu:459-491):
+    two kv heads of 4 values [1..4] and [5..8] into an 8-position cache at
+    position 3; those land at [head][3][:], everything else stays zero."""
+    nkv, hd, max_seq, pos = 2, 4, 8, 3
+    src = torch.tensor([1, 2, 3, 4, 5, 6, 7, 8], dtype=torch.float16, device="cuda")
+    cache = torch.zeros(nkv * max_seq * hd, dtype=torch.float16, device="cuda")
+    _call("spb_scatter_kv", _p(src), _p(cache), nkv, hd, max_seq, pos, None)
+    want = np.zeros((nkv, max_seq, hd))
+    want[0, pos] = [1, 2, 3, 4]
+    want[1, pos] = [5, 6, 7, 8]
+    assert np.array_equal(cache.view(nkv, max_seq, hd).float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+def test_attention_single_head_reference_kat(gpu, kind):
+    """The reference's AttentionSingleHead case (tests/test_inference_kernels.cu:376-453):
+    q = [1,0,1,0] against K rows [1,0,0,0], [0,1,0,1], [1,0,1,0] scores
+    0.5, 0 and 1.0 (dot products 1, 0, 2 times 1/sqrt(4)); the softmax of
+    those sums to 1 with score 2 largest and score 1 smallest; the output is
+    the weights times V rows [10,0,0,0], [0,20,0,0], [0,0,30,0].  Held here to
+    the kernels' own tolerances (float32 scores exact for these inputs,
+    softmax within 5e-6, output within one 16-bit ulp) rather than the
+    reference test's 1e-3 / 1e-4 / 0.1."""
+    nh, nkv, hd, max_seq, seq = 1, 1, 4, 8, 3
+    dt = KINDS[kind]
+    q = torch.tensor([1, 0, 1, 0], dtype=dt, device="cuda")
+    K = torch.zeros(max_seq, hd, dtype=dt)
+    K[0, 0] = 1
+    K[1, 1] = 1
+    K[1, 3] = 1
+    K[2, 0] = 1
+    K[2, 2] = 1
+    V = torch.zeros(max_seq, hd, dtype=dt)
+    V[0, 0], V[1, 1], V[2, 2] = 10, 20, 30
+    K, V = K.cuda(), V.cuda()
+    sc = torch.zeros(nh * max_seq, dtype=torch.float32, device="cuda")
+    _call(f"spb_attention_scores_{kind}", _p(q), _p(K), _p(sc), nh, nkv, hd, max_seq, seq,
+          0.5, None)
+    assert sc[:3].cpu().tolist() == [0.5, 0.0, 1.0]
+    assert torch.all(sc[3:] == 0)
+    _call("spb_softmax", _p(sc), nh, max_seq, seq, None)
+    p = sc[:3].double().cpu().numpy()
+    e = np.exp(np.array([0.5, 0.0, 1.0]) - 1.0)
+    assert np.allclose(p, e / e.sum(), rtol=5e-6, atol=0)
+    assert abs(p.sum() - 1.0) < 1e-6 and p[2] > p[0] > p[1]
+    out = torch.empty(nh * hd, dtype=dt, device="cuda")
+    _call(f"spb_attention_output_{kind}", _p(sc), _p(V), _p(out), nh, nkv, hd, max_seq, seq, None)
+    want = np.array([10 * p[0], 20 * p[1], 30 * p[2], 0.0])
+    got = _to_host(out)
+    assert np.all(np.abs(got - _round16(want, kind)) <= _ulp16(_round16(want, kind), kind) * 1.01)
+    assert got[3] == 0.0
+
+
 @pytest.mark.parametrize("kind", ["f16", "bf16"])
 @pytest.mark.parametrize("nh,nkv,hd,seq", [(20, 5, 128, 1), (20, 5, 128, 333), (8, 8, 64, 70),
                                            (4, 1, 256, 17)])
