@@ -69,13 +69,12 @@ struct BF16 {
     static __device__ __forceinline__ float to_float(uint16_t b) {
         return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
     }
-    // Round to nearest even; NaN stays a quiet NaN.
+    // Round to nearest even; a NaN keeps its sign and upper payload bits and
+    // becomes quiet ((bits >> 16) | 0x40).  One v_cvt_pk_bf16_f32 on gfx950,
+    // whose results equal that rule's for all 2^32 float inputs (compared
+    // exhaustively on an MI355X); the integer form took ~6 instructions.
     static __device__ __forceinline__ uint16_t from_float(float f) {
-        uint32_t u = __builtin_bit_cast(uint32_t, f);
-        if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))
-            return static_cast<uint16_t>((u >> 16) | 0x40u);
-        u += 0x7FFFu + ((u >> 16) & 1u);
-        return static_cast<uint16_t>(u >> 16);
+        return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
     }
 };
 
