@@ -1788,6 +1788,48 @@ __global__ __launch_bounds__(kBlock) void prefill_producer_kernel(P p, long stri
     if (tid == 0) amax[t] = am;
 }
 
+// The same for vectors of at most KU units per thread (P::units_per_thread,
+// every vector of the 2B model): the producer's one-pass form (fill_one, the
+// order of fill), the values in registers through the norms, and each thread
+// quantising and storing its own units (no trip of the vector through LDS).
+template <class P, int KU>
+__global__ __launch_bounds__(kBlock) void prefill_producer_one_kernel(P p, long stride,
+                                                                      const EngineState* st,
+                                                                      int cols,
+                                                                      int8_t* __restrict__ xq,
+                                                                      float* __restrict__ amax) {
+    __shared__ float red[3 * kRedSlot];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    p.at(t, stride);
+    st += t;
+    typename P::Regs regs;
+    p.template issue<KU>(tid, st, regs);
+    float v[kUnits][8];
+    const float m = p.template fill_one<KU>(v, tid, red, st, regs);
+    const float am = block_max<kBlock>(m, red + 2 * kRedSlot);
+    const float scale = quant_scale(am);
+    uint2* out = reinterpret_cast<uint2*>(xq + static_cast<long>(t) * cols);
+    const int units = cols >> 3;
+#pragma unroll
+    for (int k = 0; k < KU; ++k) {
+        const int u = tid + k * kBlock;
+        if (u < units) {
+            uint32_t w[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                w[h] = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    w[h] |= (static_cast<uint32_t>(quant_round_clamp(v[k][4 * h + e] * scale)) &
+                             0xFFu)
+                            << (8 * e);
+            }
+            out[u] = make_uint2(w[0], w[1]);
+        }
+    }
+    if (tid == 0) amax[t] = am;
+}
+
 // Rows [blockIdx.x * R, +R) of token blockIdx.y (R = kBlock, or 2 * kBlock
 // for a pair sink), from up to three GEMM outputs: row r < end0 of y0, r <
 // end1 of y1 (row r - end0), else y2 (row r - end1); y_k is token-major with
@@ -2757,9 +2799,21 @@ void launch_attention_prefill_hd(int G, int sp, int nkv, int c, hipStream_t s,
 template <class P>
 void launch_prefill_producer(const P& p, long stride, const EngineState* st, int cols, int c,
                              int8_t* xq, float* amax, hipStream_t s) {
-    const size_t lds = static_cast<size_t>(cols) * 4 * (1 + P::kAux) + 4 * 3 * kRedSlot;
-    hipLaunchKernelGGL((prefill_producer_kernel<P>), dim3(c), dim3(kBlock), lds, s, p, stride, st,
-                       cols, xq, amax);
+    switch (p.units_per_thread()) {
+    case 1:
+        hipLaunchKernelGGL((prefill_producer_one_kernel<P, 1>), dim3(c), dim3(kBlock), 0, s, p,
+                           stride, st, cols, xq, amax);
+        return;
+    case 2:
+        hipLaunchKernelGGL((prefill_producer_one_kernel<P, 2>), dim3(c), dim3(kBlock), 0, s, p,
+                           stride, st, cols, xq, amax);
+        return;
+    default: {
+        const size_t lds = static_cast<size_t>(cols) * 4 * (1 + P::kAux) + 4 * 3 * kRedSlot;
+        hipLaunchKernelGGL((prefill_producer_kernel<P>), dim3(c), dim3(kBlock), lds, s, p, stride,
+                           st, cols, xq, amax);
+    }
+    }
 }
 
 template <class Sink>
