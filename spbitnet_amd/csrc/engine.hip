@@ -36,6 +36,7 @@
 #include <cmath>
 #include <cstddef>
 #include <new>
+#include <type_traits>
 #include <vector>
 
 #include "bitplane.hpp"
@@ -1044,7 +1045,10 @@ struct ResidualSink {
     }
     // rows r .. r + 3 (r % 4 == 0, 8-byte aligned there): one load, one store
     __device__ void store4(long r, const int (&acc)[4]) const {
-        const uint2 rv = *reinterpret_cast<const uint2*>(res + r);
+        store4_with(r, acc, *reinterpret_cast<const uint2*>(res + r));
+    }
+    // the same with the four residual values already loaded (rv = res[r .. r+3])
+    __device__ void store4_with(long r, const int (&acc)[4], uint2 rv) const {
         const uint32_t rw[2] = {rv.x, rv.y};
         uint32_t h[4];
 #pragma unroll
@@ -1722,26 +1726,75 @@ struct AmaxOf {
     __device__ float absmax() const { return m; }
 };
 
+// What a sink's four-row epilogue reads from memory besides the GEMM's
+// products, loaded by the staged GEMM before its main loop (SinkOut::preload)
+// so that no load waits at the kernel's end: the residual rows of a
+// ResidualSink; the decode state and the two RoPE pairs of a QkvRopeSink.
+template <class Sink>
+struct SinkPreload {
+    struct Data {};
+    __device__ static Data load(const Sink&, int, int) { return {}; }
+};
+template <>
+struct SinkPreload<ResidualSink> {
+    struct Data {
+        uint2 res;
+    };
+    __device__ static Data load(const ResidualSink& sk, int row, int rows) {
+        // unconditional (row 0 when the lane's four rows are not all there)
+        return {*reinterpret_cast<const uint2*>(sk.res + (row + 3 < rows ? row : 0))};
+    }
+};
+template <>
+struct SinkPreload<QkvRopeSink> {
+    struct Data {
+        int pos, live;
+        float2 cs0, cs1;
+    };
+    __device__ static Data load(const QkvRopeSink& sk, int row, int) {
+        Data d;
+        d.pos = state_pos(sk.st);
+        d.live = !state_done(sk.st);
+        d.cs0 = sk.cur_rope[sk.rope_pair(row < sk.end1 ? row : 0)];
+        d.cs1 = sk.cur_rope[sk.rope_pair(row + 2 < sk.end1 ? row + 2 : 0)];
+        return d;
+    }
+};
+
 // Epilogue of the staged GEMM (gemm_staged.hpp) that passes the products
 // through a per-token sink in registers: the lane holding rows row .. row+3
 // of token tok runs the sink for them with the calls and arithmetic of
 // prefill_sink_kernel, so the outputs are those of a GEMM followed by that
-// kernel, and no int32 product is stored.
+// kernel, and no int32 product is stored.  The token's absmax and the
+// sink's own inputs (SinkPreload) come from preload, which the GEMM calls
+// before its main loop.
 template <class Sink>
 struct SinkOut {
     Sink sink;
     long stride;        // per-token output stride
     const float* amax;  // per-token absmax of the GEMM's int8 input
     int rows;           // rows of the (stacked) product
-    __device__ void store4(int tok, int row, v4i acc) const {
+    struct Pre {
+        float am;
+        typename SinkPreload<Sink>::Data d;
+    };
+    __device__ Pre preload(int tok, int row) const {
+        Sink sk = sink;
+        sk.at(tok, stride);
+        return Pre{amax[tok], SinkPreload<Sink>::load(sk, row, rows)};
+    }
+    __device__ void store4(int tok, int row, v4i acc, const Pre& pre) const {
         Sink sk = sink;
         sk.at(tok, stride);
         sk.prepare();
         if constexpr (SinkQuads<Sink>::value) {
-            sk.bind(AmaxOf{amax[tok]});
+            sk.bind(AmaxOf{pre.am});
             if (row + 3 < rows) {
                 const int a[4] = {acc[0], acc[1], acc[2], acc[3]};
-                sk.store4(row, a);
+                if constexpr (std::is_same<Sink, ResidualSink>::value)
+                    sk.store4_with(row, a, pre.d.res);
+                else
+                    sk.store4(row, a);
             } else {
                 sk.prefetch(row, 4, 0);
 #pragma unroll
@@ -1750,8 +1803,22 @@ struct SinkOut {
             }
             return;
         }
+        if constexpr (std::is_same<Sink, QkvRopeSink>::value) {
+            sk.pos = pre.d.pos;
+            sk.live = pre.d.live;
+            sk.bind(AmaxOf{pre.am});
+            sk.pre_row = row;
+            sk.pre_cs = pre.d.cs0;
+            sk.store_pair(row, acc[0], acc[1]);  // rows are even, row < rows
+            if (row + 2 < rows) {
+                sk.pre_row = row + 2;
+                sk.pre_cs = pre.d.cs1;
+                sk.store_pair(row + 2, acc[2], acc[3]);
+            }
+            return;
+        }
         sk.prefetch(row, 4, 0);
-        sk.bind(AmaxOf{amax[tok]});
+        sk.bind(AmaxOf{pre.am});
         if constexpr (SinkPairs<Sink>::value) {
             sk.store_pair(row, acc[0], acc[1]);  // rows are even, row < rows
             if (row + 2 < rows) sk.store_pair(row + 2, acc[2], acc[3]);

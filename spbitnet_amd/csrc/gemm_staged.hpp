@@ -275,6 +275,26 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[s][t] = (v4i){0, 0, 0, 0};
 
+    // The epilogue's own loads (Epi::preload: the sink's per-token inputs),
+    // issued ahead of the first chunk in the small tiles (the batched decode's
+    // few-chunk launches, whose end would otherwise wait a memory round trip
+    // for them), at the end in the 64x64 tile (their registers would cost
+    // its second block per CU); rows and tokens past the matrix load row 0 /
+    // the last token (nothing is stored for them).
+    constexpr bool kEarly = S * T <= 4;
+    typename Epi::Pre pre[S][T];
+    auto preload = [&](int s, int t) {
+        const int row = r0 + (ws * S + s) * 16 + 4 * q, tok = t0 + t * 16 + li;
+        pre[s][t] = epi.preload(tok < n ? tok : n - 1, row < rows ? row : 0);
+    };
+    if constexpr (kEarly) {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+                if (KW == 1 || (s * T + t) % KW == kw) preload(s, t);
+    }
+
     load_chunk(c_begin);
     store_chunk(0);
     __syncthreads();
@@ -403,8 +423,10 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int tok = t0 + t * 16 + li;
-            if ((KW == 1 || (s * T + t) % KW == kw) && tok < n && row < rows)
-                epi.store4(tok, row, acc[s][t]);
+            if ((KW == 1 || (s * T + t) % KW == kw) && tok < n && row < rows) {
+                if constexpr (!kEarly) preload(s, t);
+                epi.store4(tok, row, acc[s][t], pre[s][t]);
+            }
         }
     }
 }
@@ -560,7 +582,9 @@ struct Int32Out {
     int32_t* Y;
     int rows;
     bool quads;
-    __device__ void store4(int tok, int row, v4i acc) const {
+    struct Pre {};
+    __device__ Pre preload(int, int) const { return {}; }
+    __device__ void store4(int tok, int row, v4i acc, const Pre&) const {
         int32_t* y = Y + static_cast<long>(tok) * rows + row;
         if (quads) {
             *reinterpret_cast<v4i*>(y) = acc;
