@@ -218,7 +218,7 @@ int launch_smfmac_for(const uint32_t* meta, const uint32_t* values, const int8_t
 // Rows per block of the matrix-core launch launch_smfmac_for makes.
 int smfmac_row_block(const void* meta, const void* values, const void* X, int rows, int cols,
                      int n, int ms, int vs) {
-    if (staged_ok(meta, values, X, cols, ms, vs)) return staged_row_block(n, rows);
+    if (staged_ok(meta, values, X, cols, ms, vs)) return staged_row_block(n, rows, cols);
     int strips = 0, tiles = 0;
     smfmac_tiles(rows, n, &strips, &tiles);
     return 16 * strips;

@@ -450,7 +450,7 @@ bool staged_ok(const void* meta, const void* values, const void* X, int cols, in
 //   n <= 64: 64 rows x 32 tokens, 8 waves (2 row groups x 4 K ways)
 //   n > 64 : 64 rows x 64 tokens, 8 waves (2 row groups x 4 K ways), 78 KB
 // Kernels above 64 KB of LDS need their limit raised (gemm_prepare).
-enum StagedShape { kStagedN16, kStagedN64, kStagedWide };
+enum StagedShape { kStagedN16, kStagedN16Long, kStagedN64, kStagedWide };
 // Batches of up to 16 tokens take the 32x16 tile; so do batches of up to 32
 // whose 64x32 grid would fill at most half the CUs (the token tiles side by
 // side, one chunk per 2560-column row: more blocks, one memory round trip
@@ -458,15 +458,27 @@ enum StagedShape { kStagedN16, kStagedN64, kStagedWide };
 // from 9.25 to 6.44 us (240 blocks instead of 60) and o / down from 7.2 /
 // 10.1 to ~6.4 us, but gate|up (216 tiles of 64x32 already) from 7.77 to
 // 11.8 us (864 blocks); at 64 tokens it lost (6912x2560: 10.5 against 5.6 us).
+// Rows longer than one 2560-column chunk at up to 16 tokens, when the 32-row
+// grid fills at most half the CUs (the batch-8 decode step's 2560 x 6912 down
+// projection: 80 blocks walking 3 chunks), take a 16-row tile of 4 waves with
+// 3584-column chunks (two instead of three chunk round trips, twice the
+// blocks; 140 KB of LDS): 5.52 against 5.89 us per launch back to back.
 constexpr int kStagedN16Max = 32;
-StagedShape staged_shape(int n, int rows) {
-    if (n <= 16) return kStagedN16;
+StagedShape staged_shape(int n, int rows, int cols) {
+    if (n <= 16) {
+        if (cols > 10 * 256 && 2L * ((rows + 31) / 32) <= static_cast<long>(device_cu_count()))
+            return kStagedN16Long;
+        return kStagedN16;
+    }
     if (n <= kStagedN16Max &&
         2L * ((rows + 63) / 64) * ((n + 31) / 32) <= static_cast<long>(device_cu_count()))
         return kStagedN16;
     return n <= 64 ? kStagedN64 : kStagedWide;
 }
-int staged_row_block(int n, int rows) { return staged_shape(n, rows) == kStagedN16 ? 32 : 64; }
+int staged_row_block(int n, int rows, int cols) {
+    const StagedShape sh = staged_shape(n, rows, cols);
+    return sh == kStagedN16Long ? 16 : (sh == kStagedN16 ? 32 : 64);
+}
 
 template <int S, int T, int WS, int KW, int KCP, class Epi, bool kSplit = false>
 const void* staged_fn() {
@@ -529,9 +541,12 @@ template <class Epi>
 int launch_staged_for(const uint32_t* meta, const uint32_t* values, const int8_t* X,
                       const Epi& epi, int rows, int cols, int n, int ms, int vs, hipStream_t st,
                       const GemmSegs& g, const GemmSplit* split = nullptr) {
-    switch (staged_shape(n, rows)) {
+    switch (staged_shape(n, rows, cols)) {
         case kStagedN16:
             return launch_staged<1, 1, 2, 4, 10>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
+                                                 split);
+        case kStagedN16Long:
+            return launch_staged<1, 1, 1, 4, 14>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
                                                  split);
         case kStagedN64:
             return launch_staged<2, 2, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
@@ -547,9 +562,11 @@ int launch_staged_for(const uint32_t* meta, const uint32_t* values, const int8_t
 long staged_split_words(const int* rows, int nrows, int cols, int n) {
     long words = 0;
     for (int i = 0; i < nrows; ++i) {
-        const bool n16 = staged_shape(n, rows[i]) == kStagedN16;
-        const int rb = n16 ? 32 : 64, tb = n16 ? 16 : (n <= 64 ? 32 : 64);
-        const int kcp = n16 ? 10 : 2;
+        const StagedShape sh = staged_shape(n, rows[i], cols);
+        const bool n16 = sh == kStagedN16 || sh == kStagedN16Long;
+        const int rb = sh == kStagedN16Long ? 16 : (n16 ? 32 : 64);
+        const int tb = n16 ? 16 : (n <= 64 ? 32 : 64);
+        const int kcp = sh == kStagedN16Long ? 14 : (n16 ? 10 : 2);
         const int nch = (cols / 256 + kcp - 1) / kcp;
         const long tiles = static_cast<long>((rows[i] + rb - 1) / rb) * ((n + tb - 1) / tb);
         const long w = tiles * staged_split_parts(tiles, nch) * rb * tb;
@@ -563,6 +580,8 @@ long staged_split_words(const int* rows, int nrows, int cols, int n) {
 template <class Epi>
 int staged_prepare() {
     return gemm_allow_lds(staged_fn<1, 1, 2, 4, 10, Epi>()) &&
+                   gemm_allow_lds(staged_fn<1, 1, 1, 4, 14, Epi>()) &&
+                   gemm_allow_lds(staged_fn<1, 1, 1, 4, 14, Epi, true>()) &&
                    gemm_allow_lds(staged_fn<2, 2, 2, 4, 2, Epi>()) &&
                    gemm_allow_lds(staged_fn<2, 4, 2, 4, 2, Epi>()) &&
                    gemm_allow_lds(staged_fn<1, 1, 2, 4, 10, Epi, true>()) &&
@@ -616,7 +635,7 @@ int gemm_stacked_epi(const spb_sparse_linear* const* segs, int nseg, const int8_
         ends[i] = rows;
     }
     if (!staged_ok(a.meta, a.values, X, a.cols, a.meta_stride, a.values_stride)) return 1;
-    const int rb = staged_row_block(n, rows);
+    const int rb = staged_row_block(n, rows, a.cols);
     GemmSegs g{0, 0, 0, 0, ends[0], nseg > 1 ? ends[1] : ends[0]};
     if (nseg == 1) g.end0 = g.end1 = rows;
     for (int i = 1; i < nseg; ++i) {
