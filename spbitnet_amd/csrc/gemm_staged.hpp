@@ -450,7 +450,7 @@ bool staged_ok(const void* meta, const void* values, const void* X, int cols, in
 //   n <= 64: 64 rows x 32 tokens, 8 waves (2 row groups x 4 K ways)
 //   n > 64 : 64 rows x 64 tokens, 8 waves (2 row groups x 4 K ways), 78 KB
 // Kernels above 64 KB of LDS need their limit raised (gemm_prepare).
-enum StagedShape { kStagedN16, kStagedN16Long, kStagedN64, kStagedWide };
+enum StagedShape { kStagedN16, kStagedN16R16, kStagedN16Long, kStagedN16R64, kStagedN64, kStagedWide };
 // Batches of up to 16 tokens take the 32x16 tile; so do batches of up to 32
 // whose 64x32 grid would fill at most half the CUs (the token tiles side by
 // side, one chunk per 2560-column row: more blocks, one memory round trip
@@ -458,16 +458,21 @@ enum StagedShape { kStagedN16, kStagedN16Long, kStagedN64, kStagedWide };
 // from 9.25 to 6.44 us (240 blocks instead of 60) and o / down from 7.2 /
 // 10.1 to ~6.4 us, but gate|up (216 tiles of 64x32 already) from 7.77 to
 // 11.8 us (864 blocks); at 64 tokens it lost (6912x2560: 10.5 against 5.6 us).
-// Rows longer than one 2560-column chunk at up to 16 tokens, when the 32-row
-// grid fills at most half the CUs (the batch-8 decode step's 2560 x 6912 down
-// projection: 80 blocks walking 3 chunks), take a 16-row tile of 4 waves with
-// 3584-column chunks (two instead of three chunk round trips, twice the
-// blocks; 140 KB of LDS): 5.52 against 5.89 us per launch back to back.
+// Up to 16 tokens: the smallest row block (16, 32 or 64 rows) whose grid
+// stays within one block per CU -- these launches are a few chunks long, and
+// a second block on some CUs sets the time.  8 tokens, back to back (us per
+// launch, 32-row tile against the chosen one): 13824 x 2560 5.79 -> 4.63
+// (64 rows, 216 blocks), 3840 x 2560 3.58 -> 3.39 and 2560 x 2560 3.53 ->
+// 3.36 (16 rows, 240 / 160 blocks).  16-row blocks of rows longer than one
+// 2560-column chunk take 3584-column chunks (two chunk round trips instead of
+// three at 6912 columns; 140 KB of LDS): 2560 x 6912 5.89 -> 5.52.
 constexpr int kStagedN16Max = 32;
 StagedShape staged_shape(int n, int rows, int cols) {
     if (n <= 16) {
-        if (cols > 10 * 256 && 2L * ((rows + 31) / 32) <= static_cast<long>(device_cu_count()))
-            return kStagedN16Long;
+        const long cus = device_cu_count();
+        if ((rows + 15) / 16 <= cus) return cols > 10 * 256 ? kStagedN16Long : kStagedN16R16;
+        if ((rows + 31) / 32 <= cus) return kStagedN16;
+        if ((rows + 63) / 64 <= cus) return kStagedN16R64;
         return kStagedN16;
     }
     if (n <= kStagedN16Max &&
@@ -476,8 +481,12 @@ StagedShape staged_shape(int n, int rows, int cols) {
     return n <= 64 ? kStagedN64 : kStagedWide;
 }
 int staged_row_block(int n, int rows, int cols) {
-    const StagedShape sh = staged_shape(n, rows, cols);
-    return sh == kStagedN16Long ? 16 : (sh == kStagedN16 ? 32 : 64);
+    switch (staged_shape(n, rows, cols)) {
+        case kStagedN16R16:
+        case kStagedN16Long: return 16;
+        case kStagedN16: return 32;
+        default: return 64;
+    }
 }
 
 template <int S, int T, int WS, int KW, int KCP, class Epi, bool kSplit = false>
@@ -545,8 +554,14 @@ int launch_staged_for(const uint32_t* meta, const uint32_t* values, const int8_t
         case kStagedN16:
             return launch_staged<1, 1, 2, 4, 10>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
                                                  split);
+        case kStagedN16R16:
+            return launch_staged<1, 1, 1, 4, 10>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
+                                                 split);
         case kStagedN16Long:
             return launch_staged<1, 1, 1, 4, 14>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
+                                                 split);
+        case kStagedN16R64:
+            return launch_staged<2, 1, 2, 4, 10>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
                                                  split);
         case kStagedN64:
             return launch_staged<2, 2, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
@@ -563,10 +578,10 @@ long staged_split_words(const int* rows, int nrows, int cols, int n) {
     long words = 0;
     for (int i = 0; i < nrows; ++i) {
         const StagedShape sh = staged_shape(n, rows[i], cols);
-        const bool n16 = sh == kStagedN16 || sh == kStagedN16Long;
-        const int rb = sh == kStagedN16Long ? 16 : (n16 ? 32 : 64);
-        const int tb = n16 ? 16 : (n <= 64 ? 32 : 64);
-        const int kcp = sh == kStagedN16Long ? 14 : (n16 ? 10 : 2);
+        const bool t16 = n <= 16 || sh == kStagedN16;  // 16-token tiles
+        const int rb = staged_row_block(n, rows[i], cols);
+        const int tb = t16 ? 16 : (n <= 64 ? 32 : 64);
+        const int kcp = sh == kStagedN16Long ? 14 : (t16 ? 10 : 2);
         const int nch = (cols / 256 + kcp - 1) / kcp;
         const long tiles = static_cast<long>((rows[i] + rb - 1) / rb) * ((n + tb - 1) / tb);
         const long w = tiles * staged_split_parts(tiles, nch) * rb * tb;
@@ -580,8 +595,12 @@ long staged_split_words(const int* rows, int nrows, int cols, int n) {
 template <class Epi>
 int staged_prepare() {
     return gemm_allow_lds(staged_fn<1, 1, 2, 4, 10, Epi>()) &&
+                   gemm_allow_lds(staged_fn<1, 1, 1, 4, 10, Epi>()) &&
+                   gemm_allow_lds(staged_fn<1, 1, 1, 4, 10, Epi, true>()) &&
                    gemm_allow_lds(staged_fn<1, 1, 1, 4, 14, Epi>()) &&
                    gemm_allow_lds(staged_fn<1, 1, 1, 4, 14, Epi, true>()) &&
+                   gemm_allow_lds(staged_fn<2, 1, 2, 4, 10, Epi>()) &&
+                   gemm_allow_lds(staged_fn<2, 1, 2, 4, 10, Epi, true>()) &&
                    gemm_allow_lds(staged_fn<2, 2, 2, 4, 2, Epi>()) &&
                    gemm_allow_lds(staged_fn<2, 4, 2, 4, 2, Epi>()) &&
                    gemm_allow_lds(staged_fn<1, 1, 2, 4, 10, Epi, true>()) &&
