@@ -3719,11 +3719,12 @@ extern "C" int spb_generate_normal_bf16(uint64_t seed, long n, float std_, uint1
 
 namespace {
 
-void launch_attention_batch(int hd, int G, int S, int nkv, int B, hipStream_t s,
+// Launches the splits below `splits` (of S, the partials' stride).
+void launch_attention_batch(int hd, int G, int S, int splits, int nkv, int B, hipStream_t s,
                             const uint16_t* qkv, const uint16_t* kc, const uint16_t* vc, float* pm,
                             float* pl, float* pacc, const EngineState* st, int max_seq,
                             float scale, int qkv_stride, long kv_stride) {
-    const dim3 grid(S, nkv, B), block(kAttnThreads);
+    const dim3 grid(splits, nkv, B), block(kAttnThreads);
 #define SPB_ATTN_BATCH(HD, GG)                                                                     \
     hipLaunchKernelGGL((attention_batch_kernel<HD, GG>), grid, block, 0, s, qkv, kc, vc, pm, pl,  \
                        pacc, st, max_seq, S, scale, qkv_stride, kv_stride)
@@ -3774,24 +3775,39 @@ struct spb_batch_engine {
     std::vector<float2> rope_host;
     hipStream_t stream = nullptr;
     hipStream_t cap_stream = nullptr;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // One step graph per bucket of bucket_pos positions: graph k launches
+    // the attention on the splits below (k + 1) * bucket_pos only, so the
+    // blocks past every sequence's position are not launched at all.  The
+    // host replays the graph of pos_hint, an upper bound of the largest
+    // position of the live sequences (each advances at most one per step).
+    std::vector<hipGraph_t> graphs;
+    std::vector<hipGraphExec_t> execs;
+    int bucket_pos = 0;
+    int pos_hint = 0;
 
     ~spb_batch_engine() {
-        if (exec) (void)hipGraphExecDestroy(exec);
-        if (graph) (void)hipGraphDestroy(graph);
+        for (hipGraphExec_t x : execs) (void)hipGraphExecDestroy(x);
+        for (hipGraph_t g : graphs) (void)hipGraphDestroy(g);
         if (cap_stream) (void)hipStreamDestroy(cap_stream);
         for (void* p : owned) (void)hipFree(p);
+    }
+
+    hipError_t launch_step(hipStream_t s) {
+        int k = pos_hint / bucket_pos;
+        if (k >= static_cast<int>(execs.size())) k = static_cast<int>(execs.size()) - 1;
+        const hipError_t err = hipGraphLaunch(execs[k], s);
+        pos_hint = pos_hint < max_seq ? pos_hint + 1 : max_seq;
+        return err;
     }
 
     long tok_stride() const { return static_cast<long>(max_seq) + 1; }
 
     // One decode step of every sequence: per layer the producer, GEMM(s)
     // and sink of each projection over the batch's tokens and the batched
-    // attention; then the final norm and the LM head (the matrix-core
-    // logits over every sequence, then the exact candidates and the argmax
-    // per sequence).
-    hipError_t enqueue_step(hipStream_t s) const {
+    // attention (on the first `splits` splits); then the final norm and the
+    // LM head (the matrix-core logits over every sequence, then the exact
+    // candidates and the argmax per sequence).
+    hipError_t enqueue_step(hipStream_t s, int splits) const {
         const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
         const int nkv = cfg.num_key_value_heads, H = cfg.hidden_size;
         const int I = cfg.intermediate_size, kvdim = nkv * hd, qrows = nh * hd;
@@ -3828,8 +3844,8 @@ struct spb_batch_engine {
                               s, &split) != hipSuccess)
                     return hipErrorLaunchFailure;
             }
-            launch_attention_batch(hd, nh / nkv, S, nkv, B, s, step.qkv, kcache[l], vcache[l],
-                                   step.pm, step.pl, step.pacc, st, max_seq, scale,
+            launch_attention_batch(hd, nh / nkv, S, splits, nkv, B, s, step.qkv, kcache[l],
+                                   vcache[l], step.pm, step.pl, step.pacc, st, max_seq, scale,
                                    qrows + 2 * kvdim, kv_seq);
             {
                 AttnCombine p{step.pm, step.pl, step.pacc, hd, S, qrows, hd == 64 ? 6 : 7};
@@ -3993,13 +4009,25 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
         delete e;
         return launch_status(fn);
     }
-    err = hipStreamBeginCapture(e->cap_stream, hipStreamCaptureModeThreadLocal);
-    if (err == hipSuccess) {
-        const hipError_t le = e->enqueue_step(e->cap_stream);
-        err = hipStreamEndCapture(e->cap_stream, &e->graph);
-        if (err == hipSuccess && le != hipSuccess) err = le;
+    // the step graphs, one per position bucket (the bs=1 engine's buckets)
+    {
+        const int per = e->S <= 64 ? kAttnBucketSplits : (e->S + 7) / 8;
+        e->bucket_pos = per * kAttnSplit;
+        for (int s0 = 0; s0 < e->S && err == hipSuccess; s0 += per) {
+            const int splits = s0 + per < e->S ? s0 + per : e->S;
+            hipGraph_t g = nullptr;
+            hipGraphExec_t x = nullptr;
+            err = hipStreamBeginCapture(e->cap_stream, hipStreamCaptureModeThreadLocal);
+            if (err == hipSuccess) {
+                const hipError_t le = e->enqueue_step(e->cap_stream, splits);
+                err = hipStreamEndCapture(e->cap_stream, &g);
+                if (err == hipSuccess) e->graphs.push_back(g);
+                if (err == hipSuccess && le != hipSuccess) err = le;
+            }
+            if (err == hipSuccess) err = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+            if (err == hipSuccess) e->execs.push_back(x);
+        }
     }
-    if (err == hipSuccess) err = hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0);
     if (err != hipSuccess) {
         set_error("%s: graph capture failed: %s", fn, hipGetErrorString(err));
         delete e;
@@ -4108,8 +4136,11 @@ extern "C" int spb_batch_engine_generate(spb_batch_engine* e, const int* prompts
         hipMemcpyAsync(e->cur_rope, cr.data(), cr.size() * sizeof(float2), hipMemcpyHostToDevice,
                        s) != hipSuccess)
         return launch_status(fn);
+    e->pos_hint = 0;
+    for (int b = 0; b < n_seq; ++b)
+        if (hs[b].pos > e->pos_hint) e->pos_hint = hs[b].pos;
     for (int i = 0; i < n_new; ++i)
-        if (hipGraphLaunch(e->exec, s) != hipSuccess) return launch_status(fn);
+        if (e->launch_step(s) != hipSuccess) return launch_status(fn);
     if (hipMemcpyAsync(hs.data(), e->st, hs.size() * sizeof(EngineState), hipMemcpyDeviceToHost,
                        s) != hipSuccess ||
         hipMemcpyAsync(tok.data(), e->tokens, tok.size() * sizeof(int), hipMemcpyDeviceToHost, s) !=
@@ -4131,7 +4162,7 @@ extern "C" int spb_batch_engine_decode_steps(spb_batch_engine* e, int steps) {
     if (!e) return invalid("spb_batch_engine_decode_steps: null engine");
     if (steps < 0) return invalid("spb_batch_engine_decode_steps: steps < 0");
     for (int i = 0; i < steps; ++i)
-        if (hipGraphLaunch(e->exec, e->stream) != hipSuccess)
+        if (e->launch_step(e->stream) != hipSuccess)
             return launch_status("spb_batch_engine_decode_steps");
     return 0;
 }

@@ -101,6 +101,30 @@ def test_batch_decode_gqa_variants_and_eos(gpu):
         eng.close()
 
 
+def test_batch_decode_crosses_position_buckets(gpu):
+    """The step graph is chosen per step by an upper bound of the largest
+    live position, in buckets of 256 positions whose graphs launch the
+    attention on the splits below the bucket's end only.  The longest
+    prompt ends at position 249, so its steps cross from the first bucket
+    into the second (split 4 starts at 256) during one generation; then a
+    generation that starts in the second bucket, and one back in the first
+    (the bound restarts from the new prompts)."""
+    from spbitnet_amd.model import BatchInferenceEngine, Model
+    cfg = _cfg(max_position_embeddings=512)
+    model = Model.random(cfg, seed=417)
+    host = model.to_host()
+    rng = np.random.default_rng(417)
+    eng = BatchInferenceEngine(model, max_seq=512, batch=4)
+    for lens, n_new in (([250, 1, 244, 120], 14), ([497, 3], 10), ([30, 255], 4)):
+        prompts = [[int(t) for t in rng.integers(0, cfg.vocab_size, n)] for n in lens]
+        print(f"bucket crossing: prompts {lens}, {n_new} steps", flush=True)
+        want = _oracle_tokens(host, 512, prompts, n_new)
+        got = eng.generate(prompts, n_new, stop_at_eos=False)
+        for b in range(len(lens)):
+            assert got[b] == want[b], f"prompts {lens}: sequence {b}"
+    eng.close()
+
+
 @pytest.mark.parametrize("heads,kv,batch", [(8, 2, 40), (8, 1, 36), (4, 2, 48)])
 def test_batch_decode_split_k_head_dim_128(gpu, heads, kv, batch):
     """At 33-64 sequences the GEMMs take the 64x32 tile (2-pair chunks), and
