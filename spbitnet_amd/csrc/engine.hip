@@ -51,6 +51,13 @@ constexpr int kAttnThreads = 256;
 constexpr int kAttnBucketSplits = 4;  // splits per position bucket of the decode graphs
 constexpr int kPrefillChunk = 1024;      // prompt tokens per batched-prefill pass (at most)
 constexpr int kGemmSplitCounters = 1024;  // split-K tile counters of a batch engine (split launches have at most CUs / 2 tiles)
+// Sequence groups of a batched decode step: two parallel branches of the
+// step graph for 24-32 sequences (same-box bench at config 4: batch 32
+// 11,943-11,952 -> 12,358-12,380 tok/s with two groups, 9,196-11,277 with
+// four; batch 16 7,818-7,819 with one, 7,760-7,761 with two; batch 8
+// 4,509-4,512 with one, 4,354-4,384 with two).  Larger batches keep one
+// branch, so the GEMMs' split over K (33-64 tokens) sees the whole batch.
+int batch_groups(int batch) { return batch >= 24 && batch <= 32 ? 2 : 1; }
 constexpr long kPrefillPartialBytes = 1L << 30;  // split partials of one pass (at most)
 constexpr int kPrefillMinDefault = 16;   // prompt tokens before the last that switch to it
 constexpr int kAttnMaxGroup = 8;  // q heads per kv head
@@ -2766,6 +2773,10 @@ struct PrefillBufs {
     float *pm = nullptr, *pl = nullptr, *pacc = nullptr;
     EngineState* st = nullptr;  // [chunk] one decode-state record per token
     int chunk = 0;  // tokens per prefill pass
+    // per-token capacities of x, y[0] and y[1..2] (a group's rows of x and y
+    // start at its first token * these when a batch's tokens are split into
+    // groups)
+    long xrow = 0, yrow0 = 0, yrow = 0;
 };
 
 // The batched prefill's buffers: up to kPrefillChunk tokens per pass, fewer
@@ -2785,6 +2796,9 @@ bool alloc_prefill(PrefillBufs& pf, const spb_model_config& cfg, int S, std::vec
     // y[0] also holds the stacked q|k|v and gate|up products
     const size_t ymax = static_cast<size_t>(std::max(std::max(nh * hd, kvdim), std::max(H, I)));
     const size_t ystack = std::max(ymax, static_cast<size_t>(std::max(nh * hd + 2 * kvdim, 2 * I)));
+    pf.xrow = static_cast<long>(xmax);
+    pf.yrow0 = static_cast<long>(ystack);
+    pf.yrow = static_cast<long>(ymax);
     return (pf.x = dev_alloc<int8_t>(C * xmax, own)) && (pf.amax = dev_alloc<float>(C, own)) &&
            (pf.y[0] = dev_alloc<int32_t>(C * ystack, own)) &&
            (pf.y[1] = dev_alloc<int32_t>(C * ymax, own)) &&
@@ -3775,6 +3789,14 @@ struct spb_batch_engine {
     std::vector<float2> rope_host;
     hipStream_t stream = nullptr;
     hipStream_t cap_stream = nullptr;
+    // Sequence groups (batch_groups): the layers of each group of sequences
+    // run as a parallel branch of the step graph (each with its own split-K
+    // workspace), joined before the LM head.  aux: the capture streams of
+    // groups 1 .. groups - 1; ev[0] forks, ev[g] joins group g.
+    int groups = 1;
+    std::vector<hipStream_t> aux;
+    std::vector<hipEvent_t> ev;
+    std::vector<GemmSplit> gsplit;
     // One step graph per bucket of bucket_pos positions: graph k launches
     // the attention on the splits below (k + 1) * bucket_pos only, so the
     // blocks past every sequence's position are not launched at all.  The
@@ -3789,6 +3811,8 @@ struct spb_batch_engine {
         for (hipGraphExec_t x : execs) (void)hipGraphExecDestroy(x);
         for (hipGraph_t g : graphs) (void)hipGraphDestroy(g);
         if (cap_stream) (void)hipStreamDestroy(cap_stream);
+        for (hipStream_t a : aux) (void)hipStreamDestroy(a);
+        for (hipEvent_t v : ev) (void)hipEventDestroy(v);
         for (void* p : owned) (void)hipFree(p);
     }
 
@@ -3802,34 +3826,51 @@ struct spb_batch_engine {
 
     long tok_stride() const { return static_cast<long>(max_seq) + 1; }
 
-    // One decode step of every sequence: per layer the producer, GEMM(s)
-    // and sink of each projection over the batch's tokens and the batched
-    // attention (on the first `splits` splits); then the final norm and the
-    // LM head (the matrix-core logits over every sequence, then the exact
-    // candidates and the argmax per sequence).
-    hipError_t enqueue_step(hipStream_t s, int splits) const {
+    // The layers of sequences b0 .. b0 + nb - 1 on stream s: per layer the
+    // producer, GEMM(s) and sink of each projection over their tokens and
+    // the batched attention (on the first `splits` splits).  Every per-token
+    // buffer is addressed from sequence b0's row.
+    hipError_t enqueue_layers(hipStream_t s, int b0, int nb, int splits,
+                              const GemmSplit* sp) const {
         const int hd = cfg.head_dim, nh = cfg.num_attention_heads;
         const int nkv = cfg.num_key_value_heads, H = cfg.hidden_size;
         const int I = cfg.intermediate_size, kvdim = nkv * hd, qrows = nh * hd;
         const float eps = cfg.rms_norm_eps;
         const float scale = 1.0f / sqrtf(static_cast<float>(hd));  // inference.cu:182
-        const int B = batch;
+        const int B = nb;
+        const long qkv_row = qrows + 2 * kvdim, hs = static_cast<long>(nh) * S;
+        int8_t* const x = step.x + b0 * step.xrow;
+        float* const amax = step.amax + b0;
+        int32_t* const y[3] = {step.y[0] + b0 * step.yrow0, step.y[1] + b0 * step.yrow,
+                               step.y[2] + b0 * step.yrow};
+        uint16_t* const qkv = step.qkv + b0 * qkv_row;
+        uint16_t* const o = step.o + static_cast<long>(b0) * H;
+        uint16_t* const r = step.r + static_cast<long>(b0) * H;
+        uint16_t* const r2 = step.r2 + static_cast<long>(b0) * H;
+        uint16_t* const gu = step.gu + static_cast<long>(b0) * 2 * I;
+        float* const pm = step.pm + b0 * hs;
+        float* const pl = step.pl + b0 * hs;
+        float* const pacc = step.pacc + b0 * hs * hd;
+        EngineState* const stb = st + b0;
+        const int* const tok = tokens + b0 * tok_stride();
+        float2* const crope = cur_rope + static_cast<long>(b0) * (hd / 2);
         for (size_t l = 0; l < layers.size(); ++l) {
             const spb_transformer_layer& L = layers[l];
+            uint16_t* const kc = kcache[l] + b0 * kv_seq;
+            uint16_t* const vc = vcache[l] + b0 * kv_seq;
             {
-                InputNorm p{step.r, l == 0 ? embed : nullptr, tokens, step.r, L.input_layernorm,
-                            eps, H};
+                InputNorm p{r, l == 0 ? embed : nullptr, tok, r, L.input_layernorm, eps, H};
                 p.tok_stride = tok_stride();
-                launch_prefill_producer(p, H, st, H, B, step.x, step.amax, s);
+                launch_prefill_producer(p, H, stb, H, B, x, amax, s);
             }
             const spb_sparse_linear* qkv3[3] = {&L.q_proj, &L.k_proj, &L.v_proj};
             {
                 QkvRopeSink sink{};
-                sink.out = step.qkv;
-                sink.kc = kcache[l];
-                sink.vc = vcache[l];
-                sink.cur_rope = cur_rope;
-                sink.st = st;
+                sink.out = qkv;
+                sink.kc = kc;
+                sink.vc = vc;
+                sink.cur_rope = crope;
+                sink.st = stb;
                 sink.g0 = L.q_proj.gamma;
                 sink.g1 = L.k_proj.gamma;
                 sink.g2 = L.v_proj.gamma;
@@ -3840,53 +3881,81 @@ struct spb_batch_engine {
                 sink.max_seq = max_seq;
                 sink.rope_tab = nullptr;  // each sequence's own RoPE row (cur_rope)
                 sink.kv_stride = kv_seq;
-                if (gemm_sink(qkv3, 3, step.x, step.amax, sink, qrows + 2 * kvdim, step.y, B,
-                              s, &split) != hipSuccess)
+                if (gemm_sink(qkv3, 3, x, amax, sink, qkv_row, y, B, s, sp) != hipSuccess)
                     return hipErrorLaunchFailure;
             }
-            launch_attention_batch(hd, nh / nkv, S, splits, nkv, B, s, step.qkv, kcache[l],
-                                   vcache[l], step.pm, step.pl, step.pacc, st, max_seq, scale,
-                                   qrows + 2 * kvdim, kv_seq);
+            launch_attention_batch(hd, nh / nkv, S, splits, nkv, B, s, qkv, kc, vc, pm, pl, pacc,
+                                   stb, max_seq, scale, static_cast<int>(qkv_row), kv_seq);
             {
-                AttnCombine p{step.pm, step.pl, step.pacc, hd, S, qrows, hd == 64 ? 6 : 7};
-                launch_prefill_producer(p, 0, st, qrows, B, step.x, step.amax, s);
+                AttnCombine p{pm, pl, pacc, hd, S, qrows, hd == 64 ? 6 : 7};
+                launch_prefill_producer(p, 0, stb, qrows, B, x, amax, s);
             }
             {
                 const spb_sparse_linear* o1[1] = {&L.o_proj};
-                SegBf16Sink sink{step.o, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma, H, H,
+                SegBf16Sink sink{o, L.o_proj.gamma, L.o_proj.gamma, L.o_proj.gamma, H, H,
                                  0.f, 0.f, 0.f};
-                if (gemm_sink(o1, 1, step.x, step.amax, sink, H, step.y, B, s, &split) !=
-                    hipSuccess)
+                if (gemm_sink(o1, 1, x, amax, sink, H, y, B, s, sp) != hipSuccess)
                     return hipErrorLaunchFailure;
             }
             {
-                SubNormResidualNorm p{step.o, step.r, step.r2, L.attn_sub_norm,
-                                      L.post_attention_layernorm, eps, H};
-                launch_prefill_producer(p, H, st, H, B, step.x, step.amax, s);
+                SubNormResidualNorm p{o, r, r2, L.attn_sub_norm, L.post_attention_layernorm,
+                                      eps, H};
+                launch_prefill_producer(p, H, stb, H, B, x, amax, s);
             }
             {
                 const spb_sparse_linear* gu2[2] = {&L.gate_proj, &L.up_proj};
-                SegBf16Sink sink{step.gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
+                SegBf16Sink sink{gu, L.gate_proj.gamma, L.up_proj.gamma, L.up_proj.gamma,
                                  I, 2 * I, 0.f, 0.f, 0.f};
-                if (gemm_sink(gu2, 2, step.x, step.amax, sink, 2 * I, step.y, B, s, &split) !=
-                    hipSuccess)
+                if (gemm_sink(gu2, 2, x, amax, sink, 2 * I, y, B, s, sp) != hipSuccess)
                     return hipErrorLaunchFailure;
             }
             {
-                Relu2Norm p{step.gu, step.gu + I, L.ffn_sub_norm,
-                            L.ffn_sub_norm ? L.ffn_sub_norm
-                                           : reinterpret_cast<const float*>(step.gu),
+                Relu2Norm p{gu, gu + I, L.ffn_sub_norm,
+                            L.ffn_sub_norm ? L.ffn_sub_norm : reinterpret_cast<const float*>(gu),
                             eps, I};
-                launch_prefill_producer(p, 2 * I, st, I, B, step.x, step.amax, s);
+                launch_prefill_producer(p, 2 * I, stb, I, B, x, amax, s);
             }
             {
                 const spb_sparse_linear* d1[1] = {&L.down_proj};
-                ResidualSink sink{step.r, step.r2, L.down_proj.gamma, 0.f};
-                if (gemm_sink(d1, 1, step.x, step.amax, sink, H, step.y, B, s, &split) !=
-                    hipSuccess)
+                ResidualSink sink{r, r2, L.down_proj.gamma, 0.f};
+                if (gemm_sink(d1, 1, x, amax, sink, H, y, B, s, sp) != hipSuccess)
                     return hipErrorLaunchFailure;
             }
         }
+        return hipGetLastError();
+    }
+
+    // One decode step of every sequence: the layers (the sequence groups in
+    // parallel branches), then the final norm and the LM head (the
+    // matrix-core logits over every sequence, then the exact candidates and
+    // the argmax per sequence).
+    hipError_t enqueue_step(hipStream_t s, int splits) const {
+        if (groups == 1) {
+            const hipError_t err = enqueue_layers(s, 0, batch, splits, &gsplit[0]);
+            if (err != hipSuccess) return err;
+            return enqueue_head(s);
+        }
+        if (hipEventRecord(ev[0], s) != hipSuccess) return hipErrorLaunchFailure;
+        for (int g = 1; g < groups; ++g)
+            if (hipStreamWaitEvent(aux[g - 1], ev[0], 0) != hipSuccess)
+                return hipErrorLaunchFailure;
+        hipError_t err = hipSuccess;
+        for (int g = 0; g < groups && err == hipSuccess; ++g) {
+            const int b0 = g * batch / groups, b1 = (g + 1) * batch / groups;
+            err = enqueue_layers(g ? aux[g - 1] : s, b0, b1 - b0, splits, &gsplit[g]);
+        }
+        for (int g = 1; g < groups; ++g)  // rejoin every branch, also after an error
+            if (hipEventRecord(ev[g], aux[g - 1]) != hipSuccess ||
+                hipStreamWaitEvent(s, ev[g], 0) != hipSuccess)
+                err = hipErrorLaunchFailure;
+        if (err != hipSuccess) return err;
+        return enqueue_head(s);
+    }
+
+    hipError_t enqueue_head(hipStream_t s) const {
+        const int hd = cfg.head_dim, H = cfg.hidden_size;
+        const float eps = cfg.rms_norm_eps;
+        const int B = batch;
         const int V = cfg.vocab_size, xstride = lm_head_batch_xstride(H);
         const int nc64 = (H / 8 + kWave - 1) / kWave * kWave;
         hipLaunchKernelGGL(final_norm_batch_kernel<true>, dim3(B), dim3(kLmBlock), 0, s, step.r,
@@ -3976,6 +4045,11 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
         if (e->split.part_words > 0)
             ok = ok && (e->split.part = dev_alloc<int32_t>(e->split.part_words, own)) &&
                  (e->split.count = dev_alloc<unsigned>(kGemmSplitCounters, own));
+        e->groups = batch_groups(batch);
+        e->gsplit.assign(e->groups, e->split);
+        for (int g = 1; g < e->groups && e->split.part_words > 0; ++g)
+            ok = ok && (e->gsplit[g].part = dev_alloc<int32_t>(e->split.part_words, own)) &&
+                 (e->gsplit[g].count = dev_alloc<unsigned>(kGemmSplitCounters, own));
     }
     if (!ok) {
         delete e;
@@ -4002,9 +4076,21 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
     }
     if (err == hipSuccess) err = hipMemset(e->st, 0, B * sizeof(EngineState));
     if (err == hipSuccess) err = hipMemset(e->tokens, 0, B * (max_seq + 1) * sizeof(int));
-    if (err == hipSuccess && e->split.count)  // the split-K tile counters start (and end) at 0
-        err = hipMemset(e->split.count, 0, kGemmSplitCounters * sizeof(unsigned));
+    // the split-K tile counters start (and end) at 0
+    for (size_t g = 0; g < e->gsplit.size() && err == hipSuccess; ++g)
+        if (e->gsplit[g].count)
+            err = hipMemset(e->gsplit[g].count, 0, kGemmSplitCounters * sizeof(unsigned));
     if (err == hipSuccess) err = hipStreamCreateWithFlags(&e->cap_stream, hipStreamNonBlocking);
+    for (int g = 0; g < e->groups && err == hipSuccess; ++g) {
+        hipEvent_t v = nullptr;
+        err = hipEventCreateWithFlags(&v, hipEventDisableTiming);
+        if (err == hipSuccess) e->ev.push_back(v);
+        if (g > 0 && err == hipSuccess) {
+            hipStream_t a = nullptr;
+            err = hipStreamCreateWithFlags(&a, hipStreamNonBlocking);
+            if (err == hipSuccess) e->aux.push_back(a);
+        }
+    }
     if (err != hipSuccess) {
         delete e;
         return launch_status(fn);

@@ -41,12 +41,14 @@ def _oracle_tokens(host, max_seq, prompts, n_new, eos=-1):
         return list(pool.map(one, prompts))
 
 
-@pytest.mark.parametrize("batch", [8, 17, 32])
+@pytest.mark.parametrize("batch", [8, 17, 25, 32])
 def test_batch_decode_matches_oracle(gpu, batch):
     """Ragged prompts of 260-700 tokens (5-11 of the 64-position attention
     splits) in a 4096-position cache, 16 greedy steps per sequence.  17
     sequences: the GEMM's 32-token tile with 15 padding tokens (masked in
-    the sink epilogue) and LM-head groups of 8, 8 and 1."""
+    the sink epilogue) and LM-head groups of 8, 8 and 1.  25 and 32
+    sequences: the layers step in two groups of sequences (12 + 13, 16 + 16)
+    on parallel branches of the step graph, joined for the LM head."""
     from spbitnet_amd.model import BatchInferenceEngine, InferenceEngine, Model
     cfg = _cfg()
     model = Model.random(cfg, seed=101 + batch)
