@@ -53,8 +53,8 @@ constexpr int kPrefillChunk = 1024;      // prompt tokens per batched-prefill pa
 constexpr int kGemmSplitCounters = 1024;  // split-K tile counters of a batch engine (split launches have at most CUs / 2 tiles)
 // Sequence groups of a batched decode step: two parallel branches of the
 // step graph for 24-32 sequences (same-box bench at config 4: batch 32
-// 11,943-11,952 -> 12,358-12,380 tok/s with two groups, 9,196-11,277 with
-// four; batch 16 7,818-7,819 with one, 7,760-7,761 with two; batch 8
+// 11,943-11,952 -> 12,358-12,380 tok/s with two groups, 11,840-11,878 with
+// three, 9,196-11,277 with four; batch 16 7,818-7,819 with one, 7,760-7,761 with two; batch 8
 // 4,509-4,512 with one, 4,354-4,384 with two).  Larger batches keep one
 // branch, so the GEMMs' split over K (33-64 tokens) sees the whole batch.
 int batch_groups(int batch) { return batch >= 24 && batch <= 32 ? 2 : 1; }
