@@ -654,7 +654,8 @@ struct CombinedAttn {
     static constexpr int kAux = 0;
     const float* v;  // [nh * hd], bf16-rounded
     int n;
-    __device__ void at(int, long) {}
+    // batched decode: sequence t's vector at v + t * stride
+    __device__ void at(int t, long stride) { v += t * stride; }
     struct Regs {
         float4 a[kUnits], b[kUnits];
     };
@@ -1348,6 +1349,14 @@ __global__ __launch_bounds__(kWave) void attn_combine_kernel(const float* __rest
     constexpr int E = HD / kWave;  // adjacent elements per lane (one wave per head)
     extern __shared__ float wl[];  // [2][S]: w_s, l_s
     const int h = blockIdx.x, t = threadIdx.x;
+    {  // sequence blockIdx.y of a batch (its state, partials and output)
+        const long b = blockIdx.y, hs = static_cast<long>(gridDim.x) * S;
+        st += b;
+        pm += b * hs;
+        pl += b * hs;
+        pacc += b * hs * HD;
+        out += b * gridDim.x * HD;
+    }
     const int pos = state_pos(st);
     int ns = (pos >> 6) + 1;
     ns = ns < S ? ns : S;
@@ -2911,15 +2920,16 @@ void launch_prefill_sink(const Sink& sink, long stride, const float* amax, const
 // (at least 12), at most kCombineBatch.
 template <int HD, int NB>
 void launch_attn_combine_nb(int nh, hipStream_t s, const float* pm, const float* pl,
-                            const float* pacc, float* comb, const EngineState* st, int S) {
+                            const float* pacc, float* comb, const EngineState* st, int S,
+                            int B) {
     const size_t lds = 2 * static_cast<size_t>(S) * sizeof(float);
-    hipLaunchKernelGGL((attn_combine_kernel<HD, NB>), dim3(nh), dim3(kWave), lds, s, pm, pl,
+    hipLaunchKernelGGL((attn_combine_kernel<HD, NB>), dim3(nh, B), dim3(kWave), lds, s, pm, pl,
                        pacc, comb, st, S);
 }
 template <int HD>
 void launch_attn_combine_hd(int nh, int splits, hipStream_t s, const float* pm, const float* pl,
-                            const float* pacc, float* comb, const EngineState* st, int S) {
-#define SPB_COMBINE_NB(nb) launch_attn_combine_nb<HD, nb>(nh, s, pm, pl, pacc, comb, st, S); break
+                            const float* pacc, float* comb, const EngineState* st, int S, int B) {
+#define SPB_COMBINE_NB(nb) launch_attn_combine_nb<HD, nb>(nh, s, pm, pl, pacc, comb, st, S, B); break
     switch ((splits + 3) / 4) {
     case 0: case 1: case 2: case 3: SPB_COMBINE_NB(12);
     case 4: SPB_COMBINE_NB(16);
@@ -2938,13 +2948,15 @@ void launch_attn_combine_hd(int nh, int splits, hipStream_t s, const float* pm, 
     }
 #undef SPB_COMBINE_NB
 }
+// B sequences: grid (nh, B), sequence b's state st + b, partials after
+// those of b - 1, output comb + b * nh * hd.
 void launch_attn_combine(int hd, int nh, int splits, hipStream_t s, const float* pm,
                          const float* pl, const float* pacc, float* comb, const EngineState* st,
-                         int S) {
+                         int S, int B = 1) {
     if (hd == 64)
-        launch_attn_combine_hd<64>(nh, splits, s, pm, pl, pacc, comb, st, S);
+        launch_attn_combine_hd<64>(nh, splits, s, pm, pl, pacc, comb, st, S, B);
     else
-        launch_attn_combine_hd<128>(nh, splits, s, pm, pl, pacc, comb, st, S);
+        launch_attn_combine_hd<128>(nh, splits, s, pm, pl, pacc, comb, st, S, B);
 }
 
 // The first `splits` splits of S (the partials' stride stays S).
@@ -3776,6 +3788,7 @@ struct spb_batch_engine {
     PrefillBufs step;  // the decode step's per-token buffers (batch tokens)
     PrefillBufs pf;    // the prompt prefill's buffers
     float* logits = nullptr;              // [batch][vocab]
+    float* comb = nullptr;                // [batch][nh * hd]: combined attention outputs
     float* xn = nullptr;                  // [batch][padded hidden]: final-normed vectors
     float* part_lo = nullptr;             // [batch][lm_grid]: largest lower bound per row block
     float* part_hi = nullptr;             // [batch][lm_grid]: largest upper bound per row block
@@ -3887,8 +3900,10 @@ struct spb_batch_engine {
             launch_attention_batch(hd, nh / nkv, S, splits, nkv, B, s, qkv, kc, vc, pm, pl, pacc,
                                    stb, max_seq, scale, static_cast<int>(qkv_row), kv_seq);
             {
-                AttnCombine p{pm, pl, pacc, hd, S, qrows, hd == 64 ? 6 : 7};
-                launch_prefill_producer(p, 0, stb, qrows, B, x, amax, s);
+                float* const cb = comb + static_cast<long>(b0) * qrows;
+                launch_attn_combine(hd, nh, splits, s, pm, pl, pacc, cb, stb, S, B);
+                CombinedAttn p{cb, qrows};
+                launch_prefill_producer(p, qrows, stb, qrows, B, x, amax, s);
             }
             {
                 const spb_sparse_linear* o1[1] = {&L.o_proj};
@@ -4024,6 +4039,7 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
     ok = ok && alloc_prefill(e->step, *cfg, e->S, own, batch) &&
          alloc_prefill(e->pf, *cfg, e->S, own) &&
          (e->logits = dev_alloc<float>(B * V, own)) &&
+         (e->comb = dev_alloc<float>(static_cast<size_t>(B) * nh * hd, own)) &&
          (e->xn = dev_alloc<float>(B * lm_head_batch_xstride(H), own)) &&
          (e->part_lo = dev_alloc<float>(B * e->lm_grid, own)) &&
          (e->part_hi = dev_alloc<float>(B * e->lm_grid, own)) &&
