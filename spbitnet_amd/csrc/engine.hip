@@ -2780,6 +2780,7 @@ struct PrefillBufs {
     int32_t* y[3] = {nullptr, nullptr, nullptr};  // [chunk][max rows] GEMM outputs
     uint16_t *qkv = nullptr, *o = nullptr, *r = nullptr, *r2 = nullptr, *gu = nullptr;
     float *pm = nullptr, *pl = nullptr, *pacc = nullptr;
+    float* comb = nullptr;      // [chunk][nh * hd] combined attention outputs
     EngineState* st = nullptr;  // [chunk] one decode-state record per token
     int chunk = 0;  // tokens per prefill pass
     // per-token capacities of x, y[0] and y[1..2] (a group's rows of x and y
@@ -2819,6 +2820,7 @@ bool alloc_prefill(PrefillBufs& pf, const spb_model_config& cfg, int S, std::vec
            (pf.pm = dev_alloc<float>(C * nh * S, own)) &&
            (pf.pl = dev_alloc<float>(C * nh * S, own)) &&
            (pf.pacc = dev_alloc<float>(C * nh * S * hd, own)) &&
+           (pf.comb = dev_alloc<float>(C * nh * hd, own)) &&
            (pf.st = dev_alloc<EngineState>(C, own));
 }
 
@@ -3154,9 +3156,10 @@ auto vcache = [&](size_t l) { return (*t.vcache)[l] + t.kv_off; };
             launch_attention_prefill_hd<128>(nh / nkv, sp, nkv, c, s, pf.qkv, kcache(l),
                                              vcache(l), pf.pm, pf.pl, pf.pacc, max_seq, S,
                                              scale, pos0, qrows + 2 * kvdim);
-        {
-            AttnCombine p{pf.pm, pf.pl, pf.pacc, hd, S, qrows, hd == 64 ? 6 : 7};
-            launch_prefill_producer(p, 0, pf.st, qrows, c, pf.x, pf.amax, s);
+        {  // the split combine over (head, token), then the o input per token
+            launch_attn_combine(hd, nh, sp, s, pf.pm, pf.pl, pf.pacc, pf.comb, pf.st, S, c);
+            CombinedAttn p{pf.comb, qrows};
+            launch_prefill_producer(p, qrows, pf.st, qrows, c, pf.x, pf.amax, s);
         }
         {
             const spb_sparse_linear* o1[1] = {&L.o_proj};
@@ -3788,7 +3791,6 @@ struct spb_batch_engine {
     PrefillBufs step;  // the decode step's per-token buffers (batch tokens)
     PrefillBufs pf;    // the prompt prefill's buffers
     float* logits = nullptr;              // [batch][vocab]
-    float* comb = nullptr;                // [batch][nh * hd]: combined attention outputs
     float* xn = nullptr;                  // [batch][padded hidden]: final-normed vectors
     float* part_lo = nullptr;             // [batch][lm_grid]: largest lower bound per row block
     float* part_hi = nullptr;             // [batch][lm_grid]: largest upper bound per row block
@@ -3900,7 +3902,7 @@ struct spb_batch_engine {
             launch_attention_batch(hd, nh / nkv, S, splits, nkv, B, s, qkv, kc, vc, pm, pl, pacc,
                                    stb, max_seq, scale, static_cast<int>(qkv_row), kv_seq);
             {
-                float* const cb = comb + static_cast<long>(b0) * qrows;
+                float* const cb = step.comb + static_cast<long>(b0) * qrows;
                 launch_attn_combine(hd, nh, splits, s, pm, pl, pacc, cb, stb, S, B);
                 CombinedAttn p{cb, qrows};
                 launch_prefill_producer(p, qrows, stb, qrows, B, x, amax, s);
@@ -4039,7 +4041,6 @@ extern "C" int spb_batch_engine_create(const spb_model_config* cfg,
     ok = ok && alloc_prefill(e->step, *cfg, e->S, own, batch) &&
          alloc_prefill(e->pf, *cfg, e->S, own) &&
          (e->logits = dev_alloc<float>(B * V, own)) &&
-         (e->comb = dev_alloc<float>(static_cast<size_t>(B) * nh * hd, own)) &&
          (e->xn = dev_alloc<float>(B * lm_head_batch_xstride(H), own)) &&
          (e->part_lo = dev_alloc<float>(B * e->lm_grid, own)) &&
          (e->part_hi = dev_alloc<float>(B * e->lm_grid, own)) &&
