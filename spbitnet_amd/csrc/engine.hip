@@ -1652,10 +1652,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_prefill_kernel(
 // b = blockIdx.z), each sequence with its own decode state (st + b), query
 // (qkv + b * qkv_stride), KV cache (kc / vc + b * kv_stride) and partials
 // (after those of sequence b - 1).  Unlike the bs=1 kernel it reads the
-// sequence's position before loading K and V: with many sequences most
-// blocks lie past their sequence's position (splits up to max_seq), and
-// their loads would be wasted.  The per-split arithmetic is attention_split,
-// as in the bs=1 kernel.
+// sequence's position before loading K and V: the grid reaches the end of
+// the step graph's position bucket, which is set by the longest sequence,
+// so the blocks of shorter sequences past their own positions skip their
+// loads.  The per-split arithmetic is attention_split, as in the bs=1
+// kernel.
 template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attention_batch_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
