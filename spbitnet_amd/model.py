@@ -537,6 +537,19 @@ class BatchInferenceEngine:
         _lib.check(self._L.spb_batch_engine_decode_steps(self._h, int(steps)),
                    "spb_batch_engine_decode_steps")
 
+    def token_buffer(self) -> torch.Tensor:
+        """A copy of the device token buffer, int32 [batch][max_seq + 1]:
+        sequence b's prompt, then one token per decode step at its
+        positions (what decode_steps appends)."""
+        tp = ctypes.c_void_p()
+        _lib.check(self._L.spb_batch_engine_buffers(self._h, None, ctypes.byref(tp)),
+                   "spb_batch_engine_buffers")
+        out = torch.empty((self.batch, self.max_seq + 1), dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        _lib.memcpy_d2d(out.data_ptr(), tp.value, out.numel() * 4, None)
+        torch.cuda.synchronize()
+        return out
+
     def last_logits(self) -> torch.Tensor:
         """A copy of the last step's float32 logits, [batch][vocab].  Each
         sequence's argmax row holds the bs=1 engine's value bit for bit; the

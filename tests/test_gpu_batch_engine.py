@@ -127,6 +127,29 @@ def test_batch_decode_crosses_position_buckets(gpu):
     eng.close()
 
 
+def test_batch_decode_steps_cross_bucket(gpu):
+    """decode_steps() continues a generation without a host round trip,
+    choosing each step's graph from the position bound that generate()
+    left: a prefill-only generate (no new tokens) of prompts ending at
+    positions 246-249, then 14 decode steps that cross into the
+    256-position bucket; the tokens each sequence appends to its buffer
+    equal the oracle's generate."""
+    from spbitnet_amd.model import BatchInferenceEngine, Model
+    cfg = _cfg(max_position_embeddings=512)
+    model = Model.random(cfg, seed=419)
+    rng = np.random.default_rng(419)
+    lens = [250, 247, 249, 248, 250, 247]
+    prompts = [[int(t) for t in rng.integers(0, cfg.vocab_size, n)] for n in lens]
+    want = _oracle_tokens(model.to_host(), 512, prompts, 14)
+    eng = BatchInferenceEngine(model, max_seq=512, batch=6)
+    assert eng.generate(prompts, 0, stop_at_eos=False) == [[] for _ in lens]
+    eng.decode_steps(14)
+    tok = eng.token_buffer().cpu()
+    eng.close()
+    for b, n in enumerate(lens):
+        assert tok[b, n:n + 14].tolist() == want[b], f"sequence {b}"
+
+
 @pytest.mark.parametrize("heads,kv,batch", [(8, 2, 40), (8, 1, 36), (4, 2, 48)])
 def test_batch_decode_split_k_head_dim_128(gpu, heads, kv, batch):
     """At 33-64 sequences the GEMMs take the 64x32 tile (2-pair chunks), and
