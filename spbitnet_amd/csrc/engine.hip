@@ -1413,7 +1413,7 @@ __global__ __launch_bounds__(kWave) void attn_combine_kernel(const float* __rest
         out[h * HD + t] = bf16r(a[0] / l);
 }
 
-template <int HD, int G>
+template <int HD, int G, int HB = G>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, float* __restrict__ pm, float* __restrict__ pl,
@@ -1422,11 +1422,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     constexpr int kU = HD / 8;       // 16-byte units per row
     constexpr int kQU = kU / 4;      // units per quarter row
     constexpr int kVRow = HD / 2 + 1;  // 32-bit words per bf16 V row in LDS (+1: no bank conflicts)
-    __shared__ __align__(16) float qs[G][HD];
+    // HB of the group's G q heads per block, heads z * HB .. z * HB + HB - 1
+    // (z = blockIdx.z): the decode step's few blocks (one per split and kv
+    // head) split over G / HB blocks each, every block loading the split's
+    // K and V
+    static_assert(G % HB == 0, "HB divides G");
+    __shared__ __align__(16) float qs[HB][HD];
     __shared__ uint32_t vs[kAttnSplit][kVRow];
-    __shared__ __align__(16) float sc[G][kAttnSplit];
-    __shared__ float hmax[G], hsum[G];
-    const int s = blockIdx.x, kvh = blockIdx.y;
+    __shared__ __align__(16) float sc[HB][kAttnSplit];
+    __shared__ float hmax[HB], hsum[HB];
+    const int s = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z;
     const int j0 = s * kAttnSplit;
     const int tid = threadIdx.x;
     const long cache0 = static_cast<long>(kvh) * max_seq * HD;
@@ -1453,8 +1458,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
         vraw[t] = reinterpret_cast<const uint4*>(vc + cache0 + static_cast<long>(j) * HD)[c];
     }
     uint4 qraw = make_uint4(0, 0, 0, 0);
-    const bool has_q = tid < G * kU;
-    if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + (kvh * G) * HD)[tid];
+    const bool has_q = tid < HB * kU;
+    if (has_q) qraw = reinterpret_cast<const uint4*>(qkv + (kvh * G + z * HB) * HD)[tid];
     const int done = state_done(st), pos = state_pos(st);
 #pragma unroll
     for (int t = 0; t < kVPer; ++t) {
@@ -1475,7 +1480,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(
     const int jn = (pos + 1 - j0) < kAttnSplit ? (pos + 1 - j0) : kAttnSplit;
     __syncthreads();
 
-    attention_split<HD, G>(kq, qs, vs, sc, hmax, hsum, jn, scale, s, kvh, S, pm, pl, pacc);
+    // heads kvh * G + z * HB + g = (kvh * G / HB + z) * HB + g
+    attention_split<HD, HB>(kq, qs, vs, sc, hmax, hsum, jn, scale, s, kvh * (G / HB) + z, S, pm,
+                            pl, pacc);
 }
 
 // Prefill form: the queries of the tokens of a batch (token t at position
@@ -2864,11 +2871,23 @@ void launch_attention_hd(int G, dim3 grid, hipStream_t s, const uint16_t* qkv,
                          const uint16_t* kc, const uint16_t* vc, float* pm, float* pl,
                          float* pacc, const EngineState* st, int max_seq, int S, float scale) {
     const dim3 block(kAttnThreads);
+    // Short contexts (at most kFusedCombineSplits splits: a few blocks per kv
+    // head) split each group's q heads over two blocks, which both load the
+    // split's K and V: config 3 1,193.5-1,194.4 -> 1,202.2-1,202.5 tok/s;
+    // with every split count, config 4 at bs=1 (36 splits) lost 2 % (1,040.4-
+    // 1,040.7 against 1,062.4-1,063.2: the duplicated K and V loads).
+    const bool split_heads = grid.x <= kFusedCombineSplits;
     switch (G) {
     case 1: hipLaunchKernelGGL((attention_kernel<HD, 1>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
     case 2: hipLaunchKernelGGL((attention_kernel<HD, 2>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
-    case 4: hipLaunchKernelGGL((attention_kernel<HD, 4>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
-    default: hipLaunchKernelGGL((attention_kernel<HD, 8>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
+    case 4:
+        if (split_heads) hipLaunchKernelGGL((attention_kernel<HD, 4, 2>), dim3(grid.x, grid.y, 2), block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
+        else hipLaunchKernelGGL((attention_kernel<HD, 4>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
+        break;
+    default:
+        if (split_heads) hipLaunchKernelGGL((attention_kernel<HD, 8, 4>), dim3(grid.x, grid.y, 2), block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
+        else hipLaunchKernelGGL((attention_kernel<HD, 8>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
+        break;
     }
 }
 // The prefill form: c tokens at positions pos0 .. pos0 + c - 1 (grid.z).
