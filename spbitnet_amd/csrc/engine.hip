@@ -2872,16 +2872,18 @@ void launch_attention_hd(int G, dim3 grid, hipStream_t s, const uint16_t* qkv,
                          float* pacc, const EngineState* st, int max_seq, int S, float scale) {
     const dim3 block(kAttnThreads);
     // Short contexts (at most kFusedCombineSplits splits: a few blocks per kv
-    // head) split each group's q heads over two blocks, which both load the
-    // split's K and V: config 3 1,193.5-1,194.4 -> 1,202.2-1,202.5 tok/s;
-    // with every split count, config 4 at bs=1 (36 splits) lost 2 % (1,040.4-
-    // 1,040.7 against 1,062.4-1,063.2: the duplicated K and V loads).
+    // head) spread each group's q heads over several blocks, which all load
+    // the split's K and V: at config 3 (G = 4) one head per block
+    // 1,198.0-1,198.2 -> 1,209.1-1,209.3 tok/s, two per block 1,193.5-1,194.4
+    // -> 1,202.2-1,202.5; with every split count, config 4 at bs=1 (36
+    // splits) lost 2 % with two per block (1,040.4-1,040.7 against 1,062.4-
+    // 1,063.2: the duplicated K and V loads).  G = 8 takes four per block.
     const bool split_heads = grid.x <= kFusedCombineSplits;
     switch (G) {
     case 1: hipLaunchKernelGGL((attention_kernel<HD, 1>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
     case 2: hipLaunchKernelGGL((attention_kernel<HD, 2>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale); break;
     case 4:
-        if (split_heads) hipLaunchKernelGGL((attention_kernel<HD, 4, 2>), dim3(grid.x, grid.y, 2), block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
+        if (split_heads) hipLaunchKernelGGL((attention_kernel<HD, 4, 1>), dim3(grid.x, grid.y, 4), block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
         else hipLaunchKernelGGL((attention_kernel<HD, 4>), grid, block, 0, s, qkv, kc, vc, pm, pl, pacc, st, max_seq, S, scale);
         break;
     default:
