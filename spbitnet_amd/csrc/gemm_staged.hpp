@@ -448,9 +448,14 @@ bool staged_ok(const void* meta, const void* values, const void* X, int cols, in
 //            columns (a 2560-column row in one memory round trip; longer rows
 //            double-buffer 123 KB of LDS)
 //   n <= 64: 64 rows x 32 tokens, 8 waves (2 row groups x 4 K ways)
-//   n > 64 : 64 rows x 64 tokens, 8 waves (2 row groups x 4 K ways), 78 KB
+//   n > 64 : 64 rows x 64 tokens, 8 waves (2 row groups x 4 K ways), 78 KB;
+//            128 rows x 64 tokens (4 row groups x 2 K ways, one column pair
+//            per chunk, 64 KB) when that grid has at least 4/5 as many
+//            blocks as there are CUs
 // Kernels above 64 KB of LDS need their limit raised (gemm_prepare).
-enum StagedShape { kStagedN16, kStagedN16R16, kStagedN16Long, kStagedN16R64, kStagedN64, kStagedWide };
+enum StagedShape {
+    kStagedN16, kStagedN16R16, kStagedN16Long, kStagedN16R64, kStagedN64, kStagedWide, kStagedWide128
+};
 // Batches of up to 16 tokens take the 32x16 tile; so do batches of up to 32
 // whose 64x32 grid would fill at most half the CUs (the token tiles side by
 // side, one chunk per 2560-column row: more blocks, one memory round trip
@@ -478,13 +483,25 @@ StagedShape staged_shape(int n, int rows, int cols) {
     if (n <= kStagedN16Max &&
         2L * ((rows + 63) / 64) * ((n + 31) / 32) <= static_cast<long>(device_cu_count()))
         return kStagedN16;
-    return n <= 64 ? kStagedN64 : kStagedWide;
+    if (n <= 64) return kStagedN64;
+    // The 128x64 tile reads 5.4 operand bytes per product and chunk where the
+    // 64x64 tile reads 9.3, the launch's L2-to-CU traffic (82 MB at n = 256 on
+    // 6912 x 2560: the token block re-read by every row block) with it; it
+    // pays once its grid nearly fills the chip.  Sweep on MI355X, us per
+    // launch, 64x64 -> 128x64: 6912 x 2560 n = 256 / 512 / 1024 11.37 ->
+    // 11.18, 19.57 -> 17.13, 33.29 -> 30.34; 13824 x 2560 n = 128 / 256 /
+    // 1024 11.74 -> 11.20, 19.71 -> 16.79, 65.93 -> 54.95; 3840 x 2560
+    // n = 1024 20.36 -> 17.47; 2560 x 6912 n = 1024 35.48 -> 33.48, while at
+    // 160 blocks (2560 x 6912, n = 512) it lost (21.68 -> 26.08).
+    const long wide128 = static_cast<long>((rows + 127) / 128) * ((n + 63) / 64);
+    return 5 * wide128 >= 4 * device_cu_count() ? kStagedWide128 : kStagedWide;
 }
 int staged_row_block(int n, int rows, int cols) {
     switch (staged_shape(n, rows, cols)) {
         case kStagedN16R16:
         case kStagedN16Long: return 16;
         case kStagedN16: return 32;
+        case kStagedWide128: return 128;
         default: return 64;
     }
 }
@@ -566,6 +583,9 @@ int launch_staged_for(const uint32_t* meta, const uint32_t* values, const int8_t
         case kStagedN64:
             return launch_staged<2, 2, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
                                                 split);
+        case kStagedWide128:
+            return launch_staged<2, 4, 4, 2, 1>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
+                                                split);
         default:
             return launch_staged<2, 4, 2, 4, 2>(meta, values, X, epi, rows, cols, n, ms, vs, st, g,
                                                 split);
@@ -581,7 +601,7 @@ long staged_split_words(const int* rows, int nrows, int cols, int n) {
         const bool t16 = n <= 16 || sh == kStagedN16;  // 16-token tiles
         const int rb = staged_row_block(n, rows[i], cols);
         const int tb = t16 ? 16 : (n <= 64 ? 32 : 64);
-        const int kcp = sh == kStagedN16Long ? 14 : (t16 ? 10 : 2);
+        const int kcp = sh == kStagedN16Long ? 14 : (t16 ? 10 : (sh == kStagedWide128 ? 1 : 2));
         const int nch = (cols / 256 + kcp - 1) / kcp;
         const long tiles = static_cast<long>((rows[i] + rb - 1) / rb) * ((n + tb - 1) / tb);
         const long w = tiles * staged_split_parts(tiles, nch) * rb * tb;
@@ -590,7 +610,7 @@ long staged_split_words(const int* rows, int nrows, int cols, int n) {
     return words;
 }
 
-// Raises the LDS limit of the three staged tiles with epilogue Epi, unsplit
+// Raises the LDS limit of the staged tiles with epilogue Epi, unsplit
 // and split (0 = done).
 template <class Epi>
 int staged_prepare() {
@@ -605,7 +625,9 @@ int staged_prepare() {
                    gemm_allow_lds(staged_fn<2, 4, 2, 4, 2, Epi>()) &&
                    gemm_allow_lds(staged_fn<1, 1, 2, 4, 10, Epi, true>()) &&
                    gemm_allow_lds(staged_fn<2, 2, 2, 4, 2, Epi, true>()) &&
-                   gemm_allow_lds(staged_fn<2, 4, 2, 4, 2, Epi, true>())
+                   gemm_allow_lds(staged_fn<2, 4, 2, 4, 2, Epi, true>()) &&
+                   gemm_allow_lds(staged_fn<2, 4, 4, 2, 1, Epi>()) &&
+                   gemm_allow_lds(staged_fn<2, 4, 4, 2, 1, Epi, true>())
                ? 0
                : 1;
 }

@@ -139,6 +139,29 @@ def test_gemm_staged_rows_not_multiple_of_4(gpu, rows, cols, n):
     assert (out[n * rows:] == -7).all()
 
 
+@pytest.mark.parametrize("rows,cols,n", [(6900, 2560, 250), (3333, 768, 500), (13824, 512, 129),
+                                         (2560, 6912, 700), (6912, 2560, 256)])
+def test_gemm_wide_128_row_tile(gpu, rows, cols, n):
+    """Batches above 64 tokens whose 128-row x 64-token grid nearly fills the
+    chip take the 128-row staged tile (one column pair per chunk): rows that
+    end inside a row block or are not a multiple of 4, batches that end inside
+    a token tile, 27-pair rows; exact, and nothing written past Y (guard
+    words)."""
+    L = W.random_layer(rows, cols, W.seed_for("gemm-wide128", rows, cols, n))
+    X = np.random.default_rng(rows + 11 * cols + n).integers(-128, 128, (n, cols)).astype(np.int8)
+    m_dev, v_dev, X_dev = dev_u32(L.meta, gpu), dev_u32(L.values, gpu), dev(X, gpu)
+    assert K.gemm_kernel_id(m_dev, v_dev, X_dev, rows, cols, n, L.meta_stride,
+                            L.values_stride) == 2
+    guard = 64
+    buf = torch.full((n * rows + guard,), -7, dtype=torch.int32, device=gpu)
+    K.sparse_ternary_gemm_gpu(m_dev, v_dev, X_dev, buf, rows, cols, n, L.meta_stride,
+                              L.values_stride)
+    torch.cuda.synchronize()
+    out = buf.cpu().numpy()
+    assert (out[:n * rows].reshape(n, rows) == expected(L, X)).all()
+    assert (out[n * rows:] == -7).all()
+
+
 def test_gemm_staged_unaligned_output(gpu):
     """Y that starts 4 bytes past a 16-byte boundary (rows a multiple of 4):
     the staged kernel stores rows one by one instead of 16-byte quads."""
