@@ -278,8 +278,10 @@ __global__ __launch_bounds__(WS * KW * kWave) void gemm_smfmac_kernel(
     // The epilogue's own loads (Epi::preload: the sink's per-token inputs),
     // issued ahead of the first chunk in the small tiles (the batched decode's
     // few-chunk launches, whose end would otherwise wait a memory round trip
-    // for them), at the end in the 64x64 tile (their registers would cost
-    // its second block per CU); rows and tokens past the matrix load row 0 /
+    // for them), at the end in the tiles of more than four 16x16 products
+    // per wave (the 64x64 and 128x64 tiles: held through the loop, their
+    // registers cost the 64x64 tile its second block per CU); rows and
+    // tokens past the matrix load row 0 /
     // the last token (nothing is stored for them).
     constexpr bool kEarly = S * T <= 4;
     typename Epi::Pre pre[S][T];
