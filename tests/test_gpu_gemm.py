@@ -162,11 +162,12 @@ def test_gemm_wide_128_row_tile(gpu, rows, cols, n):
     assert (out[n * rows:] == -7).all()
 
 
-def test_gemm_staged_unaligned_output(gpu):
+@pytest.mark.parametrize("rows,cols,n", [(256, 512, 20), (6912, 2560, 256)])
+def test_gemm_staged_unaligned_output(gpu, rows, cols, n):
     """Y that starts 4 bytes past a 16-byte boundary (rows a multiple of 4):
-    the staged kernel stores rows one by one instead of 16-byte quads."""
-    rows, cols, n = 256, 512, 20
-    L = W.random_layer(rows, cols, W.seed_for("gemm-unaligned-y"))
+    the staged kernel stores rows one by one instead of 16-byte quads (the
+    32x16 tile, and the 128-row tile at 256 tokens)."""
+    L = W.random_layer(rows, cols, W.seed_for("gemm-unaligned-y", rows, cols, n))
     X = np.random.default_rng(91).integers(-128, 128, (n, cols)).astype(np.int8)
     buf = torch.full((n * rows + 8,), -7, dtype=torch.int32, device=gpu)
     Y = buf[1:1 + n * rows]
